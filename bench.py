@@ -1,0 +1,208 @@
+"""Benchmark: Q38 MoE-layer forward (one Qwen3_8MoeSparseMoeBlock) on one MI355X.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--no-cpu-baseline]
+
+A step is one fused block forward (router, permutation, grouped gate/up + SwiGLU, grouped down x
+routing weight, shared expert, gated combine) over the workload's packed tokens, inputs resident in
+HBM. Prints ONE JSON line: whole-job tokens/s, the roofline of the dominant kernel (per-kernel
+durations measured here with HIP events on the launch stream), and the reference's CPU block
+forward timed on this host on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "qwen35-moe-sparse_amd"))
+sys.path.insert(0, str(REPO))
+
+METRIC = "MoE-layer tokens/sec at 16K tokens bf16 (1 GPU) + % MFMA peak"
+PEAK_BF16 = 2.5e15   # dense bf16 MFMA, MI355X datasheet
+PEAK_HBM = 8.0e12    # HBM3E bytes/s
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_stream(fn, iters, stream):
+    import torch
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / iters * 1e-3  # seconds per launch
+
+
+def kernel_breakdown(wl, x, d, bias, iters, stream):
+    """Average duration of each stage kernel, launched alone back to back on `stream`."""
+    import torch
+    from q38.hip import ops
+    T, h, E, k, I, Is = wl.tokens, wl.hidden, wl.experts, wl.topk, wl.inter, wl.shared_inter
+    P = T * k
+    logits, idx, w, gate, hist = ops.route(x, d["gate.weight"], k, w_shared_gate=d["shared_expert_gate.weight"],
+                                           logit_bias=bias, want_hist=True)
+    counts, starts, perm, tiles = ops.permute(idx, hist, E)
+    H = ops.gate_up(x, d["experts.gate_up_proj"], perm, tiles, k)
+    y = ops.down(H, d["experts.down_proj"], perm, tiles, w)
+    sh = ops.shared_expert(x, d["shared_expert.gate_proj.weight"], d["shared_expert.up_proj.weight"],
+                           d["shared_expert.down_proj.weight"])
+    torch.cuda.synchronize()
+    fl = wl.flops()
+    stages = {
+        "route": (lambda: ops.route(x, d["gate.weight"], k, w_shared_gate=d["shared_expert_gate.weight"],
+                                    logit_bias=bias, want_hist=True), "hbm",
+                  # x read + router weights + idx/w/gate/hist written
+                  T * h * 2 + (E + 1) * h * 2 + P * 6 + T * 2),
+        "permute": (lambda: ops.permute(idx, hist, E), "hbm", P * 4 * 2),
+        "gate_up": (lambda: ops.gate_up(x, d["experts.gate_up_proj"], perm, tiles, k), "mfma", fl["gate_up"]),
+        "down": (lambda: ops.down(H, d["experts.down_proj"], perm, tiles, w), "mfma", fl["down"]),
+        "shared_expert": (lambda: ops.shared_expert(x, d["shared_expert.gate_proj.weight"],
+                                                    d["shared_expert.up_proj.weight"],
+                                                    d["shared_expert.down_proj.weight"]), "mfma", fl["shared"]),
+        # combine reads k bf16 rows + the shared row, writes one row per token
+        "combine": (lambda: ops.combine(y, k, E, shared_out=sh, shared_gate_logit=gate), "hbm",
+                    T * h * 2 * (k + 2)),
+    }
+    out = {}
+    for name, (fn, bound, work) in stages.items():
+        fn()
+        dt = time_stream(fn, iters, stream)
+        if bound == "mfma":
+            achieved, peak, unit = work / dt / 1e12, PEAK_BF16 / 1e12, "TFLOP/s"
+        else:
+            achieved, peak, unit = work / dt / 1e9, PEAK_HBM / 1e9, "GB/s"
+        out[name] = dict(us=round(dt * 1e6, 2), bound=bound, work=work, achieved=round(achieved, 2),
+                         peak=peak, unit=unit, frac=round(achieved / peak, 4))
+    return out
+
+
+def cpu_baseline(wl, budget_s=20.0):
+    """The reference block's own op sequence (eager experts loop) in bf16 on this host's CPU."""
+    import torch
+    from oracle import moe_oracle
+    from q38 import workloads
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    x_all, params, _ = workloads.make(wl, tokens=2048)
+    tokens = 256
+    with torch.inference_mode():
+        t0 = time.perf_counter()
+        moe_oracle.reference_block_forward(x_all[:tokens], params, wl.topk)  # warmup
+        first = time.perf_counter() - t0
+        # Size the sample so the 3 timed runs take about budget_s.
+        per_tok = first / tokens
+        tokens = int(max(256, min(2048, budget_s / 3 / max(per_tok, 1e-9))))
+        x = x_all[:tokens]
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            moe_oracle.reference_block_forward(x, params, wl.topk)
+            times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[1]
+    return dict(value=round(tokens / med, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"{tokens} tokens of {wl.name} (h={wl.hidden}, E={wl.experts}, k={wl.topk}, I={wl.inter}), "
+                       f"bf16 torch CPU, reference op sequence with the eager experts loop "
+                       f"(modeling_qwen3_8_moe.py:769-793,805-813,824-835), median of 3 after 1 warmup",
+                seconds=[round(t, 3) for t in times])
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="c2")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-iters", type=int, default=20)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this benchmark measures one GPU only; the MoE block is data-parallel "
+                                   "across GPUs with no exchange, run one process per GPU", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+    from q38 import workloads
+    from q38.hip import ops
+
+    wl = workloads.get(args.workload)
+    dev = torch.device("cuda:0")
+    log(f"[bench] workload {wl.name}: T={wl.tokens} h={wl.hidden} E={wl.experts} k={wl.topk} I={wl.inter} "
+        f"Is={wl.shared_inter}")
+    x, params, bias = workloads.make(wl, device="cpu")
+    x = x.to(dev)
+    d = {n: p.to(dev).contiguous() for n, p in params.items()}
+    if bias is not None:
+        bias = bias.to(dev)
+    T, h = x.shape
+    k = wl.topk
+    ws = torch.empty(ops.block_workspace_bytes(T, h, wl.experts, k, wl.inter, wl.shared_inter), dtype=torch.uint8,
+                     device=dev)
+    out = torch.empty(T, h, dtype=torch.bfloat16, device=dev)
+    weights = [d[n] for n in workloads.PARAM_ORDER]
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        ops.block_forward(x, *weights, k, logit_bias=bias, workspace=ws, out=out)
+
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        log(f"[bench] warmup {args.warmup} done")
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(args.steps):
+            step()
+        end.record(stream)
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / args.steps
+        log(f"[bench] timed {args.steps} steps: {ms:.4f} ms/step")
+        kernels = kernel_breakdown(wl, x, d, bias, args.kernel_iters, stream)
+        log(f"[bench] kernels: " + ", ".join(f"{n} {v['us']}us" for n, v in kernels.items()))
+
+    fl = wl.flops()
+    dom = max(kernels, key=lambda n: kernels[n]["us"])
+    dk = kernels[dom]
+    expert_us = kernels["gate_up"]["us"] + kernels["down"]["us"]
+    res = {
+        "metric": METRIC,
+        "value": round(T / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights; no checkpoint)",
+        "config": {"workload": f"{wl.name}: one Q38 MoE block forward, {wl.batch}x{wl.seq} packed tokens",
+                   "tokens": T, "hidden": h, "experts": wl.experts, "top_k": k, "expert_inter": wl.inter,
+                   "shared_inter": wl.shared_inter, "routing_skew": wl.zipf_s, "parallelism": "single GPU"},
+        "roofline": {"kernel": dom, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
+                     "unit": dk["unit"], "frac": dk["frac"], "traffic": None,
+                     "work_per_launch": dk["work"]},
+        "mfma_frac_expert_gemms": round(fl["experts"] / (expert_us * 1e-6) / PEAK_BF16, 4),
+        "mfma_frac_block": round(fl["block"] / (ms * 1e-3) / PEAK_BF16, 4),
+        "kernels": kernels,
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] timing the CPU baseline")
+        res["cpu_baseline"] = cpu_baseline(wl)
+        log(f"[bench] cpu baseline: {res['cpu_baseline']['value']} tokens/s")
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

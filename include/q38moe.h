@@ -1,0 +1,189 @@
+/*
+ * q38moe.h — C ABI of the MI355X (gfx950) Q38 MoE feed-forward prefill library (libq38moe.so).
+ *
+ * The reference implements this path in Python/Triton; there is no C interface to mirror, so each
+ * entry point below names the reference function whose semantics it replaces (paths relative to
+ * the reference repository root; "modeling" = q38/models/qwen3_8_moe/modeling_qwen3_8_moe.py).
+ *
+ * Conventions shared by every entry point
+ *  - All tensor arguments are device pointers to caller-allocated, contiguous, row-major memory.
+ *    The library never allocates or frees device memory; scratch space is a caller-provided
+ *    workspace whose size comes from the matching *_workspace_bytes query.
+ *  - bf16 tensors are passed as raw 16-bit storage (torch.bfloat16 bit patterns).
+ *  - Expert/token indices produced by the library are int32. q38moe_experts_forward also accepts
+ *    the int64 indices torch.topk returns (idx_is_int64 = 1).
+ *  - `stream` is a hipStream_t (NULL = the legacy default stream). All work is enqueued
+ *    asynchronously on it; no entry point synchronises the host or the device.
+ *  - Return value: 0 on success, negative on error (Q38MOE_E*); q38moe_last_error() then returns a
+ *    thread-local, human-readable message. A launch failure reports the HIP error string.
+ *  - Shapes: T tokens (T*k < 2^31), hidden h, E experts, top-k k, routed intermediate I, shared
+ *    intermediate Is. Supported: 1 <= E <= 64, 1 <= k <= min(8, E), h % 64 == 0,
+ *    I % 64 == 0, Is % 64 == 0; every pointer 16-byte aligned. dtype must be Q38MOE_BF16.
+ *  - The library keeps no mutable global state, so calls on different streams may overlap as long
+ *    as they use different workspaces and outputs.
+ */
+#ifndef Q38MOE_H
+#define Q38MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q38MOE_ABI_VERSION 1
+
+#define Q38MOE_OK 0
+#define Q38MOE_EINVAL (-1)   /* bad shape, null pointer, misalignment, unsupported dtype */
+#define Q38MOE_EWORKSPACE (-2) /* workspace missing or too small */
+#define Q38MOE_EHIP (-3)     /* a HIP runtime call or kernel launch failed */
+
+#define Q38MOE_BF16 1
+
+/* Library ABI version (Q38MOE_ABI_VERSION). */
+int q38moe_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* q38moe_last_error(void);
+
+/*
+ * Router, R1-R2: replaces Qwen3_8MoeTopKRouter.forward (modeling:805-813).
+ *   logits[t,e] = bf16(sum_c x[t,c] * w_router[e,c])                         (F.linear, :807)
+ *   probs = softmax(float(logits) (+ logit_bias), fp32)                       (:808)
+ *   (v, topk_idx) = torch CPU topk(probs, k, largest, sorted)                 (:809)
+ *     -- tie order reproduces ATen/native/TopKImpl.h (std::nth_element + std::sort with a
+ *        value-only comparator, NaN first; std::partial_sort when k*64 <= E).
+ *   topk_w = bf16(v / sum(v))                                                 (:810-811)
+ * Optional extras:
+ *   w_shared_gate [h] (NULL to skip): shared_gate_logit[t] = bf16(x[t] . w_shared_gate), the
+ *     shared_expert_gate projection of modeling:831, computed from the same pass over x.
+ *   logit_bias [E] fp32 (NULL = reference behaviour): added to the logits before the softmax
+ *     (the routing-skew workload; no reference counterpart).
+ *   logits [T,E] bf16 (NULL to skip): the router_logits element of the returned tuple.
+ *   hist [ceil(T/64), E] int32 (NULL to skip): per-64-token-block expert counts, the input of
+ *     q38moe_permute.
+ * Outputs: topk_idx [T,k] int32, topk_w [T,k] bf16.
+ */
+int q38moe_route(const void* x, const void* w_router, const void* w_shared_gate,
+                 const float* logit_bias, void* logits, int32_t* topk_idx, void* topk_w,
+                 void* shared_gate_logit, int32_t* hist, int64_t T, int32_t h, int32_t E,
+                 int32_t k, int32_t dtype, void* stream);
+
+/*
+ * Router selection only (R2) from given bf16 logits [T,E]: modeling:808-812 with the logits of
+ * :807 supplied by the caller. Same outputs and tie semantics as q38moe_route.
+ */
+int q38moe_route_from_logits(const void* logits, const float* logit_bias, int32_t* topk_idx,
+                             void* topk_w, int32_t* hist, int64_t T, int32_t E, int32_t k,
+                             int32_t dtype, void* stream);
+
+/*
+ * Per-64-token-block expert histogram of given routing indices (int32, or int64 when
+ * idx_is_int64): hist [ceil(T/64), E]. Indices outside [0,E) are not counted (the sentinel rows
+ * transformers' grouped_mm drops, integrations/moe.py:405-420).
+ */
+int q38moe_histogram(const void* topk_idx, int32_t idx_is_int64, int32_t* hist, int64_t T,
+                     int32_t E, int32_t k, void* stream);
+
+/*
+ * Permutation, R3-R4: replaces the stable sort + searchsorted of inference.py:163-171 and the
+ * block mapping of inference.py:39-50 / 174-183.
+ *   counts[e] = #{p : ids[p] == e}; starts = exclusive prefix sum of counts;
+ *   perm[starts[e] + r] = the r-th pair p (ascending p = t*k + j) routed to expert e
+ *   (identical to torch.sort(ids, stable=True).indices).
+ *   tiles[i] = {expert, first sorted row, valid rows, 0} for the i-th block_m-row tile of the
+ *   grouped GEMMs (experts ascending; each expert padded to a multiple of block_m, never to a
+ *   global capacity); entries past the last tile hold {-1, 0, 0, 0}. tiles must hold
+ *   q38moe_max_tiles(T, E, k, block_m) entries of int32[4].
+ * hist comes from q38moe_route or q38moe_histogram.
+ */
+int q38moe_permute(const void* topk_idx, int32_t idx_is_int64, const int32_t* hist,
+                   int32_t* counts, int32_t* starts, int32_t* perm, int32_t* tiles,
+                   int32_t block_m, int64_t T, int32_t E, int32_t k, void* stream);
+
+/* Upper bound on grouped-GEMM tiles: ceil(T*k / block_m) + E (inference.py:179). */
+int64_t q38moe_max_tiles(int64_t T, int32_t E, int32_t k, int32_t block_m);
+
+/* Tile height (rows) the grouped GEMM kernels of this build expect in `tiles`. */
+int32_t q38moe_gemm_block_m(void);
+
+/*
+ * Grouped gate/up GEMM with fused SwiGLU, R5-R6: replaces _gate_up_kernel (inference.py:60-96).
+ * For sorted row r of expert e (token = perm[r] / k):
+ *   g = bf16(x[token] . w_gate_up[e, n, :]), u = bf16(x[token] . w_gate_up[e, I+n, :]),
+ *   H[r, n] = bf16(bf16(silu(g)) * u).
+ * w_gate_up [E, 2I, h] bf16 (the experts.gate_up_proj parameter). H [T*k, I] bf16, sorted order.
+ */
+int q38moe_gate_up(const void* x, const void* w_gate_up, const int32_t* perm,
+                   const int32_t* tiles, void* H, int64_t T, int32_t h, int32_t E, int32_t k,
+                   int32_t I, int32_t dtype, void* stream);
+
+/*
+ * Grouped down GEMM with the routing-weight epilogue, R7: replaces _down_kernel
+ * (inference.py:99-130). For sorted row r of expert e, pair p = perm[r]:
+ *   y[p, c] = bf16(bf16(H[r] . w_down[e, c, :]) * topk_w[p]).
+ * w_down [E, h, I] bf16 (experts.down_proj). y [T*k, h] bf16 in pair order.
+ */
+int q38moe_down(const void* H, const void* w_down, const int32_t* perm, const int32_t* tiles,
+                const void* topk_w, void* y, int64_t T, int32_t h, int32_t E, int32_t k,
+                int32_t I, int32_t dtype, void* stream);
+
+/*
+ * Shared expert, R9 (Qwen3_8MoeMLP.forward, modeling:751-753):
+ *   out[t] = bf16(bf16(bf16(silu(bf16(x.Wg^T))) * bf16(x.Wu^T)) . Wd^T).
+ * w_gate [Is,h], w_up [Is,h], w_down [h,Is] bf16; Hs workspace [T,Is] bf16; out [T,h] bf16.
+ */
+int q38moe_shared_expert(const void* x, const void* w_gate, const void* w_up,
+                         const void* w_down, void* Hs, void* out, int64_t T, int32_t h,
+                         int32_t Is, int32_t dtype, void* stream);
+
+/*
+ * Combine, R8 (+ the block tail of modeling:831-833):
+ *   routed[t] = bf16(sum_j fp32(y[t*k+j]))                                    (inference.py:199)
+ *   shared_out == NULL: out = routed.
+ *   otherwise:          out = bf16(routed + bf16(bf16(sigmoid(gate_logit[t])) * shared_out[t])).
+ * topk_idx (NULL = all pairs valid; int32 or int64 per idx_is_int64): pairs whose index lies
+ * outside [0,E) contribute nothing.
+ */
+int q38moe_combine(const void* y, const void* topk_idx, int32_t idx_is_int64,
+                   const void* shared_out, const void* shared_gate_logit, void* out, int64_t T,
+                   int32_t h, int32_t E, int32_t k, int32_t dtype, void* stream);
+
+/*
+ * Routed experts, R3-R8: the ExpertsInterface contract
+ *   fn(self, hidden_states[T,h], top_k_index[T,k], top_k_weights[T,k]) -> [T,h]
+ * (transformers integrations/moe.py:567-570; implementations inference.py:158-199 and
+ * modeling:769-793). Runs histogram, permute, gate/up, down and combine.
+ */
+int q38moe_experts_workspace_bytes(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
+                                   size_t* bytes);
+int q38moe_experts_forward(const void* x, const void* topk_idx, int32_t idx_is_int64,
+                           const void* topk_w, const void* w_gate_up, const void* w_down,
+                           void* out, int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
+                           void* workspace, size_t workspace_bytes, int32_t dtype, void* stream);
+
+/*
+ * Whole MoE block, R0: Qwen3_8MoeSparseMoeBlock.forward (modeling:824-835) on hidden_states
+ * viewed as [T,h]: shared expert, router, routed experts, sigmoid shared gate, sum.
+ *   w_router [E,h]; w_gate_up [E,2I,h]; w_down [E,h,I]; w_sh_gate/w_sh_up [Is,h];
+ *   w_sh_down [h,Is]; w_sh_gate_proj [1,h] (shared_expert_gate.weight); all bf16.
+ *   logit_bias [E] fp32 or NULL. out [T,h] bf16.
+ *   Optional router outputs (NULL to skip): logits [T,E] bf16, topk_idx [T,k] int32,
+ *   topk_w [T,k] bf16.
+ */
+int q38moe_block_workspace_bytes(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
+                                 int32_t Is, size_t* bytes);
+int q38moe_block_forward(const void* x, const void* w_router, const void* w_gate_up,
+                         const void* w_down, const void* w_sh_gate, const void* w_sh_up,
+                         const void* w_sh_down, const void* w_sh_gate_proj,
+                         const float* logit_bias, void* out, void* logits, int32_t* topk_idx,
+                         void* topk_w, int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
+                         int32_t Is, void* workspace, size_t workspace_bytes, int32_t dtype,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q38MOE_H */

@@ -1,0 +1,203 @@
+"""CPU oracle of the Q38 MoE feed-forward prefill. TEST INFRASTRUCTURE ONLY.
+
+Imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the checker and
+as the timed CPU baseline; the product path (qwen35-moe-sparse_amd/q38) never imports it.
+
+What each function restates (reference paths; "modeling" = q38/models/qwen3_8_moe/
+modeling_qwen3_8_moe.py, "inference" = q38/inference.py):
+
+  topk_cpu        torch CPU top-k tie order, ATen/native/TopKImpl.h:45-76, via the C restatement
+                  in q38_oracle.cpp (liboracle.so) that calls libstdc++'s nth_element/sort.
+  permute_cpu     stable counting sort = torch.sort(ids, stable=True) + searchsorted,
+                  inference:163-171 (C, q38_oracle.cpp).
+  router          Qwen3_8MoeTopKRouter.forward, modeling:805-813 (fp32 matmul rounded once to
+                  bf16 stands for the bf16 F.linear; softmax fp32; torch CPU topk; renorm).
+  experts_grouped routed experts with the rounding sequence of inference:60-130,199 (also that
+                  of transformers' grouped_mm path): per-expert fp32 matmuls on gathered rows,
+                  bf16 rounding of gate/up, silu, product, down, weight; fp32 k-sum.
+  experts_eager   Qwen3_8MoeExperts.forward, modeling:769-793, op for op (index_add_ in D).
+  shared_expert   Qwen3_8MoeMLP.forward, modeling:751-753.
+  block           Qwen3_8MoeSparseMoeBlock.forward, modeling:824-835.
+  reference_block_forward  the whole block computed with the reference's own torch op sequence in
+                  the module dtype (eager experts): the timed CPU baseline.
+
+Parity pins (tests/test_oracle.py): topk_cpu vs torch.topk on tie-heavy rows and hand-worked
+cases; permute_cpu vs torch.sort(stable=True)/bincount and its invariants; the FP functions vs
+float64 brute force on tiny shapes, vs each other (grouped vs eager), and on special cases with
+closed forms (zero router weight, k = E, zero shared-gate weight).
+"""
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+ORACLE_DIR = Path(__file__).resolve().parent
+LIB_PATH = ORACLE_DIR / "_build" / "liboracle.so"
+
+
+def build():
+    """Compile q38_oracle.cpp with g++ into oracle/_build/liboracle.so."""
+    (ORACLE_DIR / "_build").mkdir(exist_ok=True)
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    subprocess.run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC", str(ORACLE_DIR / "q38_oracle.cpp"), "-o",
+                    str(tmp)], check=True)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+_lib = None
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        lib = ctypes.CDLL(str(LIB_PATH))
+        lib.oracle_topk.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                    ctypes.c_void_p, ctypes.c_void_p]
+        lib.oracle_topk.restype = None
+        lib.oracle_permute.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p,
+                                       ctypes.c_void_p, ctypes.c_void_p]
+        lib.oracle_permute.restype = None
+        _lib = lib
+    return _lib
+
+
+def topk_cpu(values, k):
+    """(values fp32 [R,k], indices int64 [R,k]) of torch CPU topk(values, k, largest, sorted)."""
+    v = np.ascontiguousarray(np.asarray(values, dtype=np.float32))
+    R, n = v.shape
+    ov = np.empty((R, k), np.float32)
+    oi = np.empty((R, k), np.int64)
+    _load().oracle_topk(v.ctypes.data, R, n, k, ov.ctypes.data, oi.ctypes.data)
+    return ov, oi
+
+
+def permute_cpu(ids, E):
+    """(counts int32 [E], starts int32 [E], perm int32 [sum counts]) of a stable sort by expert."""
+    a = np.ascontiguousarray(np.asarray(ids, dtype=np.int64).reshape(-1))
+    counts = np.empty(E, np.int32)
+    starts = np.empty(E, np.int32)
+    valid = int(((a >= 0) & (a < E)).sum())
+    perm = np.empty(valid, np.int32)
+    _load().oracle_permute(a.ctypes.data, a.size, E, counts.ctypes.data, starts.ctypes.data, perm.ctypes.data)
+    return counts, starts, perm
+
+
+def bf16(t):
+    return t.to(torch.bfloat16)
+
+
+def _f(t):
+    return t.to(torch.float32)
+
+
+def router(x, w_router, k, logit_bias=None, logits=None):
+    """modeling:805-813. Returns (logits bf16 [T,E], probs fp32 [T,E], idx int64 [T,k], w bf16 [T,k]).
+
+    ``logits`` may be supplied (bf16) to run only the selection, as q38moe_route_from_logits does.
+    The optional fp32 ``logit_bias`` [E] is added before the softmax (routing-skew workload).
+    """
+    if logits is None:
+        logits = bf16(_f(x) @ _f(w_router).T)
+    z = _f(logits)
+    if logit_bias is not None:
+        z = z + _f(logit_bias)
+    probs = torch.softmax(z, dim=-1)
+    vals, idx = topk_cpu(probs.numpy(), k)
+    vals = torch.from_numpy(vals)
+    vals = vals / vals.sum(dim=-1, keepdim=True)
+    return logits, probs, torch.from_numpy(idx), bf16(vals)
+
+
+def experts_grouped(x, idx, w, w_gate_up, w_down):
+    """Routed experts, rounding of inference:60-130 and the k-sum of inference:199. Also returns
+    the per-pair rows y [T*k,h] bf16 and H [T*k,I] bf16 in sorted order."""
+    T, h = x.shape
+    k = idx.shape[1]
+    E, twoI, _ = w_gate_up.shape
+    I = twoI // 2
+    counts, starts, perm = permute_cpu(idx.numpy(), E)
+    perm_t = torch.from_numpy(perm.astype(np.int64))
+    wflat = _f(w.reshape(-1))
+    y = torch.zeros(T * k, h, dtype=torch.bfloat16)
+    H = torch.zeros(perm.size, I, dtype=torch.bfloat16)
+    xf = _f(x)
+    for e in range(E):
+        c, s = int(counts[e]), int(starts[e])
+        if c == 0:
+            continue
+        rows = perm_t[s:s + c]
+        A = xf[rows // k]
+        gu = A @ _f(w_gate_up[e]).T
+        g = _f(bf16(gu[:, :I]))
+        u = _f(bf16(gu[:, I:]))
+        act = _f(bf16(F.silu(g)))
+        He = bf16(act * u)
+        H[s:s + c] = He
+        d = _f(bf16(_f(He) @ _f(w_down[e]).T))
+        y[rows] = bf16(d * wflat[rows][:, None])
+    out = bf16(_f(y).view(T, k, h).sum(dim=1))
+    return out, y, H
+
+
+def experts_eager(x, idx, w, w_gate_up, w_down):
+    """Qwen3_8MoeExperts.forward (modeling:769-793) op for op, in the dtype of x."""
+    final = torch.zeros_like(x)
+    E = w_gate_up.shape[0]
+    mask = F.one_hot(idx, num_classes=E + 1).permute(2, 1, 0)
+    hit = torch.greater(mask.sum(dim=(-1, -2)), 0).nonzero()
+    for e in hit:
+        e = int(e[0])
+        if e == E:
+            continue
+        pos, tok = torch.where(mask[e])
+        cur = x[tok]
+        gate, up = F.linear(cur, w_gate_up[e]).chunk(2, dim=-1)
+        hcur = F.silu(gate) * up
+        hcur = F.linear(hcur, w_down[e])
+        hcur = hcur * w[tok, pos, None]
+        final.index_add_(0, tok, hcur.to(final.dtype))
+    return final
+
+
+def shared_expert(x, w_gate, w_up, w_down):
+    """modeling:751-753 with fp32 matmuls rounded once to bf16 at each linear."""
+    g = _f(bf16(_f(x) @ _f(w_gate).T))
+    u = _f(bf16(_f(x) @ _f(w_up).T))
+    hs = bf16(_f(bf16(F.silu(g))) * u)
+    return bf16(_f(hs) @ _f(w_down).T)
+
+
+def block(x, params, k, logit_bias=None):
+    """modeling:824-835 (grouped expert rounding). Returns out bf16 [T,h] and the intermediates."""
+    logits, probs, idx, w = router(x, params["gate.weight"], k, logit_bias)
+    routed, y, H = experts_grouped(x, idx, w, params["experts.gate_up_proj"], params["experts.down_proj"])
+    sh = shared_expert(x, params["shared_expert.gate_proj.weight"], params["shared_expert.up_proj.weight"],
+                       params["shared_expert.down_proj.weight"])
+    gate_logit = bf16(_f(x) @ _f(params["shared_expert_gate.weight"]).reshape(-1))
+    gated = bf16(_f(bf16(torch.sigmoid(_f(gate_logit))))[:, None] * _f(sh))
+    out = bf16(_f(routed) + _f(gated))
+    return out, dict(logits=logits, probs=probs, idx=idx, w=w, routed=routed, y=y, H=H, shared=sh,
+                     gate_logit=gate_logit)
+
+
+def reference_block_forward(x, params, k):
+    """The reference block's own op sequence (modeling:805-813, 769-793, 751-753, 824-835) in the
+    dtype of the inputs, eager experts loop. This is the CPU baseline that bench.py times."""
+    logits = F.linear(x, params["gate.weight"])
+    probs = torch.softmax(logits, dtype=torch.float, dim=-1)
+    top, idx = torch.topk(probs, k, dim=-1)
+    top /= top.sum(dim=-1, keepdim=True)
+    w = top.to(logits.dtype)
+    g = F.linear(x, params["shared_expert.gate_proj.weight"])
+    u = F.linear(x, params["shared_expert.up_proj.weight"])
+    sh = F.linear(F.silu(g) * u, params["shared_expert.down_proj.weight"])
+    routed = experts_eager(x, idx, w, params["experts.gate_up_proj"], params["experts.down_proj"])
+    sh = torch.sigmoid(F.linear(x, params["shared_expert_gate.weight"])) * sh
+    return routed + sh

@@ -1,0 +1,173 @@
+// Token->expert permutation (R3-R4): per-block histogram, expert prefix sums and a stable
+// counting-sort scatter, plus the padded tile table of the grouped GEMMs.
+//
+// Reference semantics (q38/inference.py:163-171, 39-50, 174-183): perm is
+// torch.sort(ids, stable=True).indices over the flattened pair ids (pair p = t*k + j),
+// starts/counts are the expert boundaries in sorted order. Here the sort is a counting sort:
+// perm[starts[e] + r] = the r-th pair (ascending p) routed to e. Every block of 64 tokens derives
+// its base offsets from the per-block histograms, so the scatter needs no atomics and the order is
+// deterministic.
+#include "q38moe_common.h"
+#include "q38moe_kernels.h"
+
+namespace q38 {
+
+constexpr int PERM_TOKENS = 64;  // tokens per histogram block (matches the router's blocks)
+constexpr int PERM_KMAX = 8;
+
+template <typename IdxT>
+__global__ __launch_bounds__(256) void hist_kernel(const IdxT* __restrict__ idx, int64_t T, int E,
+                                                   int k, int32_t* __restrict__ hist) {
+  __shared__ int s_h[64];
+  const int tid = threadIdx.x;
+  if (tid < 64) s_h[tid] = 0;
+  __syncthreads();
+  const int64_t t0 = (int64_t)blockIdx.x * PERM_TOKENS;
+  const int64_t t1 = min(t0 + PERM_TOKENS, T);
+  const int np = (int)((t1 - t0) * k);
+  for (int i = tid; i < np; i += 256) {
+    const int64_t e = (int64_t)idx[t0 * k + i];
+    if (e >= 0 && e < E) atomicAdd(&s_h[(int)e], 1);
+  }
+  __syncthreads();
+  if (tid < E) hist[(int64_t)blockIdx.x * E + tid] = s_h[tid];
+}
+
+template <typename IdxT>
+__global__ __launch_bounds__(256) void permute_kernel(
+    const IdxT* __restrict__ idx, const int32_t* __restrict__ hist, int64_t T, int E, int k,
+    int nblk, int32_t* __restrict__ counts, int32_t* __restrict__ starts,
+    int32_t* __restrict__ perm, int4* __restrict__ tiles, int block_m, int max_tiles) {
+  __shared__ int s_tot[4][64];
+  __shared__ int s_bef[4][64];
+  __shared__ int s_base[64];
+  __shared__ int s_start[64];
+  __shared__ int s_total[64];
+  __shared__ int s_tile0[64];
+  __shared__ int s_ntile[64];
+  __shared__ int s_wcnt[4][64];
+  __shared__ int s_ids[PERM_TOKENS * PERM_KMAX];
+  const int tid = threadIdx.x, e = tid & 63, part = tid >> 6;
+  const int b = blockIdx.x;
+
+  // Expert totals over all blocks and the counts of the blocks before this one.
+  int tot = 0, bef = 0;
+  if (e < E) {
+    for (int bb = part; bb < nblk; bb += 4) {
+      const int c = hist[(int64_t)bb * E + e];
+      tot += c;
+      if (bb < b) bef += c;
+    }
+  }
+  s_tot[part][e] = tot;
+  s_bef[part][e] = bef;
+  const int64_t t0 = (int64_t)b * PERM_TOKENS;
+  const int64_t t1 = min(t0 + PERM_TOKENS, T);
+  const int np = (int)((t1 - t0) * k);
+  const int64_t p0 = t0 * k;
+  for (int i = tid; i < np; i += 256) {
+    const int64_t v = (int64_t)idx[p0 + i];
+    s_ids[i] = (v >= 0 && v < E) ? (int)v : -1;
+  }
+  __syncthreads();
+
+  if (tid < 64) {
+    const int t = s_tot[0][tid] + s_tot[1][tid] + s_tot[2][tid] + s_tot[3][tid];
+    const int bf = s_bef[0][tid] + s_bef[1][tid] + s_bef[2][tid] + s_bef[3][tid];
+    int incl = t;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int nb = __shfl_up(incl, o);
+      if (tid >= o) incl += nb;
+    }
+    const int st = incl - t;
+    s_start[tid] = st;
+    s_total[tid] = t;
+    s_base[tid] = st + bf;
+    // Padded tiles per expert and their prefix (the blk_cum of inference.py:176).
+    const int nt = (tid < E) ? (t + block_m - 1) / block_m : 0;
+    int tincl = nt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int nb = __shfl_up(tincl, o);
+      if (tid >= o) tincl += nb;
+    }
+    s_ntile[tid] = nt;
+    s_tile0[tid] = tincl - nt;
+    if (b == 0 && tid < E) {
+      counts[tid] = t;
+      starts[tid] = st;
+    }
+  }
+  // Stable scatter: wave `part` owns a contiguous segment of this block's pairs.
+  const int seg = (np + 3) / 4;
+  const int s0 = min(part * seg, np), s1 = min(s0 + seg, np);
+  int cnt = 0;
+  if (e < E) {
+    for (int i = s0; i < s1; ++i) cnt += (s_ids[i] == e);
+  }
+  s_wcnt[part][e] = cnt;
+  __syncthreads();
+  if (e < E) {
+    int off = s_base[e];
+    for (int w = 0; w < part; ++w) off += s_wcnt[w][e];
+    // perm holds T*k entries; the bound only matters for a hist inconsistent with idx.
+    const int64_t cap = T * k;
+    for (int i = s0; i < s1; ++i) {
+      if (s_ids[i] == e) {
+        if (off < cap) perm[off] = (int32_t)(p0 + i);
+        ++off;
+      }
+    }
+  }
+
+  if (b == 0 && tiles != nullptr) {
+    const int total_tiles = s_tile0[63] + s_ntile[63];
+    for (int i = tid; i < max_tiles; i += 256) {
+      int4 ti = make_int4(-1, 0, 0, 0);
+      if (i < total_tiles) {
+        int lo = 0;
+        // Largest expert whose first tile is <= i and that owns at least one tile.
+        for (int ee = 0; ee < E; ++ee) {
+          if (s_ntile[ee] > 0 && s_tile0[ee] <= i) lo = ee;
+        }
+        const int local = i - s_tile0[lo];
+        const int row0 = s_start[lo] + local * block_m;
+        ti = make_int4(lo, row0, min(block_m, s_total[lo] - local * block_m), 0);
+      }
+      tiles[i] = ti;
+    }
+  }
+}
+
+hipError_t launch_histogram(const void* idx, bool idx64, int32_t* hist, int64_t T, int E, int k,
+                            hipStream_t stream) {
+  const int64_t nblk = (T + PERM_TOKENS - 1) / PERM_TOKENS;
+  if (nblk == 0) return hipSuccess;
+  if (idx64)
+    hipLaunchKernelGGL(hist_kernel<int64_t>, dim3((unsigned)nblk), dim3(256), 0, stream,
+                       (const int64_t*)idx, T, E, k, hist);
+  else
+    hipLaunchKernelGGL(hist_kernel<int32_t>, dim3((unsigned)nblk), dim3(256), 0, stream,
+                       (const int32_t*)idx, T, E, k, hist);
+  return hipGetLastError();
+}
+
+hipError_t launch_permute(const void* idx, bool idx64, const int32_t* hist, int32_t* counts,
+                          int32_t* starts, int32_t* perm, int4* tiles, int block_m,
+                          int max_tiles, int64_t T, int E, int k, hipStream_t stream) {
+  // At least one block, so T == 0 still writes zero counts and an empty tile table.
+  const int64_t nblk = (T + PERM_TOKENS - 1) / PERM_TOKENS;
+  const unsigned grid = (unsigned)(nblk > 0 ? nblk : 1);
+  if (idx64)
+    hipLaunchKernelGGL(permute_kernel<int64_t>, dim3(grid), dim3(256), 0, stream,
+                       (const int64_t*)idx, hist, T, E, k, (int)nblk, counts, starts, perm, tiles,
+                       block_m, max_tiles);
+  else
+    hipLaunchKernelGGL(permute_kernel<int32_t>, dim3(grid), dim3(256), 0, stream,
+                       (const int32_t*)idx, hist, T, E, k, (int)nblk, counts, starts, perm, tiles,
+                       block_m, max_tiles);
+  return hipGetLastError();
+}
+
+}  // namespace q38

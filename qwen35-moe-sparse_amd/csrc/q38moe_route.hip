@@ -1,0 +1,444 @@
+// Router (R1-R2): bf16 logits on MFMA, fp32 softmax, top-k with torch-CPU tie semantics,
+// renormalisation, shared-expert gate logit and the per-block expert histogram, in one pass.
+//
+// Reference semantics: Qwen3_8MoeTopKRouter.forward (modeling_qwen3_8_moe.py:805-813) with the
+// tie order of torch's CPU topk (ATen/native/TopKImpl.h:45-76):
+//   queue[j] = (value_j, j); std::nth_element(q, q+k-1, q+n, cmp); std::sort(q, q+k-1, cmp)
+//   cmp(x, y) = (isnan(x) && !isnan(y)) || x > y
+// (std::partial_sort when k*64 <= n). The selection here replays libstdc++'s introselect step by
+// step, with each Hoare partition evaluated wave-parallel (one lane per queue slot), so indices
+// match the CPU library bit for bit. Rows whose k+1 largest values are all distinct have a unique
+// answer and take a fast path (k+1 wave arg-max rounds).
+//
+// Selection compares the bf16 logits (plus the optional fp32 bias) rather than the fp32
+// probabilities: softmax is monotone, so the order is the same whenever the CPU softmax keeps
+// distinct logits distinct; this keeps indices independent of the exp() implementation.
+#include "q38moe_common.h"
+#include "q38moe_kernels.h"
+
+namespace q38 {
+
+constexpr int KMAX = 8;
+
+__device__ __forceinline__ bool cmp_gt(float a, float b) {
+  return (__builtin_isnan(a) && !__builtin_isnan(b)) || (a > b);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+#pragma unroll
+  for (int o = 32; o; o >>= 1) {
+    uint32_t lo = __shfl_xor((unsigned)(uint32_t)k, o);
+    uint32_t hi = __shfl_xor((unsigned)(uint32_t)(k >> 32), o);
+    uint64_t other = ((uint64_t)hi << 32) | lo;
+    k = other > k ? other : k;
+  }
+  return k;
+}
+
+// Position of the i-th (0-based) set bit of m, or 64 when m has no such bit.
+__device__ __forceinline__ int select_bit(uint64_t m, int i) {
+  if (i < 0 || i >= __popcll(m)) return 64;
+  int pos = 0;
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1) {
+    const uint64_t low = m & ((1ull << w) - 1ull);
+    const int c = __popcll(low);
+    if (i >= c) {
+      i -= c;
+      m >>= w;
+      pos += w;
+    } else {
+      m = low;
+    }
+  }
+  return pos;
+}
+
+// Swap queue slots a and b (lanes).
+__device__ __forceinline__ void swap_slots(float& qv, int& qi, int lane, int a, int b) {
+  const int src = lane == a ? b : (lane == b ? a : lane);
+  qv = __shfl(qv, src);
+  qi = __shfl(qi, src);
+}
+
+// libstdc++ __insertion_sort (a stable insertion sort) of slots [lo, hi), hi - lo <= KMAX.
+__device__ void insertion_sort_slots(float& qv, int& qi, int lane, int lo, int hi) {
+  const int n = hi - lo;
+  if (n <= 1) return;
+  float v[KMAX];
+  int id[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    const int src = min(lo + j, 63);
+    v[j] = __shfl(qv, src);
+    id[j] = __shfl(qi, src);
+  }
+#pragma unroll
+  for (int i = 1; i < KMAX; ++i) {
+    if (i < n) {
+      const float cv = v[i];
+      const int ci = id[i];
+      int j = i;
+#pragma unroll
+      for (int jj = i; jj > 0; --jj) {
+        if (j == jj && cmp_gt(cv, v[jj - 1])) {
+          v[jj] = v[jj - 1];
+          id[jj] = id[jj - 1];
+          j = jj - 1;
+        }
+      }
+#pragma unroll
+      for (int jj = 0; jj <= i; ++jj) {
+        if (jj == j) {
+          v[jj] = cv;
+          id[jj] = ci;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    if (j < n && lane == lo + j) {
+      qv = v[j];
+      qi = id[j];
+    }
+  }
+}
+
+// libstdc++ __adjust_heap + __push_heap on LDS arrays based at `first` (single lane).
+__device__ void heap_adjust(float* v, int* id, int first, int hole, int len, float val, int vid) {
+  const int top = hole;
+  int second = hole;
+  while (second < (len - 1) / 2) {
+    second = 2 * (second + 1);
+    if (cmp_gt(v[first + second], v[first + second - 1])) second--;
+    v[first + hole] = v[first + second];
+    id[first + hole] = id[first + second];
+    hole = second;
+  }
+  if ((len & 1) == 0 && second == (len - 2) / 2) {
+    second = 2 * (second + 1);
+    v[first + hole] = v[first + second - 1];
+    id[first + hole] = id[first + second - 1];
+    hole = second - 1;
+  }
+  int parent = (hole - 1) / 2;
+  while (hole > top && cmp_gt(v[first + parent], val)) {
+    v[first + hole] = v[first + parent];
+    id[first + hole] = id[first + parent];
+    hole = parent;
+    parent = (hole - 1) / 2;
+  }
+  v[first + hole] = val;
+  id[first + hole] = vid;
+}
+
+// libstdc++ __heap_select(first, middle, last) followed by iter_swap(first, nth): the
+// depth-limit exit of __introselect. Runs on one lane over an LDS copy of the queue.
+__device__ void heap_select_slots(float& qv, int& qi, int lane, int first, int middle, int last,
+                                  int nth, float* sv, int* si) {
+  sv[lane] = qv;
+  si[lane] = qi;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (lane == 0) {
+    const int len = middle - first;
+    if (len >= 2) {
+      int parent = (len - 2) / 2;
+      while (true) {
+        heap_adjust(sv, si, first, parent, len, sv[first + parent], si[first + parent]);
+        if (parent == 0) break;
+        parent--;
+      }
+    }
+    for (int i = middle; i < last; ++i) {
+      if (cmp_gt(sv[i], sv[first])) {
+        const float val = sv[i];
+        const int vid = si[i];
+        sv[i] = sv[first];
+        si[i] = si[first];
+        heap_adjust(sv, si, first, 0, len, val, vid);
+      }
+    }
+    const float tv = sv[first];
+    const int ti = si[first];
+    sv[first] = sv[nth];
+    si[first] = si[nth];
+    sv[nth] = tv;
+    si[nth] = ti;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  qv = sv[lane];
+  qi = si[lane];
+}
+
+// std::nth_element(q, q+k-1, q+n, cmp) then std::sort(q, q+k-1, cmp), with queue slot = lane.
+__device__ void nth_element_then_sort(float& qv, int& qi, int lane, int n, int k, float* sv,
+                                      int* si) {
+  const int nth = k - 1;
+  int first = 0, last = n;
+  int depth = 2 * (31 - __clz(n));
+  bool sorted_tail = true;
+  while (last - first > 3) {
+    if (depth == 0) {
+      heap_select_slots(qv, qi, lane, first, nth + 1, last, nth, sv, si);
+      sorted_tail = false;
+      break;
+    }
+    --depth;
+    // __unguarded_partition_pivot: median of (first+1, mid, last-1) moved to first.
+    const int mid = first + (last - first) / 2;
+    const float a = __shfl(qv, first + 1), b = __shfl(qv, mid), c = __shfl(qv, last - 1);
+    int s;
+    if (cmp_gt(a, b)) {
+      if (cmp_gt(b, c)) s = mid;
+      else if (cmp_gt(a, c)) s = last - 1;
+      else s = first + 1;
+    } else if (cmp_gt(a, c)) {
+      s = first + 1;
+    } else if (cmp_gt(b, c)) {
+      s = last - 1;
+    } else {
+      s = mid;
+    }
+    swap_slots(qv, qi, lane, first, s);
+    const float pv = __shfl(qv, first);
+    // __unguarded_partition(first+1, last, pivot=first): the i-th left stop (slot holding a value
+    // not cmp-greater than the pivot) swaps with the i-th right stop (value the pivot is not
+    // cmp-greater than; the pivot slot itself guards the scan) while left < right.
+    const uint64_t le = ballot64(lane > first && lane < last && !cmp_gt(qv, pv));
+    const uint64_t ge = ballot64(lane >= first && lane < last && !cmp_gt(pv, qv));
+    const int nl = __popcll(le), nr = __popcll(ge);
+    const int li = lane < nl ? select_bit(le, lane) : 64;
+    const int ri = lane < nr ? select_bit(ge, nr - 1 - lane) : -1;
+    const int sw = __popcll(ballot64(lane < nl && lane < nr && li < ri));
+    int cut;
+    if (sw == 0) {
+      cut = select_bit(le, 0);
+    } else {
+      const int l_next = sw < nl ? select_bit(le, sw) : (1 << 20);
+      const int r_last = select_bit(ge, nr - sw);
+      cut = min(l_next, r_last);
+    }
+    int src = lane;
+    if ((le >> lane) & 1ull) {
+      const int lr = __popcll(le & ((1ull << lane) - 1ull));
+      if (lr < sw) src = select_bit(ge, nr - 1 - lr);
+    }
+    if (src == lane && ((ge >> lane) & 1ull)) {
+      const int rr = __popcll(ge >> lane) - 1;
+      if (rr < sw) src = select_bit(le, rr);
+    }
+    qv = __shfl(qv, src & 63);
+    qi = __shfl(qi, src & 63);
+    if (cut <= nth) first = cut;
+    else last = cut;
+  }
+  if (sorted_tail) insertion_sort_slots(qv, qi, lane, first, last);
+  // std::sort on k-1 <= 16 elements is __insertion_sort.
+  insertion_sort_slots(qv, qi, lane, 0, k - 1);
+}
+
+// Route one token held by the calling wave. z: selection value of expert `lane` (lanes >= E
+// ignored). Lane r < k receives the r-th selected expert and its renormalised weight.
+__device__ void route_token(float z, int lane, int E, int k, int& out_idx, float& out_w,
+                            float* sv, int* si) {
+  const bool valid = lane < E;
+  z = z + 0.0f;  // -0 -> +0: the comparator treats them as equal
+  const bool has_nan = ballot64(valid && __builtin_isnan(z)) != 0ull;
+  const float m = wave_max(valid ? z : -INFINITY);
+  const bool all_nan = has_nan || !__builtin_isfinite(m);  // softmax is NaN everywhere then
+  float p;
+  if (all_nan) {
+    p = __builtin_nanf("");
+  } else {
+    const float ex = valid ? expf(z - m) : 0.0f;
+    const float s = wave_sum(ex);
+    p = ex * (1.0f / s);
+  }
+  const float sel = all_nan ? __builtin_nanf("") : z;
+  float qv = sel;
+  int qi = lane;
+
+  if (k * 64 <= E) {
+    // std::partial_sort path (k == 1, E == 64): first slot whose value is cmp-greater than all
+    // before it = lowest-index maximum (slot 0 when every value is NaN).
+    int best = 0;
+    if (!all_nan) {
+      const uint64_t key = valid ? ((uint64_t)order_key(sel) << 32) | (uint32_t)(63 - lane) : 0ull;
+      best = 63 - (int)(uint32_t)wave_max_u64(key);
+    }
+    qi = best;
+  } else {
+    bool tie = all_nan;
+    if (!all_nan) {
+      const int rounds = min(k + 1, E);
+      uint64_t key = valid ? ((uint64_t)order_key(sel) << 32) | (uint32_t)(63 - lane) : 0ull;
+      uint32_t prev_key = 0;
+      int top_lane[KMAX];
+#pragma unroll
+      for (int r = 0; r < KMAX + 1; ++r) {
+        if (r < rounds) {
+          const uint64_t best = wave_max_u64(key);
+          const int bl = 63 - (int)(uint32_t)best;
+          const uint32_t bk = (uint32_t)(best >> 32);
+          if (r > 0 && bk == prev_key) tie = true;
+          prev_key = bk;
+          if (r < KMAX) top_lane[r] = bl;
+          if (lane == bl) key = 0ull;
+        }
+      }
+      if (!tie) {
+#pragma unroll
+        for (int r = 0; r < KMAX; ++r) {
+          if (lane == r) qi = top_lane[r];
+        }
+      }
+    }
+    if (tie) nth_element_then_sort(qv, qi, lane, E, k, sv, si);
+  }
+  // Renormalise over the selected probabilities, summed in selection order.
+  const float pr = __shfl(p, qi & 63);
+  float s = 0.0f;
+  for (int r = 0; r < k; ++r) s += __shfl(pr, r);
+  out_idx = qi;
+  out_w = pr / s;
+}
+
+constexpr int ROUTE_TOKENS = 64;  // per block: 4 waves x 16 tokens
+
+// Logits tile per block on 16x16x32 MFMA: columns 0..E-1 are experts, column 64 is the
+// shared-expert gate projection (when given).
+__global__ __launch_bounds__(256) void route_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
+    const uint16_t* __restrict__ wsg, const uint16_t* __restrict__ logits_in,
+    const float* __restrict__ bias, uint16_t* __restrict__ logits_out,
+    int32_t* __restrict__ idx_out, uint16_t* __restrict__ w_out,
+    uint16_t* __restrict__ gate_out, int32_t* __restrict__ hist, int64_t T, int h, int E, int k) {
+  __shared__ float s_logit[ROUTE_TOKENS][65];
+  __shared__ int s_hist[64];
+  __shared__ float s_sv[4][64];
+  __shared__ int s_si[4][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t tb = (int64_t)blockIdx.x * ROUTE_TOKENS;
+  if (tid < 64) s_hist[tid] = 0;
+
+  if (logits_in == nullptr) {
+    const int ntile = (E + 15) >> 4;
+    f32x4_t acc[5];
+#pragma unroll
+    for (int j = 0; j < 5; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int64_t trow = tb + wave * 16 + (lane & 15);
+    const bool tvalid = trow < T;
+    const int kc = 8 * (lane >> 4);
+    const uint16_t* xa = x + (tvalid ? trow : 0) * (int64_t)h + kc;
+    const uint16_t* wb[5];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = 16 * j + (lane & 15);
+      wb[j] = col < E ? wr + (int64_t)col * h + kc : nullptr;
+    }
+    wb[4] = ((lane & 15) == 0 && wsg != nullptr) ? wsg + kc : nullptr;
+    const bool gate_tile = wsg != nullptr;
+    const u32x4_t zero = {0u, 0u, 0u, 0u};
+#pragma unroll 2
+    for (int k0 = 0; k0 < h; k0 += 32) {
+      const u32x4_t av = tvalid ? ld16(xa + k0) : zero;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (j < ntile) {
+          const u32x4_t bv = wb[j] ? ld16(wb[j] + k0) : zero;
+          acc[j] = mfma16x16x32(av, bv, acc[j]);
+        }
+      }
+      if (gate_tile) {
+        const u32x4_t bv = wb[4] ? ld16(wb[4] + k0) : zero;
+        acc[4] = mfma16x16x32(av, bv, acc[4]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j < ntile) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int col = 16 * j + (lane & 15);
+          if (col < E) s_logit[wave * 16 + 4 * (lane >> 4) + i][col] = round_bf16(acc[j][i]);
+        }
+      }
+    }
+    if (gate_tile && (lane & 15) == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_logit[wave * 16 + 4 * (lane >> 4) + i][64] = round_bf16(acc[4][i]);
+    }
+  } else {
+    for (int i = tid; i < ROUTE_TOKENS * E; i += 256) {
+      const int tl = i / E, e = i - tl * E;
+      const int64_t t = tb + tl;
+      s_logit[tl][e] = t < T ? bf16_to_f32(logits_in[t * E + e]) : 0.0f;
+    }
+  }
+  __syncthreads();
+
+  if (logits_out != nullptr && logits_in == nullptr) {
+    for (int i = tid; i < ROUTE_TOKENS * E; i += 256) {
+      const int tl = i / E, e = i - tl * E;
+      const int64_t t = tb + tl;
+      if (t < T) logits_out[t * E + e] = (uint16_t)f32_to_bf16_rne(s_logit[tl][e]);
+    }
+  }
+  if (gate_out != nullptr && wsg != nullptr && logits_in == nullptr && tid < ROUTE_TOKENS) {
+    const int64_t t = tb + tid;
+    if (t < T) gate_out[t] = (uint16_t)f32_to_bf16_rne(s_logit[tid][64]);
+  }
+
+  const float b = (bias != nullptr && lane < E) ? bias[lane] : 0.0f;
+  for (int tt = 0; tt < 16; ++tt) {
+    const int tl = wave * 16 + tt;
+    const int64_t t = tb + tl;
+    if (t >= T) break;
+    const float z = lane < E ? s_logit[tl][lane] + b : -INFINITY;
+    int oi;
+    float ow;
+    route_token(z, lane, E, k, oi, ow, s_sv[wave], s_si[wave]);
+    if (lane < k) {
+      idx_out[t * k + lane] = oi;
+      w_out[t * k + lane] = (uint16_t)f32_to_bf16_rne(ow);
+      atomicAdd(&s_hist[oi], 1);
+    }
+  }
+  __syncthreads();
+  if (hist != nullptr && tid < E) hist[(int64_t)blockIdx.x * E + tid] = s_hist[tid];
+}
+
+hipError_t launch_route(const uint16_t* x, const uint16_t* wr, const uint16_t* wsg,
+                        const uint16_t* logits_in, const float* bias, uint16_t* logits_out,
+                        int32_t* idx_out, uint16_t* w_out, uint16_t* gate_out, int32_t* hist,
+                        int64_t T, int h, int E, int k, hipStream_t stream) {
+  const int64_t nblk = (T + ROUTE_TOKENS - 1) / ROUTE_TOKENS;
+  if (nblk == 0) return hipSuccess;
+  hipLaunchKernelGGL(route_kernel, dim3((unsigned)nblk), dim3(256), 0, stream, x, wr, wsg,
+                     logits_in, bias, logits_out, idx_out, w_out, gate_out, hist, T, h, E, k);
+  return hipGetLastError();
+}
+
+}  // namespace q38

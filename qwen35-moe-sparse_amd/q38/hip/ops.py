@@ -1,0 +1,272 @@
+"""Torch-tensor front end of the C ABI: shape/dtype checks, output allocation, stream passing.
+
+Every function launches HIP kernels on the current torch stream of the input's device and
+returns without synchronising. Inputs must be contiguous bf16 CUDA (HIP) tensors; weights use the
+reference parameter layouts (experts.gate_up_proj [E,2I,h], experts.down_proj [E,h,I],
+nn.Linear weights [out,in]).
+"""
+import ctypes
+
+import torch
+
+from ._lib import BF16, check, lib
+
+_NULL = None
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _need(t, name, dtype=torch.bfloat16, ndim=None):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA/HIP tensor (the Q38 MoE path runs only on the GPU)")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name} must have {ndim} dims, got shape {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+def _idx_flag(idx):
+    if idx.dtype == torch.int64:
+        return 1
+    if idx.dtype == torch.int32:
+        return 0
+    raise TypeError(f"routing indices must be int32 or int64, got {idx.dtype}")
+
+
+def gemm_block_m():
+    return int(lib.q38moe_gemm_block_m())
+
+
+def max_tiles(T, E, k, block_m=None):
+    return int(lib.q38moe_max_tiles(T, E, k, gemm_block_m() if block_m is None else block_m))
+
+
+def route(x, w_router, k, w_shared_gate=None, logit_bias=None, want_logits=False, want_hist=False):
+    """Router (modeling:805-813). Returns (logits|None, idx int32 [T,k], w bf16 [T,k],
+    shared_gate_logit bf16 [T]|None, hist int32 [ceil(T/64),E]|None)."""
+    _need(x, "x", ndim=2)
+    _need(w_router, "w_router", ndim=2)
+    T, h = x.shape
+    E = w_router.shape[0]
+    if w_router.shape[1] != h:
+        raise ValueError(f"w_router {tuple(w_router.shape)} does not match hidden {h}")
+    dev = x.device
+    if w_shared_gate is not None:
+        _need(w_shared_gate, "w_shared_gate")
+        if w_shared_gate.numel() != h:
+            raise ValueError("w_shared_gate must hold h elements")
+    if logit_bias is not None:
+        _need(logit_bias, "logit_bias", dtype=torch.float32, ndim=1)
+        if logit_bias.numel() != E:
+            raise ValueError("logit_bias must hold E elements")
+    logits = torch.empty(T, E, dtype=torch.bfloat16, device=dev) if want_logits else None
+    idx = torch.empty(T, k, dtype=torch.int32, device=dev)
+    w = torch.empty(T, k, dtype=torch.bfloat16, device=dev)
+    gate = torch.empty(T, dtype=torch.bfloat16, device=dev) if w_shared_gate is not None else None
+    hist = torch.empty((T + 63) // 64, E, dtype=torch.int32, device=dev) if want_hist else None
+    check(lib.q38moe_route(_ptr(x), _ptr(w_router), _ptr(w_shared_gate), _ptr(logit_bias), _ptr(logits),
+                           _ptr(idx), _ptr(w), _ptr(gate), _ptr(hist), T, h, E, k, BF16, _stream(dev)),
+          "q38moe_route")
+    return logits, idx, w, gate, hist
+
+
+def route_from_logits(logits, k, logit_bias=None, want_hist=False):
+    """Router selection (modeling:808-812) on given bf16 logits [T,E]: (idx int32, w bf16, hist)."""
+    _need(logits, "logits", ndim=2)
+    T, E = logits.shape
+    dev = logits.device
+    if logit_bias is not None:
+        _need(logit_bias, "logit_bias", dtype=torch.float32, ndim=1)
+    idx = torch.empty(T, k, dtype=torch.int32, device=dev)
+    w = torch.empty(T, k, dtype=torch.bfloat16, device=dev)
+    hist = torch.empty((T + 63) // 64, E, dtype=torch.int32, device=dev) if want_hist else None
+    check(lib.q38moe_route_from_logits(_ptr(logits), _ptr(logit_bias), _ptr(idx), _ptr(w), _ptr(hist),
+                                       T, E, k, BF16, _stream(dev)), "q38moe_route_from_logits")
+    return idx, w, hist
+
+
+def histogram(idx, E):
+    """Per-64-token-block expert counts of routing indices idx [T,k] (int32/int64)."""
+    _need(idx, "topk_idx", dtype=None, ndim=2)
+    T, k = idx.shape
+    hist = torch.empty((T + 63) // 64, E, dtype=torch.int32, device=idx.device)
+    check(lib.q38moe_histogram(_ptr(idx), _idx_flag(idx), _ptr(hist), T, E, k, _stream(idx.device)),
+          "q38moe_histogram")
+    return hist
+
+
+def permute(idx, hist, E, block_m=None):
+    """Stable counting sort of pairs by expert (inference.py:163-171): (counts, starts, perm, tiles)."""
+    _need(idx, "topk_idx", dtype=None, ndim=2)
+    _need(hist, "hist", dtype=torch.int32, ndim=2)
+    T, k = idx.shape
+    bm = gemm_block_m() if block_m is None else int(block_m)
+    dev = idx.device
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    starts = torch.empty(E, dtype=torch.int32, device=dev)
+    perm = torch.empty(T * k, dtype=torch.int32, device=dev)
+    tiles = torch.empty(max_tiles(T, E, k, bm), 4, dtype=torch.int32, device=dev)
+    check(lib.q38moe_permute(_ptr(idx), _idx_flag(idx), _ptr(hist), _ptr(counts), _ptr(starts), _ptr(perm),
+                             _ptr(tiles), bm, T, E, k, _stream(dev)), "q38moe_permute")
+    return counts, starts, perm, tiles
+
+
+def gate_up(x, w_gate_up, perm, tiles, k):
+    """Grouped gate/up GEMM + SwiGLU (inference.py:60-96): H [T*k, I] bf16 in sorted order."""
+    _need(x, "x", ndim=2)
+    _need(w_gate_up, "w_gate_up", ndim=3)
+    _need(perm, "perm", dtype=torch.int32)
+    _need(tiles, "tiles", dtype=torch.int32, ndim=2)
+    T, h = x.shape
+    E, twoI, hh = w_gate_up.shape
+    if hh != h or twoI % 2:
+        raise ValueError(f"w_gate_up {tuple(w_gate_up.shape)} does not match hidden {h}")
+    I = twoI // 2
+    if tiles.shape[0] != max_tiles(T, E, k):
+        raise ValueError("tiles was not built for this shape and the GEMM tile height")
+    H = torch.empty(T * k, I, dtype=torch.bfloat16, device=x.device)
+    check(lib.q38moe_gate_up(_ptr(x), _ptr(w_gate_up), _ptr(perm), _ptr(tiles), _ptr(H), T, h, E, k, I, BF16,
+                             _stream(x.device)), "q38moe_gate_up")
+    return H
+
+
+def down(H, w_down, perm, tiles, topk_w):
+    """Grouped down GEMM x routing weight (inference.py:99-130): y [T*k, h] bf16 in pair order."""
+    _need(H, "H", ndim=2)
+    _need(w_down, "w_down", ndim=3)
+    _need(perm, "perm", dtype=torch.int32)
+    _need(tiles, "tiles", dtype=torch.int32, ndim=2)
+    _need(topk_w, "topk_w", ndim=2)
+    T, k = topk_w.shape
+    E, h, I = w_down.shape
+    if H.shape != (T * k, I):
+        raise ValueError(f"H {tuple(H.shape)} does not match ({T * k}, {I})")
+    if tiles.shape[0] != max_tiles(T, E, k):
+        raise ValueError("tiles was not built for this shape and the GEMM tile height")
+    y = torch.empty(T * k, h, dtype=torch.bfloat16, device=H.device)
+    check(lib.q38moe_down(_ptr(H), _ptr(w_down), _ptr(perm), _ptr(tiles), _ptr(topk_w), _ptr(y), T, h, E, k, I,
+                          BF16, _stream(H.device)), "q38moe_down")
+    return y
+
+
+def shared_expert(x, w_gate, w_up, w_down):
+    """Qwen3_8MoeMLP.forward (modeling:751-753) on x [T,h]: [T,h] bf16."""
+    _need(x, "x", ndim=2)
+    for t, n in ((w_gate, "w_gate"), (w_up, "w_up"), (w_down, "w_down")):
+        _need(t, n, ndim=2)
+    T, h = x.shape
+    Is = w_gate.shape[0]
+    if w_gate.shape != (Is, h) or w_up.shape != (Is, h) or w_down.shape != (h, Is):
+        raise ValueError("shared expert weights must be [Is,h], [Is,h], [h,Is]")
+    Hs = torch.empty(T, Is, dtype=torch.bfloat16, device=x.device)
+    out = torch.empty(T, h, dtype=torch.bfloat16, device=x.device)
+    check(lib.q38moe_shared_expert(_ptr(x), _ptr(w_gate), _ptr(w_up), _ptr(w_down), _ptr(Hs), _ptr(out), T, h,
+                                   Is, BF16, _stream(x.device)), "q38moe_shared_expert")
+    return out
+
+
+def combine(y, k, E, idx=None, shared_out=None, shared_gate_logit=None):
+    """routed = bf16(sum_j y[t*k+j]) (inference.py:199), optionally + sigmoid-gated shared output."""
+    _need(y, "y", ndim=2)
+    P, h = y.shape
+    T = P // k
+    flag = 0
+    if idx is not None:
+        _need(idx, "topk_idx", dtype=None, ndim=2)
+        flag = _idx_flag(idx)
+    if shared_out is not None:
+        _need(shared_out, "shared_out", ndim=2)
+        _need(shared_gate_logit, "shared_gate_logit")
+    out = torch.empty(T, h, dtype=torch.bfloat16, device=y.device)
+    check(lib.q38moe_combine(_ptr(y), _ptr(idx), flag, _ptr(shared_out), _ptr(shared_gate_logit), _ptr(out), T, h,
+                             E, k, BF16, _stream(y.device)), "q38moe_combine")
+    return out
+
+
+def experts_workspace_bytes(T, h, E, k, I):
+    n = ctypes.c_size_t()
+    check(lib.q38moe_experts_workspace_bytes(T, h, E, k, I, ctypes.byref(n)), "q38moe_experts_workspace_bytes")
+    return n.value
+
+
+def experts_forward(x, topk_idx, topk_w, w_gate_up, w_down, workspace=None):
+    """Routed experts (ExpertsInterface contract, integrations/moe.py:567-570): [T,h] bf16."""
+    _need(x, "hidden_states", ndim=2)
+    _need(topk_idx, "top_k_index", dtype=None, ndim=2)
+    _need(topk_w, "top_k_weights", ndim=2)
+    _need(w_gate_up, "gate_up_proj", ndim=3)
+    _need(w_down, "down_proj", ndim=3)
+    T, h = x.shape
+    k = topk_idx.shape[1]
+    E, twoI, _ = w_gate_up.shape
+    I = twoI // 2
+    if topk_w.shape != topk_idx.shape or topk_idx.shape[0] != T:
+        raise ValueError("top_k_index/top_k_weights must both be [T,k]")
+    nbytes = experts_workspace_bytes(T, h, E, k, I)
+    if workspace is None:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    out = torch.empty(T, h, dtype=torch.bfloat16, device=x.device)
+    check(lib.q38moe_experts_forward(_ptr(x), _ptr(topk_idx), _idx_flag(topk_idx), _ptr(topk_w), _ptr(w_gate_up),
+                                     _ptr(w_down), _ptr(out), T, h, E, k, I, _ptr(workspace), workspace.numel(),
+                                     BF16, _stream(x.device)), "q38moe_experts_forward")
+    return out
+
+
+def block_workspace_bytes(T, h, E, k, I, Is):
+    n = ctypes.c_size_t()
+    check(lib.q38moe_block_workspace_bytes(T, h, E, k, I, Is, ctypes.byref(n)), "q38moe_block_workspace_bytes")
+    return n.value
+
+
+def block_forward(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_sh_down, w_sh_gate_proj, k,
+                  logit_bias=None, return_router=False, workspace=None, out=None):
+    """Qwen3_8MoeSparseMoeBlock.forward (modeling:824-835) on x [T,h]. Returns out [T,h] bf16, or
+    (out, logits [T,E], idx int32 [T,k], w bf16 [T,k]) with return_router."""
+    _need(x, "x", ndim=2)
+    for t, n in ((w_router, "w_router"), (w_sh_gate, "w_sh_gate"), (w_sh_up, "w_sh_up"),
+                 (w_sh_down, "w_sh_down")):
+        _need(t, n, ndim=2)
+    _need(w_gate_up, "w_gate_up", ndim=3)
+    _need(w_down, "w_down", ndim=3)
+    _need(w_sh_gate_proj, "w_sh_gate_proj")
+    T, h = x.shape
+    E = w_router.shape[0]
+    I = w_gate_up.shape[1] // 2
+    Is = w_sh_gate.shape[0]
+    if w_gate_up.shape != (E, 2 * I, h) or w_down.shape != (E, h, I) or w_router.shape != (E, h):
+        raise ValueError("expert weights must be [E,2I,h] and [E,h,I], router [E,h]")
+    if w_sh_gate.shape != (Is, h) or w_sh_up.shape != (Is, h) or w_sh_down.shape != (h, Is):
+        raise ValueError("shared expert weights must be [Is,h], [Is,h], [h,Is]")
+    if w_sh_gate_proj.numel() != h:
+        raise ValueError("shared_expert_gate weight must hold h elements")
+    if logit_bias is not None:
+        _need(logit_bias, "logit_bias", dtype=torch.float32, ndim=1)
+    dev = x.device
+    nbytes = block_workspace_bytes(T, h, E, k, I, Is)
+    if workspace is None or workspace.numel() < nbytes:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    if out is None:
+        out = torch.empty(T, h, dtype=torch.bfloat16, device=dev)
+    logits = idx = w = None
+    if return_router:
+        logits = torch.empty(T, E, dtype=torch.bfloat16, device=dev)
+        idx = torch.empty(T, k, dtype=torch.int32, device=dev)
+        w = torch.empty(T, k, dtype=torch.bfloat16, device=dev)
+    check(lib.q38moe_block_forward(_ptr(x), _ptr(w_router), _ptr(w_gate_up), _ptr(w_down), _ptr(w_sh_gate),
+                                   _ptr(w_sh_up), _ptr(w_sh_down), _ptr(w_sh_gate_proj), _ptr(logit_bias), _ptr(out),
+                                   _ptr(logits), _ptr(idx), _ptr(w), T, h, E, k, I, Is, _ptr(workspace),
+                                   workspace.numel(), BF16, _stream(dev)), "q38moe_block_forward")
+    if return_router:
+        return out, logits, idx, w
+    return out

@@ -1,0 +1,106 @@
+"""The C ABI library: loads, exports every entry point of include/q38moe.h, validates arguments on
+the host. CPU only: no call here reaches a kernel launch."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "q38moe.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(q38moe_\w+)\s*\(", text)))
+
+
+def _lib():
+    from q38.hip import _lib
+    return _lib
+
+
+def test_header_symbols_exported():
+    m = _lib()
+    names = _declared()
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(m.lib, n), f"{n} declared in q38moe.h but not exported"
+    assert set(names) == set(m.SIGNATURES), "ctypes signatures and header disagree"
+
+
+def test_abi_version():
+    m = _lib()
+    assert m.lib.q38moe_abi_version() == m.ABI_VERSION == 1
+
+
+def test_max_tiles_and_block_m():
+    m = _lib()
+    bm = m.lib.q38moe_gemm_block_m()
+    assert bm in (64, 128, 256)
+    assert m.lib.q38moe_max_tiles(16384, 64, 5, 128) == (16384 * 5 + 127) // 128 + 64
+    assert m.lib.q38moe_max_tiles(-1, 64, 5, 128) == -1
+
+
+def test_workspace_sizes():
+    m = _lib()
+    n = ctypes.c_size_t()
+    assert m.lib.q38moe_experts_workspace_bytes(16384, 1024, 64, 5, 256, ctypes.byref(n)) == 0
+    P = 16384 * 5
+    assert n.value >= P * 256 * 2 + P * 1024 * 2 + P * 4
+    nb = ctypes.c_size_t()
+    assert m.lib.q38moe_block_workspace_bytes(16384, 1024, 64, 5, 256, 256, ctypes.byref(nb)) == 0
+    assert nb.value > n.value
+
+
+@pytest.mark.parametrize("T,h,E,k,I,msg", [
+    (16, 1000, 64, 5, 256, "h must be"),
+    (16, 1024, 65, 5, 256, "E must be"),
+    (16, 1024, 64, 9, 256, "k must be"),
+    (16, 1024, 4, 5, 256, "k must be"),
+    (16, 1024, 64, 5, 100, "I must be"),
+    (-1, 1024, 64, 5, 256, "T must be"),
+    (1 << 29, 1024, 64, 5, 256, "T\\*k"),
+])
+def test_invalid_shapes_rejected(T, h, E, k, I, msg):
+    m = _lib()
+    n = ctypes.c_size_t()
+    rc = m.lib.q38moe_experts_workspace_bytes(T, h, E, k, I, ctypes.byref(n))
+    assert rc == -1
+    assert re.search(msg, m.lib.q38moe_last_error().decode())
+
+
+def test_bad_dtype_and_pointers():
+    m = _lib()
+    rc = m.lib.q38moe_route(None, None, None, None, None, None, None, None, None, 16, 1024, 64, 5, 7, None)
+    assert rc == -1 and "dtype" in m.lib.q38moe_last_error().decode()
+    rc = m.lib.q38moe_route(None, None, None, None, None, None, None, None, None, 16, 1024, 64, 5, m.BF16, None)
+    assert rc == -1 and "x must not be NULL" in m.lib.q38moe_last_error().decode()
+    rc = m.lib.q38moe_route(ctypes.c_void_p(8), ctypes.c_void_p(16), None, None, None, None, None, None, None,
+                            16, 1024, 64, 5, m.BF16, None)
+    assert rc == -1 and "16-byte aligned" in m.lib.q38moe_last_error().decode()
+
+
+def test_workspace_too_small():
+    m = _lib()
+    p = ctypes.c_void_p(1 << 20)
+    rc = m.lib.q38moe_experts_forward(p, p, 0, p, p, p, p, 64, 1024, 64, 5, 256, p, 16, m.BF16, None)
+    assert rc == -2 and "workspace needs" in m.lib.q38moe_last_error().decode()
+
+
+def test_empty_problem_is_noop():
+    m = _lib()
+    assert m.lib.q38moe_route(None, None, None, None, None, None, None, None, None, 0, 1024, 64, 5, m.BF16, None) == 0
+    assert m.lib.q38moe_experts_forward(None, None, 0, None, None, None, None, 0, 1024, 64, 5, 256, None, 0,
+                                        m.BF16, None) == 0
+
+
+def test_ops_reject_cpu_tensors():
+    """The torch front end fails loudly for non-GPU tensors: there is no CPU fallback."""
+    import torch
+    from q38.hip import ops
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    w = torch.zeros(8, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="CUDA/HIP tensor"):
+        ops.route(x, w, 2)

@@ -1,0 +1,132 @@
+"""GPU parity of the grouped GEMMs, combine, shared expert and the whole MoE block (R0, R5-R9)
+against the CPU oracle (fp32 matmuls with the reference's explicit bf16 rounding points).
+
+Tolerance (bf16): max-abs <= 2e-2 and relative L2 <= 1e-2 (tests/_util.py).
+"""
+import pytest
+import torch
+
+from _util import assert_bf16_close, assert_gemm_bf16_rounding, bf16_ulp_diff
+from oracle import moe_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from q38.hip import ops
+    return ops
+
+
+def _setup(name, T=None, **over):
+    from q38 import workloads
+    wl = workloads.get(name, **over) if over else workloads.get(name)
+    x, params, bias = workloads.make(wl, tokens=T)
+    return wl, x, params, bias
+
+
+@pytest.mark.parametrize("name,T", [("c1", 2048), ("c2", 4096)])
+def test_gate_up_down_stages(gpu, name, T):
+    """Each stage against the oracle on identical inputs (oracle routing, GPU permutation)."""
+    ops = _ops()
+    wl, x, params, _ = _setup(name, T)
+    k = wl.topk
+    _, _, ridx, rw = orc.router(x, params["gate.weight"], k)
+    ref_out, ref_y, ref_H = orc.experts_grouped(x, ridx, rw, params["experts.gate_up_proj"],
+                                                params["experts.down_proj"])
+    dx, didx, dw = x.to(gpu), ridx.to(gpu), rw.to(gpu)
+    wgu, wdn = params["experts.gate_up_proj"].to(gpu), params["experts.down_proj"].to(gpu)
+    hist = ops.histogram(didx, wl.experts)
+    counts, starts, perm, tiles = ops.permute(didx, hist, wl.experts)
+    H = ops.gate_up(dx, wgu, perm, tiles, k)
+    torch.cuda.synchronize()
+    # H in sorted order: bf16 results of identical roundings; fp32 accumulation order differs.
+    assert_bf16_close(H.cpu(), ref_H, what="H (gate/up + SwiGLU)")
+    assert float((bf16_ulp_diff(H.cpu(), ref_H) > 1).float().mean()) < 1e-3
+    y = ops.down(H, wdn, perm, tiles, dw)
+    torch.cuda.synchronize()
+    assert_bf16_close(y.cpu(), ref_y, what="y (down x weight)")
+    # Down alone on the oracle's H: isolates the down GEMM.
+    y2 = ops.down(ref_H.to(gpu), wdn, perm, tiles, dw)
+    torch.cuda.synchronize()
+    assert float((bf16_ulp_diff(y2.cpu(), ref_y) > 1).float().mean()) < 1e-3
+    out = ops.combine(y, k, wl.experts)
+    torch.cuda.synchronize()
+    assert_bf16_close(out.cpu(), ref_out, what="routed experts output")
+
+
+@pytest.mark.parametrize("name,T", [("c1", 2048), ("c2", 4096), ("c2", 333)])
+def test_shared_expert(gpu, name, T):
+    ops = _ops()
+    wl, x, params, _ = _setup(name, T)
+    wg, wu, wd = (params[f"shared_expert.{n}_proj.weight"] for n in ("gate", "up", "down"))
+    ref = orc.shared_expert(x, wg, wu, wd)
+    out = ops.shared_expert(x.to(gpu), wg.to(gpu), wu.to(gpu), wd.to(gpu))
+    torch.cuda.synchronize()
+    assert_bf16_close(out.cpu(), ref, what="shared expert")
+
+
+@pytest.mark.parametrize("name,T", [("c1", 2048), ("c2", 16384), ("c3", 16384), ("c2", 1000)])
+def test_block_forward(gpu, name, T):
+    """Whole block vs the oracle; routing compared on the GPU's own logits (bit-exact)."""
+    ops = _ops()
+    wl, x, params, bias = _setup(name, T)
+    d = {n: p.to(gpu) for n, p in params.items()}
+    out, logits, idx, w = ops.block_forward(
+        x.to(gpu), d["gate.weight"], d["experts.gate_up_proj"], d["experts.down_proj"],
+        d["shared_expert.gate_proj.weight"], d["shared_expert.up_proj.weight"], d["shared_expert.down_proj.weight"],
+        d["shared_expert_gate.weight"], wl.topk, logit_bias=None if bias is None else bias.to(gpu),
+        return_router=True)
+    torch.cuda.synchronize()
+    ref_out, inter = orc.block(x, params, wl.topk, logit_bias=bias)
+    assert_gemm_bf16_rounding(logits, x, params["gate.weight"], "router logits")
+    _, _, sidx, _ = orc.router(None, None, wl.topk, logit_bias=bias, logits=logits.cpu())
+    assert torch.equal(idx.cpu().long(), sidx)
+    mx, r = assert_bf16_close(out.cpu(), ref_out, what=f"{name} block output")
+    print(f"{name} T={T}: max-abs {mx:.3e} rel {r:.3e}")
+
+
+def test_experts_forward_int64(gpu):
+    """ExpertsInterface entry (int64 top_k_index, as torch.topk returns) vs the oracle."""
+    ops = _ops()
+    wl, x, params, _ = _setup("c2", 2048)
+    _, _, ridx, rw = orc.router(x, params["gate.weight"], wl.topk)
+    ref, _, _ = orc.experts_grouped(x, ridx, rw, params["experts.gate_up_proj"], params["experts.down_proj"])
+    out = ops.experts_forward(x.to(gpu), ridx.to(gpu), rw.to(gpu), params["experts.gate_up_proj"].to(gpu),
+                              params["experts.down_proj"].to(gpu))
+    torch.cuda.synchronize()
+    assert_bf16_close(out.cpu(), ref, what="experts_forward")
+
+
+def test_dropin_module_and_registry(gpu):
+    """Drop-in modules load a reference-named state dict; the registered experts implementation
+    and the fused block agree with the oracle."""
+    from q38.inference import register_experts_implementation
+    from q38.models.qwen3_8_moe import Qwen3_8MoeSparseMoeBlock, new_config
+    wl, x, params, _ = _setup("c1", 512)
+    cfg = new_config(hidden_size=wl.hidden, num_experts=wl.experts, num_experts_per_tok=wl.topk,
+                     moe_intermediate_size=wl.inter, shared_expert_intermediate_size=wl.shared_inter)
+    block = Qwen3_8MoeSparseMoeBlock(cfg).to(torch.bfloat16)
+    missing, unexpected = block.load_state_dict(params, strict=True)
+    assert not missing and not unexpected
+    block = block.to(gpu)
+    ref_out, inter = orc.block(x, params, wl.topk)
+    with torch.inference_mode():
+        out = block(x.view(1, -1, wl.hidden).to(gpu))
+        logits, scores, sel = block.gate(x.to(gpu))
+        assert sel.dtype == torch.int64
+        assert register_experts_implementation() == "q38_hip"
+        routed = block.experts(x.to(gpu), sel, scores)
+        hooked = []
+        h = block.gate.register_forward_hook(lambda m, i, o: hooked.append(o[0]))
+        out2 = block(x.view(1, -1, wl.hidden).to(gpu))
+        h.remove()
+    torch.cuda.synchronize()
+    assert_bf16_close(out.view(-1, wl.hidden).cpu(), ref_out, what="drop-in block")
+    assert_bf16_close(out2.view(-1, wl.hidden).cpu(), ref_out, what="drop-in block (hooked router)")
+    assert len(hooked) == 1 and hooked[0].shape == (512, wl.experts)
+    ref_routed, _, _ = orc.experts_grouped(x, sel.cpu(), scores.cpu(), params["experts.gate_up_proj"],
+                                           params["experts.down_proj"])
+    assert_bf16_close(routed.cpu(), ref_routed, what="drop-in experts")
+    with pytest.raises(RuntimeError, match="no backward"):
+        block.float().requires_grad_(True)
+        block(x.view(1, -1, wl.hidden).to(gpu).float())

@@ -1,0 +1,132 @@
+"""GPU parity of the router (R1-R2): routing indices bit-exact against the CPU oracle.
+
+The oracle is torch's CPU top-k restated in oracle/q38_oracle.cpp (libstdc++ nth_element/sort,
+ATen/native/TopKImpl.h:45-76) applied to the CPU fp32 softmax of the same bf16 logits.
+"""
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_gemm_bf16_rounding, bf16_ulp_diff
+from oracle import moe_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from q38.hip import ops
+    return ops
+
+
+def _check_selection(logits, k, gpu, bias=None):
+    ops = _ops()
+    idx, w, hist = ops.route_from_logits(logits.to(gpu), k,
+                                         logit_bias=None if bias is None else bias.to(gpu), want_hist=True)
+    torch.cuda.synchronize()
+    _, _, ridx, rw = orc.router(None, None, k, logit_bias=bias, logits=logits)
+    idx = idx.cpu().long()
+    bad = (idx != ridx).any(dim=1)
+    assert int(bad.sum()) == 0, f"{int(bad.sum())} rows differ; first: {torch.nonzero(bad)[:5].flatten().tolist()}"
+    # Renormalised weights: fp32 softmax with a different exp(); at most 1 bf16 ulp apart.
+    assert int(bf16_ulp_diff(w.cpu(), rw).max()) <= 1
+    T, E = logits.shape
+    # Histogram of 64-token blocks.
+    ref_hist = torch.zeros((T + 63) // 64, E, dtype=torch.int64)
+    blk = torch.arange(T).repeat_interleave(k) // 64
+    ref_hist.index_put_((blk, ridx.reshape(-1)), torch.ones(T * k, dtype=torch.int64), accumulate=True)
+    assert torch.equal(hist.cpu().long(), ref_hist)
+
+
+@pytest.mark.parametrize("T,E,k,scale,seed", [
+    (16384, 64, 5, 0.64, 0),   # config-2 logit scale (x ~ N(0,1), h=1024, W ~ N(0,0.02))
+    (2048, 64, 5, 0.32, 1),    # config-1 logit scale
+    (1000, 8, 3, 1.0, 2),      # the reference's parity-script routing shape (E=8, k=3)
+    (777, 64, 8, 0.5, 3),      # k = 8, ragged T
+    (129, 17, 4, 0.5, 4),      # E not a multiple of 16
+])
+def test_route_from_logits_random(gpu, T, E, k, scale, seed):
+    g = torch.Generator().manual_seed(seed)
+    logits = (torch.randn(T, E, generator=g) * scale).to(torch.bfloat16)
+    _check_selection(logits, k, gpu)
+
+
+@pytest.mark.parametrize("levels,seed", [(6, 10), (3, 11), (2, 12), (1, 13)])
+def test_route_from_logits_ties(gpu, levels, seed):
+    """Tie-heavy rows: integer-valued logits in [0, levels); exercises the libstdc++ replay."""
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randint(0, levels, (8192, 64), generator=g).to(torch.bfloat16)
+    _check_selection(logits, 5, gpu)
+
+
+def test_route_known_answer(gpu):
+    """[.1,.5,.5,.2,.5,.5,.5,0] top-5 -> [1,6,5,4,2] on torch CPU (not index order)."""
+    vals = torch.tensor([[0.1, 0.5, 0.5, 0.2, 0.5, 0.5, 0.5, 0.0]]).log().to(torch.bfloat16)
+    ops = _ops()
+    idx, _, _ = ops.route_from_logits(vals.to(gpu), 5)
+    assert idx.cpu().tolist() == [[1, 6, 5, 4, 2]]
+
+
+def test_route_partial_sort_path(gpu):
+    """k*64 <= E (k=1, E=64): torch takes std::partial_sort -> lowest-index maximum."""
+    g = torch.Generator().manual_seed(5)
+    logits = torch.randint(0, 3, (4096, 64), generator=g).to(torch.bfloat16)
+    _check_selection(logits, 1, gpu)
+
+
+def test_route_special_rows(gpu):
+    T, E = 64, 64
+    logits = torch.zeros(T, E)
+    logits[1, 7] = float("nan")               # softmax row all NaN -> all tied
+    logits[2, :] = float("-inf")              # all -inf -> NaN row
+    logits[3, 5] = float("inf")
+    logits[4, :] = -0.0                       # signed zeros tie with +0
+    logits[4, ::2] = 0.0
+    logits[5, :] = torch.arange(E, dtype=torch.float32)  # strictly increasing
+    logits[6, :] = -torch.arange(E, dtype=torch.float32)
+    logits = logits.to(torch.bfloat16)
+    ops = _ops()
+    idx, w, _ = ops.route_from_logits(logits.to(gpu), 5)
+    _, probs, ridx, rw = orc.router(None, None, 5, logits=logits)
+    assert torch.equal(idx.cpu().long(), ridx)
+    # Rows with finite softmax: weights match within 1 ulp; NaN rows are NaN in both.
+    wn, rn = w.cpu().float(), rw.float()
+    assert torch.equal(torch.isnan(wn), torch.isnan(rn))
+    fin = ~torch.isnan(rn)
+    assert int(bf16_ulp_diff(w.cpu()[fin], rw[fin]).max()) <= 1
+
+
+def test_route_with_bias(gpu):
+    """Routing-skew bias added to the logits before the softmax (configuration 3)."""
+    g = torch.Generator().manual_seed(21)
+    logits = (torch.randn(4096, 64, generator=g) * 0.64).to(torch.bfloat16)
+    ranks = torch.from_numpy(np.random.RandomState(7).permutation(64) + 1).double()
+    bias = (-1.2 * ranks.log()).float()
+    _check_selection(logits, 5, gpu, bias=bias)
+
+
+@pytest.mark.parametrize("wl_name,T", [("c1", 2048), ("c2", 16384)])
+def test_route_full(gpu, wl_name, T):
+    """Logits GEMM on MFMA: within 1 bf16 ulp of the fp32 reference; selection exact on them."""
+    from q38 import workloads
+    wl = workloads.get(wl_name)
+    x, params, _ = workloads.make(wl, tokens=T)
+    ops = _ops()
+    wr = params["gate.weight"]
+    ws = params["shared_expert_gate.weight"]
+    logits, idx, w, gate, hist = ops.route(x.to(gpu), wr.to(gpu), wl.topk, w_shared_gate=ws.to(gpu),
+                                           want_logits=True, want_hist=True)
+    torch.cuda.synchronize()
+    ref_logits = orc.bf16(x.float() @ wr.float().T)
+    assert_gemm_bf16_rounding(logits, x, wr, "router logits")
+    assert_gemm_bf16_rounding(gate, x, ws, "shared gate logit")
+    # Selection is a function of the logits: exact against the oracle on the GPU logits.
+    _, _, ridx, rw = orc.router(None, None, wl.topk, logits=logits.cpu())
+    assert torch.equal(idx.cpu().long(), ridx)
+    assert int(bf16_ulp_diff(w.cpu(), rw).max()) <= 1
+    # End to end against CPU-computed logits: every differing row must trace to a 1-ulp logit
+    # difference (report, do not hide, the count).
+    _, _, eidx, _ = orc.router(x, wr, wl.topk)
+    rows = (idx.cpu().long() != eidx).any(dim=1)
+    if rows.any():
+        assert (logits.cpu()[rows] != ref_logits[rows]).any(dim=1).all()
+    print(f"{wl_name}: {int(rows.sum())} of {T} rows route differently from CPU-computed logits")

@@ -1,0 +1,151 @@
+"""Pins of the CPU oracle (oracle/) against independent facts. CPU only.
+
+The reference ships no MoE golden vectors (its only parity artefact, audits/q38_kernel_parity.json,
+holds error magnitudes). The oracle is pinned instead by: torch's own CPU top-k on tie-heavy data
+(the library whose semantics the router must reproduce), a hand-worked tie case, torch.sort(stable)
+for the permutation, float64 brute force on tiny blocks, and closed-form special cases.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import moe_oracle as orc
+
+
+def test_topk_known_answer():
+    """Hand-worked libstdc++ introselect on [.1,.5,.5,.2,.5,.5,.5,0], k=5 -> [1,6,5,4,2]."""
+    v = np.array([[0.1, 0.5, 0.5, 0.2, 0.5, 0.5, 0.5, 0.0]], np.float32)
+    vals, idx = orc.topk_cpu(v, 5)
+    assert idx.tolist() == [[1, 6, 5, 4, 2]]
+    assert torch.topk(torch.from_numpy(v), 5).indices.tolist() == [[1, 6, 5, 4, 2]]
+
+
+@pytest.mark.parametrize("kind", ["int", "bf16", "nan"])
+def test_topk_matches_torch_cpu(kind):
+    g = torch.Generator().manual_seed(0)
+    if kind == "int":
+        v = torch.randint(0, 6, (20000, 64), generator=g).float()
+    elif kind == "bf16":
+        v = torch.softmax((torch.randn(20000, 64, generator=g) * 0.64).to(torch.bfloat16).float(), -1)
+    else:
+        v = torch.randint(0, 4, (5000, 64), generator=g).float()
+        v[torch.rand(5000, 64, generator=g) < 0.05] = float("nan")
+    for k in (1, 3, 5, 8):
+        ov, oi = orc.topk_cpu(v.numpy(), k)
+        tv, ti = torch.topk(v, k)
+        assert np.array_equal(oi, ti.numpy()), f"k={k}"
+        assert np.array_equal(np.isnan(ov), torch.isnan(tv).numpy())
+
+
+def test_topk_small_n():
+    g = torch.Generator().manual_seed(1)
+    v = torch.randint(0, 3, (5000, 8), generator=g).float()
+    ov, oi = orc.topk_cpu(v.numpy(), 3)
+    assert np.array_equal(oi, torch.topk(v, 3).indices.numpy())
+
+
+@pytest.mark.parametrize("T,E,k", [(1000, 64, 5), (53, 8, 3), (0, 64, 5)])
+def test_permute_matches_stable_sort(T, E, k):
+    g = torch.Generator().manual_seed(2)
+    idx = torch.randint(0, E, (T, k), generator=g)
+    counts, starts, perm = orc.permute_cpu(idx.numpy(), E)
+    ids = idx.reshape(-1)
+    sorted_ids, tperm = torch.sort(ids, stable=True)
+    assert np.array_equal(perm, tperm.numpy())
+    assert np.array_equal(counts, torch.bincount(ids, minlength=E).numpy())
+    bounds = torch.searchsorted(sorted_ids, torch.arange(E + 1))
+    assert np.array_equal(starts, bounds[:-1].numpy())
+    # Invariants: a permutation, ids non-decreasing along it, ascending within an expert.
+    assert np.array_equal(np.sort(perm), np.arange(T * k))
+    assert (np.diff(ids.numpy()[perm]) >= 0).all()
+
+
+def test_permute_drops_sentinels():
+    ids = np.array([3, 8, -1, 0, 3, 7, 9], np.int64)
+    counts, starts, perm = orc.permute_cpu(ids, 8)
+    assert perm.tolist() == [3, 0, 4, 5] and counts.sum() == 4
+
+
+def _tiny_params(h=64, E=8, I=64, Is=64, seed=0):
+    from q38 import workloads
+    wl = workloads.Workload("tiny", hidden=h, experts=E, topk=3, inter=I, shared_inter=Is, batch=1, seq=37)
+    x, p, _ = workloads.make(wl, seed_w=seed)
+    return wl, x, p
+
+
+def test_block_vs_float64_bruteforce():
+    """Per-token float64 loop of the block's math; oracle (bf16 roundings) must be within bf16
+    tolerance. A transposed weight, wrong gate/up half or dropped routing weight fails this."""
+    wl, x, p = _tiny_params()
+    out, inter = orc.block(x, p, wl.topk)
+    xd = x.double()
+    wr, gu, dn = p["gate.weight"].double(), p["experts.gate_up_proj"].double(), p["experts.down_proj"].double()
+    I = wl.inter
+    ref = torch.zeros_like(xd)
+    for t in range(xd.shape[0]):
+        probs = torch.softmax(xd[t] @ wr.T, -1)
+        idx = inter["idx"][t]
+        wsel = probs[idx] / probs[idx].sum()
+        for j, e in enumerate(idx.tolist()):
+            hv = gu[e] @ xd[t]
+            act = hv[:I] / (1 + torch.exp(-hv[:I])) * hv[I:]
+            ref[t] += wsel[j] * (dn[e] @ act)
+        g = p["shared_expert.gate_proj.weight"].double() @ xd[t]
+        u = p["shared_expert.up_proj.weight"].double() @ xd[t]
+        sh = p["shared_expert.down_proj.weight"].double() @ (g / (1 + torch.exp(-g)) * u)
+        sg = torch.sigmoid(p["shared_expert_gate.weight"].double().reshape(-1) @ xd[t])
+        ref[t] += sg * sh
+    diff = (out.double() - ref).abs()
+    assert float(diff.max()) < 2e-2
+    assert float(diff.norm() / ref.norm()) < 1e-2
+
+
+def test_grouped_vs_eager_experts():
+    """The oracle's grouped rounding (inference.py:60-130,199) vs the eager loop (modeling:769-793)."""
+    from q38 import workloads
+    wl = workloads.get("c1")
+    x, p, _ = workloads.make(wl, tokens=512)
+    _, _, idx, w = orc.router(x, p["gate.weight"], wl.topk)
+    a, _, _ = orc.experts_grouped(x, idx, w, p["experts.gate_up_proj"], p["experts.down_proj"])
+    b = orc.experts_eager(x, idx, w, p["experts.gate_up_proj"], p["experts.down_proj"])
+    diff = (a.float() - b.float()).abs()
+    assert float(diff.max()) < 2e-2 and float(diff.norm() / b.float().norm()) < 1e-2
+
+
+def test_reference_block_forward_matches_oracle():
+    from q38 import workloads
+    wl = workloads.get("c1")
+    x, p, _ = workloads.make(wl, tokens=256)
+    a, _ = orc.block(x, p, wl.topk)
+    b = orc.reference_block_forward(x, p, wl.topk)
+    diff = (a.float() - b.float()).abs()
+    assert float(diff.max()) < 2e-2 and float(diff.norm() / b.float().norm()) < 1e-2
+
+
+def test_special_cases():
+    """Zero router weight: uniform probabilities, all tied -> torch's tie order, equal weights 1/k.
+    k = E: every expert selected. Zero shared-gate weight: sigmoid(0) = 0.5 exactly."""
+    wl, x, p = _tiny_params()
+    p0 = dict(p)
+    p0["gate.weight"] = torch.zeros_like(p["gate.weight"])
+    _, probs, idx, w = orc.router(x, p0["gate.weight"], wl.topk)
+    ti = torch.topk(torch.full((1, wl.experts), 1.0 / wl.experts), wl.topk).indices
+    assert torch.equal(idx, ti.expand_as(idx))
+    assert torch.equal(w, torch.full_like(w, 1.0 / wl.topk))
+    _, _, idx_all, w_all = orc.router(x, p["gate.weight"], wl.experts)
+    assert torch.equal(idx_all.sort(-1).values, torch.arange(wl.experts).expand_as(idx_all))
+    p2 = dict(p)
+    p2["shared_expert_gate.weight"] = torch.zeros_like(p["shared_expert_gate.weight"])
+    _, inter = orc.block(x, p2, wl.topk)
+    out2, _ = orc.block(x, p2, wl.topk)
+    half = orc.bf16(0.5 * inter["shared"].float())
+    assert torch.equal(out2, orc.bf16(inter["routed"].float() + half.float()))
+
+
+def test_shared_expert_matches_linear_chain():
+    wl, x, p = _tiny_params()
+    wg, wu, wd = (p[f"shared_expert.{n}_proj.weight"] for n in ("gate", "up", "down"))
+    ref = F.linear(F.silu(F.linear(x, wg)) * F.linear(x, wu), wd)
+    diff = (orc.shared_expert(x, wg, wu, wd).float() - ref.float()).abs()
+    assert float(diff.max()) < 2e-2
