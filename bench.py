@@ -48,28 +48,36 @@ def kernel_breakdown(wl, x, d, bias, iters, stream):
     P = T * k
     logits, idx, w, gate, hist = ops.route(x, d["gate.weight"], k, w_shared_gate=d["shared_expert_gate.weight"],
                                            logit_bias=bias, want_hist=True)
-    counts, starts, perm, tiles = ops.permute(idx, hist, E)
-    H = ops.gate_up(x, d["experts.gate_up_proj"], perm, tiles, k)
-    y = ops.down(H, d["experts.down_proj"], perm, tiles, w)
-    sh = ops.shared_expert(x, d["shared_expert.gate_proj.weight"], d["shared_expert.up_proj.weight"],
-                           d["shared_expert.down_proj.weight"])
+    fused = I == Is
+    srows = T if fused else 0
+    counts, starts, perm, inv, tiles, tcount = ops.permute(idx, hist, E, shared_rows=srows)
+    sh_w = (d["shared_expert.gate_proj.weight"], d["shared_expert.up_proj.weight"])
+    H = ops.gate_up(x, d["experts.gate_up_proj"], perm, tiles, tcount, k, shared_weights=sh_w, shared_rows=srows)
+    Y = ops.down(H, d["experts.down_proj"], tiles, tcount, T, k, w_shared_down=d["shared_expert.down_proj.weight"],
+                 shared_rows=srows)
+    sh = Y[P:] if fused else ops.shared_expert(x, *sh_w, d["shared_expert.down_proj.weight"])
     torch.cuda.synchronize()
     fl = wl.flops()
+    sh_fl = fl["shared"] if fused else 0
     stages = {
         "route": (lambda: ops.route(x, d["gate.weight"], k, w_shared_gate=d["shared_expert_gate.weight"],
                                     logit_bias=bias, want_hist=True), "hbm",
                   # x read + router weights + idx/w/gate/hist written
                   T * h * 2 + (E + 1) * h * 2 + P * 6 + T * 2),
-        "permute": (lambda: ops.permute(idx, hist, E), "hbm", P * 4 * 2),
-        "gate_up": (lambda: ops.gate_up(x, d["experts.gate_up_proj"], perm, tiles, k), "mfma", fl["gate_up"]),
-        "down": (lambda: ops.down(H, d["experts.down_proj"], perm, tiles, w), "mfma", fl["down"]),
-        "shared_expert": (lambda: ops.shared_expert(x, d["shared_expert.gate_proj.weight"],
-                                                    d["shared_expert.up_proj.weight"],
-                                                    d["shared_expert.down_proj.weight"]), "mfma", fl["shared"]),
+        "permute": (lambda: ops.permute(idx, hist, E, shared_rows=srows), "hbm", P * 4 * 3),
+        # gate/up: routed pairs (+ the shared expert's gate/up when it runs in the same launch)
+        "gate_up": (lambda: ops.gate_up(x, d["experts.gate_up_proj"], perm, tiles, tcount, k, shared_weights=sh_w,
+                                        shared_rows=srows), "mfma", fl["gate_up"] + sh_fl * 2 // 3),
+        "down": (lambda: ops.down(H, d["experts.down_proj"], tiles, tcount, T, k,
+                                  w_shared_down=d["shared_expert.down_proj.weight"], shared_rows=srows), "mfma",
+                 fl["down"] + sh_fl // 3),
         # combine reads k bf16 rows + the shared row, writes one row per token
-        "combine": (lambda: ops.combine(y, k, E, shared_out=sh, shared_gate_logit=gate), "hbm",
+        "combine": (lambda: ops.combine(Y, inv, w, E, shared_out=sh, shared_gate_logit=gate), "hbm",
                     T * h * 2 * (k + 2)),
     }
+    if not fused:
+        stages["shared_expert"] = (lambda: ops.shared_expert(x, *sh_w, d["shared_expert.down_proj.weight"]), "mfma",
+                                   fl["shared"])
     out = {}
     for name, (fn, bound, work) in stages.items():
         fn()
@@ -83,22 +91,22 @@ def kernel_breakdown(wl, x, d, bias, iters, stream):
     return out
 
 
-def cpu_baseline(wl, budget_s=20.0):
-    """The reference block's own op sequence (eager experts loop) in bf16 on this host's CPU."""
+def cpu_baseline(wl, budget_s=15.0):
+    """The reference block's own op sequence (eager experts loop) in bf16 on this host's CPU, on the
+    first `tokens` tokens of the same workload (all of them when they fit the time budget)."""
     import torch
     from oracle import moe_oracle
     from q38 import workloads
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
-    x_all, params, _ = workloads.make(wl, tokens=2048)
-    tokens = 256
+    x_all, params, _ = workloads.make(wl)
+    tokens = min(1024, wl.tokens)
     with torch.inference_mode():
         t0 = time.perf_counter()
-        moe_oracle.reference_block_forward(x_all[:tokens], params, wl.topk)  # warmup
-        first = time.perf_counter() - t0
-        # Size the sample so the 3 timed runs take about budget_s.
-        per_tok = first / tokens
-        tokens = int(max(256, min(2048, budget_s / 3 / max(per_tok, 1e-9))))
+        moe_oracle.reference_block_forward(x_all[:tokens], params, wl.topk)  # warmup + size probe
+        per_tok = (time.perf_counter() - t0) / tokens
+        # Size the sample so the 3 timed runs take about budget_s (whole workload if it fits).
+        tokens = int(max(1024, min(wl.tokens, budget_s / 3 / max(per_tok, 1e-9))))
         x = x_all[:tokens]
         times = []
         for _ in range(3):
@@ -108,8 +116,8 @@ def cpu_baseline(wl, budget_s=20.0):
     times.sort()
     med = times[1]
     return dict(value=round(tokens / med, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
-                sample=f"{tokens} tokens of {wl.name} (h={wl.hidden}, E={wl.experts}, k={wl.topk}, I={wl.inter}), "
-                       f"bf16 torch CPU, reference op sequence with the eager experts loop "
+                sample=f"{tokens} of the {wl.tokens} tokens of {wl.name} (h={wl.hidden}, E={wl.experts}, k={wl.topk}, "
+                       f"I={wl.inter}), bf16 torch CPU, reference op sequence with the eager experts loop "
                        f"(modeling_qwen3_8_moe.py:769-793,805-813,824-835), median of 3 after 1 warmup",
                 seconds=[round(t, 3) for t in times])
 
@@ -174,6 +182,7 @@ def main():
     dom = max(kernels, key=lambda n: kernels[n]["us"])
     dk = kernels[dom]
     expert_us = kernels["gate_up"]["us"] + kernels["down"]["us"]
+    expert_fl = kernels["gate_up"]["work"] + kernels["down"]["work"]
     res = {
         "metric": METRIC,
         "value": round(T / (ms * 1e-3), 1),
@@ -193,7 +202,8 @@ def main():
         "roofline": {"kernel": dom, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
                      "unit": dk["unit"], "frac": dk["frac"], "traffic": None,
                      "work_per_launch": dk["work"]},
-        "mfma_frac_expert_gemms": round(fl["experts"] / (expert_us * 1e-6) / PEAK_BF16, 4),
+        # Routed + shared expert GEMM FLOPs over the two grouped launches that compute them.
+        "mfma_frac_expert_gemms": round(expert_fl / (expert_us * 1e-6) / PEAK_BF16, 4),
         "mfma_frac_block": round(fl["block"] / (ms * 1e-3) / PEAK_BF16, 4),
         "kernels": kernels,
     }

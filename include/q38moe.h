@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define Q38MOE_ABI_VERSION 1
+#define Q38MOE_ABI_VERSION 2
 
 #define Q38MOE_OK 0
 #define Q38MOE_EINVAL (-1)   /* bad shape, null pointer, misalignment, unsupported dtype */
@@ -91,46 +91,54 @@ int q38moe_histogram(const void* topk_idx, int32_t idx_is_int64, int32_t* hist, 
  * block mapping of inference.py:39-50 / 174-183.
  *   counts[e] = #{p : ids[p] == e}; starts = exclusive prefix sum of counts;
  *   perm[starts[e] + r] = the r-th pair p (ascending p = t*k + j) routed to expert e
- *   (identical to torch.sort(ids, stable=True).indices).
- *   tiles[i] = {expert, first sorted row, valid rows, 0} for the i-th block_m-row tile of the
- *   grouped GEMMs (experts ascending; each expert padded to a multiple of block_m, never to a
- *   global capacity); entries past the last tile hold {-1, 0, 0, 0}. tiles must hold
- *   q38moe_max_tiles(T, E, k, block_m) entries of int32[4].
- * hist comes from q38moe_route or q38moe_histogram.
+ *   (identical to torch.sort(ids, stable=True).indices); inv[perm[r]] = r (NULL to skip).
+ *   tiles[i] = {group, first row, valid rows, 0}: the row tiles of the grouped GEMMs, each expert
+ *   padded to a multiple of q38moe_gemm_block_m() rows (never to a global capacity), experts
+ *   ascending; then, when shared_rows > 0, the shared-expert rows [T*k, T*k + shared_rows) as
+ *   group E; then unused entries {-1, 0, 0, 0}. *tile_count = number of used entries.
+ *   tiles must hold q38moe_max_tiles(T, E, k, shared_rows) entries of int32[4].
+ * hist comes from q38moe_route or q38moe_histogram of the same indices.
  */
 int q38moe_permute(const void* topk_idx, int32_t idx_is_int64, const int32_t* hist,
-                   int32_t* counts, int32_t* starts, int32_t* perm, int32_t* tiles,
-                   int32_t block_m, int64_t T, int32_t E, int32_t k, void* stream);
+                   int32_t* counts, int32_t* starts, int32_t* perm, int32_t* inv, int32_t* tiles,
+                   int32_t* tile_count, int64_t shared_rows, int64_t T, int32_t E, int32_t k,
+                   void* stream);
 
-/* Upper bound on grouped-GEMM tiles: ceil(T*k / block_m) + E (inference.py:179). */
-int64_t q38moe_max_tiles(int64_t T, int32_t E, int32_t k, int32_t block_m);
+/* Entries of the tile table: ceil(T*k / BM) + E + ceil(shared_rows / BM) (cf. the grid bound of
+ * inference.py:179), BM = q38moe_gemm_block_m(). */
+int64_t q38moe_max_tiles(int64_t T, int32_t E, int32_t k, int64_t shared_rows);
 
-/* Tile height (rows) the grouped GEMM kernels of this build expect in `tiles`. */
+/* Rows per grouped-GEMM tile of this build. */
 int32_t q38moe_gemm_block_m(void);
 
 /*
- * Grouped gate/up GEMM with fused SwiGLU, R5-R6: replaces _gate_up_kernel (inference.py:60-96).
- * For sorted row r of expert e (token = perm[r] / k):
+ * Grouped gate/up GEMM with fused SwiGLU, R5-R6 (+R9 first half): replaces _gate_up_kernel
+ * (inference.py:60-96). Row r of a routed tile (expert e, token = perm[r] / k):
  *   g = bf16(x[token] . w_gate_up[e, n, :]), u = bf16(x[token] . w_gate_up[e, I+n, :]),
  *   H[r, n] = bf16(bf16(silu(g)) * u).
- * w_gate_up [E, 2I, h] bf16 (the experts.gate_up_proj parameter). H [T*k, I] bf16, sorted order.
+ * Rows r >= T*k of shared tiles (group E) compute the same with token r - T*k and the shared
+ * expert's gate_proj / up_proj weights (w_sh_gate, w_sh_up [I,h]; needed iff shared_rows > 0,
+ * which also requires Is == I).
+ * w_gate_up [E, 2I, h] bf16 (experts.gate_up_proj). H [T*k + shared_rows, I] bf16.
  */
-int q38moe_gate_up(const void* x, const void* w_gate_up, const int32_t* perm,
-                   const int32_t* tiles, void* H, int64_t T, int32_t h, int32_t E, int32_t k,
-                   int32_t I, int32_t dtype, void* stream);
+int q38moe_gate_up(const void* x, const void* w_gate_up, const void* w_sh_gate,
+                   const void* w_sh_up, const int32_t* perm, const int32_t* tiles,
+                   const int32_t* tile_count, int64_t shared_rows, void* H, int64_t T, int32_t h,
+                   int32_t E, int32_t k, int32_t I, int32_t dtype, void* stream);
 
 /*
- * Grouped down GEMM with the routing-weight epilogue, R7: replaces _down_kernel
- * (inference.py:99-130). For sorted row r of expert e, pair p = perm[r]:
- *   y[p, c] = bf16(bf16(H[r] . w_down[e, c, :]) * topk_w[p]).
- * w_down [E, h, I] bf16 (experts.down_proj). y [T*k, h] bf16 in pair order.
+ * Grouped down GEMM, R7 without its routing-weight factor (applied by q38moe_combine with the
+ * same rounding): replaces _down_kernel (inference.py:99-130).
+ *   Y[r, c] = bf16(H[r] . w_down[e, c, :]) for routed rows (expert e of the row's tile), and with
+ *   w_sh_down [h, I] (shared_expert.down_proj) for shared rows. Y [T*k + shared_rows, h] bf16,
+ *   expert-sorted row order.
  */
-int q38moe_down(const void* H, const void* w_down, const int32_t* perm, const int32_t* tiles,
-                const void* topk_w, void* y, int64_t T, int32_t h, int32_t E, int32_t k,
-                int32_t I, int32_t dtype, void* stream);
+int q38moe_down(const void* H, const void* w_down, const void* w_sh_down, const int32_t* tiles,
+                const int32_t* tile_count, int64_t shared_rows, void* Y, int64_t T, int32_t h,
+                int32_t E, int32_t k, int32_t I, int32_t dtype, void* stream);
 
 /*
- * Shared expert, R9 (Qwen3_8MoeMLP.forward, modeling:751-753):
+ * Shared expert alone, R9 (Qwen3_8MoeMLP.forward, modeling:751-753):
  *   out[t] = bf16(bf16(bf16(silu(bf16(x.Wg^T))) * bf16(x.Wu^T)) . Wd^T).
  * w_gate [Is,h], w_up [Is,h], w_down [h,Is] bf16; Hs workspace [T,Is] bf16; out [T,h] bf16.
  */
@@ -139,22 +147,26 @@ int q38moe_shared_expert(const void* x, const void* w_gate, const void* w_up,
                          int32_t Is, int32_t dtype, void* stream);
 
 /*
- * Combine, R8 (+ the block tail of modeling:831-833):
- *   routed[t] = bf16(sum_j fp32(y[t*k+j]))                                    (inference.py:199)
- *   shared_out == NULL: out = routed.
+ * Combine, R7 weight + R8 (+ the block tail of modeling:831-833), for pairs p = t*k + j:
+ *   y_p = bf16(Y[inv[p]] * topk_w[p])                                          (inference.py:128-130)
+ *   routed[t] = bf16(sum_j fp32(y_p))                                          (inference.py:199)
+ *   shared_out == NULL: out = routed;
  *   otherwise:          out = bf16(routed + bf16(bf16(sigmoid(gate_logit[t])) * shared_out[t])).
  * topk_idx (NULL = all pairs valid; int32 or int64 per idx_is_int64): pairs whose index lies
- * outside [0,E) contribute nothing.
+ * outside [0,E) contribute nothing. shared_out may point into Y (rows T*k..) when the shared
+ * expert ran inside the grouped GEMMs.
  */
-int q38moe_combine(const void* y, const void* topk_idx, int32_t idx_is_int64,
-                   const void* shared_out, const void* shared_gate_logit, void* out, int64_t T,
-                   int32_t h, int32_t E, int32_t k, int32_t dtype, void* stream);
+int q38moe_combine(const void* Y, const int32_t* inv, const void* topk_idx, int32_t idx_is_int64,
+                   const void* topk_w, const void* shared_out, const void* shared_gate_logit,
+                   void* out, int64_t T, int32_t h, int32_t E, int32_t k, int32_t dtype,
+                   void* stream);
 
 /*
  * Routed experts, R3-R8: the ExpertsInterface contract
  *   fn(self, hidden_states[T,h], top_k_index[T,k], top_k_weights[T,k]) -> [T,h]
  * (transformers integrations/moe.py:567-570; implementations inference.py:158-199 and
- * modeling:769-793). Runs histogram, permute, gate/up, down and combine.
+ * modeling:769-793). Runs histogram, permute, gate/up, down and combine. Requires
+ * T*h < 2^31.
  */
 int q38moe_experts_workspace_bytes(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
                                    size_t* bytes);
@@ -171,6 +183,7 @@ int q38moe_experts_forward(const void* x, const void* topk_idx, int32_t idx_is_i
  *   logit_bias [E] fp32 or NULL. out [T,h] bf16.
  *   Optional router outputs (NULL to skip): logits [T,E] bf16, topk_idx [T,k] int32,
  *   topk_w [T,k] bf16.
+ * With Is == I the shared expert runs inside the routed grouped GEMM launches.
  */
 int q38moe_block_workspace_bytes(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
                                  int32_t Is, size_t* bytes);

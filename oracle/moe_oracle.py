@@ -115,9 +115,10 @@ def router(x, w_router, k, logit_bias=None, logits=None):
     return logits, probs, torch.from_numpy(idx), bf16(vals)
 
 
-def experts_grouped(x, idx, w, w_gate_up, w_down):
+def experts_grouped(x, idx, w, w_gate_up, w_down, return_sorted=False):
     """Routed experts, rounding of inference:60-130 and the k-sum of inference:199. Also returns
-    the per-pair rows y [T*k,h] bf16 and H [T*k,I] bf16 in sorted order."""
+    the weighted per-pair rows y [T*k,h] bf16 (pair order) and H [T*k,I] bf16 (sorted order);
+    with return_sorted, also Y_raw = bf16(H . Wd^T) [T*k,h] in sorted order."""
     T, h = x.shape
     k = idx.shape[1]
     E, twoI, _ = w_gate_up.shape
@@ -127,6 +128,7 @@ def experts_grouped(x, idx, w, w_gate_up, w_down):
     wflat = _f(w.reshape(-1))
     y = torch.zeros(T * k, h, dtype=torch.bfloat16)
     H = torch.zeros(perm.size, I, dtype=torch.bfloat16)
+    Y_raw = torch.zeros(perm.size, h, dtype=torch.bfloat16)
     xf = _f(x)
     for e in range(E):
         c, s = int(counts[e]), int(starts[e])
@@ -140,9 +142,12 @@ def experts_grouped(x, idx, w, w_gate_up, w_down):
         act = _f(bf16(F.silu(g)))
         He = bf16(act * u)
         H[s:s + c] = He
-        d = _f(bf16(_f(He) @ _f(w_down[e]).T))
-        y[rows] = bf16(d * wflat[rows][:, None])
+        d = bf16(_f(He) @ _f(w_down[e]).T)
+        Y_raw[s:s + c] = d
+        y[rows] = bf16(_f(d) * wflat[rows][:, None])
     out = bf16(_f(y).view(T, k, h).sum(dim=1))
+    if return_sorted:
+        return out, y, H, Y_raw
     return out, y, H
 
 

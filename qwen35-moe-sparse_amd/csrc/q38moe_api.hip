@@ -71,45 +71,54 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 int64_t hist_blocks(int64_t T) { return (T + 63) / 64; }
 
-int64_t max_tiles_impl(int64_t T, int32_t E, int32_t k, int32_t bm) {
-  return (T * k + bm - 1) / bm + E;
+int64_t max_tiles_impl(int64_t T, int32_t E, int32_t k, int64_t shared_rows) {
+  const int64_t bm = q38::gemm_block_m();
+  return (T * k + bm - 1) / bm + E + (shared_rows + bm - 1) / bm;
 }
 
-// Workspace of the routed-experts pipeline.
+// Workspace of the routed-experts pipeline. With shared_rows > 0 the shared expert's rows are
+// appended to H and Y (rows T*k ..) and its tiles to the tile table.
 struct ExpertsWs {
-  size_t hist, counts, starts, perm, tiles, H, y, end;
+  size_t hist, counts, starts, perm, inv, tiles, tile_count, H, Y, end;
+  int64_t max_tiles;
 };
 
-ExpertsWs experts_layout(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I) {
+ExpertsWs experts_layout(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int64_t shared_rows) {
   ExpertsWs w;
   const int64_t P = T * k;
+  const int64_t rows = P + shared_rows;
+  w.max_tiles = max_tiles_impl(T, E, k, shared_rows);
   size_t off = 0;
   w.hist = off; off = align_up(off + sizeof(int32_t) * hist_blocks(T) * E);
   w.counts = off; off = align_up(off + sizeof(int32_t) * E);
   w.starts = off; off = align_up(off + sizeof(int32_t) * E);
   w.perm = off; off = align_up(off + sizeof(int32_t) * P);
-  w.tiles = off; off = align_up(off + 4 * sizeof(int32_t) * max_tiles_impl(T, E, k, q38::gemm_block_m()));
-  w.H = off; off = align_up(off + 2 * (size_t)P * I);
-  w.y = off; off = align_up(off + 2 * (size_t)P * h);
+  w.inv = off; off = align_up(off + sizeof(int32_t) * P);
+  w.tiles = off; off = align_up(off + 4 * sizeof(int32_t) * w.max_tiles);
+  w.tile_count = off; off = align_up(off + sizeof(int32_t));
+  w.H = off; off = align_up(off + 2 * (size_t)rows * I);
+  w.Y = off; off = align_up(off + 2 * (size_t)rows * h);
   w.end = off;
   return w;
 }
 
 struct BlockWs {
   ExpertsWs ex;
+  bool fused;  // shared expert inside the grouped GEMMs (Is == I)
   size_t idx, w, gate, Hs, sh, end;
 };
 
 BlockWs block_layout(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int32_t Is) {
   BlockWs b;
-  b.ex = experts_layout(T, h, E, k, I);
+  b.fused = Is == I;
+  b.ex = experts_layout(T, h, E, k, I, b.fused ? T : 0);
   size_t off = b.ex.end;
   const int64_t P = T * k;
   b.idx = off; off = align_up(off + sizeof(int32_t) * P);
   b.w = off; off = align_up(off + 2 * (size_t)P);
   b.gate = off; off = align_up(off + 2 * (size_t)T);
-  b.Hs = off; off = align_up(off + 2 * (size_t)T * Is);
-  b.sh = off; off = align_up(off + 2 * (size_t)T * h);
+  b.Hs = off; off = align_up(off + (b.fused ? 0 : 2 * (size_t)T * Is));
+  b.sh = off; off = align_up(off + (b.fused ? 0 : 2 * (size_t)T * h));
   b.end = off;
   return b;
 }
@@ -119,37 +128,48 @@ P* at(void* base, size_t off) {
   return reinterpret_cast<P*>(static_cast<char*>(base) + off);
 }
 
-// Routed experts from routing indices/weights already in device memory.
+int check_rows(int64_t T, int32_t h, int32_t k) {
+  if ((T * k + T) * (int64_t)h >= (int64_t)1 << 31)
+    return fail(Q38MOE_EINVAL, "(T*k + T) * h must be < 2^31 (got T=%lld, h=%d)", (long long)T, h);
+  return Q38MOE_OK;
+}
+
+// Routed experts (+ the shared expert when sh_* weights are given and fused) from routing
+// indices/weights in device memory: permute, gate/up, down, combine.
 int run_experts(const void* x, const void* idx, bool idx64, const uint16_t* topk_w,
-                const void* w_gate_up, const void* w_down, const uint16_t* shared,
+                const void* w_gate_up, const void* w_down, const uint16_t* sh_gate,
+                const uint16_t* sh_up, const uint16_t* sh_down, const uint16_t* shared_out,
                 const uint16_t* gate, void* out, int64_t T, int32_t h, int32_t E, int32_t k,
-                int32_t I, const int32_t* hist_ready, void* ws, const ExpertsWs& L,
-                hipStream_t st) {
+                int32_t I, int64_t shared_rows, const int32_t* hist_ready, void* ws,
+                const ExpertsWs& L, hipStream_t st) {
   const int bm = q38::gemm_block_m();
-  const int64_t mt = max_tiles_impl(T, E, k, bm);
   int32_t* hist = at<int32_t>(ws, L.hist);
   int32_t* counts = at<int32_t>(ws, L.counts);
   int32_t* starts = at<int32_t>(ws, L.starts);
   int32_t* perm = at<int32_t>(ws, L.perm);
+  int32_t* inv = at<int32_t>(ws, L.inv);
   int4* tiles = at<int4>(ws, L.tiles);
+  int32_t* tile_count = at<int32_t>(ws, L.tile_count);
   uint16_t* H = at<uint16_t>(ws, L.H);
-  uint16_t* y = at<uint16_t>(ws, L.y);
+  uint16_t* Y = at<uint16_t>(ws, L.Y);
+  const int64_t P = T * k;
   if (hist_ready == nullptr) {
     Q38_HIP(q38::launch_histogram(idx, idx64, hist, T, E, k, st), "histogram launch");
     hist_ready = hist;
   }
-  Q38_HIP(q38::launch_permute(idx, idx64, hist_ready, counts, starts, perm, tiles, bm, (int)mt, T,
-                              E, k, st),
+  Q38_HIP(q38::launch_permute(idx, idx64, hist_ready, counts, starts, perm, inv, tiles, tile_count,
+                              bm, (int)L.max_tiles, (int)shared_rows, T, E, k, st),
           "permute launch");
-  const uint16_t* wgu = static_cast<const uint16_t*>(w_gate_up);
-  Q38_HIP(q38::launch_gate_up(static_cast<const uint16_t*>(x), perm, tiles, (int)mt, wgu,
-                              wgu + (int64_t)I * h, (int64_t)2 * I * h, H, T * k, I, h, k, st),
+  Q38_HIP(q38::launch_gate_up(static_cast<const uint16_t*>(x), perm, tiles, tile_count,
+                              (int)L.max_tiles, 0, (int)P, static_cast<const uint16_t*>(w_gate_up),
+                              sh_gate, sh_up, H, I, h, E, k, st),
           "gate_up launch");
-  Q38_HIP(q38::launch_down(H, perm, tiles, (int)mt, static_cast<const uint16_t*>(w_down),
-                           (int64_t)h * I, topk_w, y, T * k, h, I, st),
+  Q38_HIP(q38::launch_down(H, tiles, tile_count, (int)L.max_tiles, 0,
+                           static_cast<const uint16_t*>(w_down), sh_down, Y, h, I, E, st),
           "down launch");
-  Q38_HIP(q38::launch_combine(y, idx, idx64, shared, gate, static_cast<uint16_t*>(out), T, h, E,
-                              k, st),
+  const uint16_t* shared = shared_out != nullptr ? shared_out : (shared_rows > 0 ? Y + P * h : nullptr);
+  Q38_HIP(q38::launch_combine(Y, inv, idx, idx64, topk_w, shared, gate, static_cast<uint16_t*>(out),
+                              T, h, E, k, st),
           "combine launch");
   return Q38MOE_OK;
 }
@@ -162,9 +182,9 @@ int q38moe_abi_version(void) { return Q38MOE_ABI_VERSION; }
 
 const char* q38moe_last_error(void) { return g_err; }
 
-int64_t q38moe_max_tiles(int64_t T, int32_t E, int32_t k, int32_t block_m) {
-  if (T < 0 || E < 1 || k < 1 || block_m < 1) return -1;
-  return max_tiles_impl(T, E, k, block_m);
+int64_t q38moe_max_tiles(int64_t T, int32_t E, int32_t k, int64_t shared_rows) {
+  if (T < 0 || E < 1 || k < 1 || shared_rows < 0) return -1;
+  return max_tiles_impl(T, E, k, shared_rows);
 }
 
 int32_t q38moe_gemm_block_m(void) { return q38::gemm_block_m(); }
@@ -225,72 +245,78 @@ int q38moe_histogram(const void* topk_idx, int32_t idx_is_int64, int32_t* hist, 
 }
 
 int q38moe_permute(const void* topk_idx, int32_t idx_is_int64, const int32_t* hist,
-                   int32_t* counts, int32_t* starts, int32_t* perm, int32_t* tiles,
-                   int32_t block_m, int64_t T, int32_t E, int32_t k, void* stream) {
+                   int32_t* counts, int32_t* starts, int32_t* perm, int32_t* inv, int32_t* tiles,
+                   int32_t* tile_count, int64_t shared_rows, int64_t T, int32_t E, int32_t k,
+                   void* stream) {
   g_err[0] = 0;
   Q38_CHECK(check_routing(T, E, k));
-  if (counts == nullptr || starts == nullptr)
-    return fail(Q38MOE_EINVAL, "counts and starts must not be NULL");
+  if (shared_rows < 0 || shared_rows > (int64_t)1 << 30) return fail(Q38MOE_EINVAL, "bad shared_rows");
+  if (counts == nullptr || starts == nullptr) return fail(Q38MOE_EINVAL, "counts and starts must not be NULL");
   if (T > 0 && (topk_idx == nullptr || hist == nullptr || perm == nullptr))
     return fail(Q38MOE_EINVAL, "topk_idx, hist and perm must not be NULL");
-  if (tiles != nullptr && (block_m < 1 || block_m > 4096))
-    return fail(Q38MOE_EINVAL, "block_m must be in [1, 4096] (got %d)", block_m);
   if (tiles != nullptr && !aligned16(tiles)) return fail(Q38MOE_EINVAL, "tiles must be 16-byte aligned");
   (void)hipGetLastError();
-  const int64_t mt = tiles != nullptr ? max_tiles_impl(T, E, k, block_m) : 0;
-  Q38_HIP(q38::launch_permute(topk_idx, idx_is_int64 != 0, hist, counts, starts, perm,
-                              reinterpret_cast<int4*>(tiles), tiles != nullptr ? block_m : 1,
-                              (int)mt, T, E, k, static_cast<hipStream_t>(stream)),
+  const int64_t mt = tiles != nullptr ? max_tiles_impl(T, E, k, shared_rows) : 0;
+  Q38_HIP(q38::launch_permute(topk_idx, idx_is_int64 != 0, hist, counts, starts, perm, inv,
+                              reinterpret_cast<int4*>(tiles), tile_count, q38::gemm_block_m(), (int)mt,
+                              (int)shared_rows, T, E, k, static_cast<hipStream_t>(stream)),
           "permute launch");
   return Q38MOE_OK;
 }
 
-int q38moe_gate_up(const void* x, const void* w_gate_up, const int32_t* perm,
-                   const int32_t* tiles, void* H, int64_t T, int32_t h, int32_t E, int32_t k,
-                   int32_t I, int32_t dtype, void* stream) {
+int q38moe_gate_up(const void* x, const void* w_gate_up, const void* w_sh_gate,
+                   const void* w_sh_up, const int32_t* perm, const int32_t* tiles,
+                   const int32_t* tile_count, int64_t shared_rows, void* H, int64_t T, int32_t h,
+                   int32_t E, int32_t k, int32_t I, int32_t dtype, void* stream) {
   g_err[0] = 0;
   Q38_CHECK(check_dtype(dtype));
   Q38_CHECK(check_routing(T, E, k));
   Q38_CHECK(check_dim(h, "h"));
   Q38_CHECK(check_dim(I, "I"));
   if (T == 0) return Q38MOE_OK;
+  Q38_CHECK(check_rows(T, h, k));
   Q38_CHECK(check_ptr(x, "x"));
   Q38_CHECK(check_ptr(w_gate_up, "w_gate_up"));
   Q38_CHECK(check_ptr(H, "H"));
   Q38_CHECK(check_ptr(tiles, "tiles"));
-  if (perm == nullptr) return fail(Q38MOE_EINVAL, "perm must not be NULL");
+  if (perm == nullptr || tile_count == nullptr) return fail(Q38MOE_EINVAL, "perm and tile_count must not be NULL");
+  if (shared_rows < 0 || shared_rows > T) return fail(Q38MOE_EINVAL, "shared_rows must be in [0, T]");
+  if (shared_rows > 0) {
+    Q38_CHECK(check_ptr(w_sh_gate, "w_sh_gate"));
+    Q38_CHECK(check_ptr(w_sh_up, "w_sh_up"));
+  }
   (void)hipGetLastError();
-  const int64_t mt = max_tiles_impl(T, E, k, q38::gemm_block_m());
-  const uint16_t* w = static_cast<const uint16_t*>(w_gate_up);
-  Q38_HIP(q38::launch_gate_up(static_cast<const uint16_t*>(x), perm,
-                              reinterpret_cast<const int4*>(tiles), (int)mt, w, w + (int64_t)I * h,
-                              (int64_t)2 * I * h, static_cast<uint16_t*>(H), T * k, I, h, k,
+  Q38_HIP(q38::launch_gate_up(static_cast<const uint16_t*>(x), perm, reinterpret_cast<const int4*>(tiles),
+                              tile_count, (int)max_tiles_impl(T, E, k, shared_rows), 0, (int)(T * k),
+                              static_cast<const uint16_t*>(w_gate_up), static_cast<const uint16_t*>(w_sh_gate),
+                              static_cast<const uint16_t*>(w_sh_up), static_cast<uint16_t*>(H), I, h, E, k,
                               static_cast<hipStream_t>(stream)),
           "gate_up launch");
   return Q38MOE_OK;
 }
 
-int q38moe_down(const void* H, const void* w_down, const int32_t* perm, const int32_t* tiles,
-                const void* topk_w, void* y, int64_t T, int32_t h, int32_t E, int32_t k,
-                int32_t I, int32_t dtype, void* stream) {
+int q38moe_down(const void* H, const void* w_down, const void* w_sh_down, const int32_t* tiles,
+                const int32_t* tile_count, int64_t shared_rows, void* Y, int64_t T, int32_t h,
+                int32_t E, int32_t k, int32_t I, int32_t dtype, void* stream) {
   g_err[0] = 0;
   Q38_CHECK(check_dtype(dtype));
   Q38_CHECK(check_routing(T, E, k));
   Q38_CHECK(check_dim(h, "h"));
   Q38_CHECK(check_dim(I, "I"));
   if (T == 0) return Q38MOE_OK;
+  Q38_CHECK(check_rows(T, h, k));
   Q38_CHECK(check_ptr(H, "H"));
   Q38_CHECK(check_ptr(w_down, "w_down"));
-  Q38_CHECK(check_ptr(y, "y"));
+  Q38_CHECK(check_ptr(Y, "Y"));
   Q38_CHECK(check_ptr(tiles, "tiles"));
-  if (perm == nullptr || topk_w == nullptr) return fail(Q38MOE_EINVAL, "perm and topk_w must not be NULL");
+  if (tile_count == nullptr) return fail(Q38MOE_EINVAL, "tile_count must not be NULL");
+  if (shared_rows < 0 || shared_rows > T) return fail(Q38MOE_EINVAL, "shared_rows must be in [0, T]");
+  if (shared_rows > 0) Q38_CHECK(check_ptr(w_sh_down, "w_sh_down"));
   (void)hipGetLastError();
-  const int64_t mt = max_tiles_impl(T, E, k, q38::gemm_block_m());
-  Q38_HIP(q38::launch_down(static_cast<const uint16_t*>(H), perm,
-                           reinterpret_cast<const int4*>(tiles), (int)mt,
-                           static_cast<const uint16_t*>(w_down), (int64_t)h * I,
-                           static_cast<const uint16_t*>(topk_w), static_cast<uint16_t*>(y), T * k,
-                           h, I, static_cast<hipStream_t>(stream)),
+  Q38_HIP(q38::launch_down(static_cast<const uint16_t*>(H), reinterpret_cast<const int4*>(tiles), tile_count,
+                           (int)max_tiles_impl(T, E, k, shared_rows), 0, static_cast<const uint16_t*>(w_down),
+                           static_cast<const uint16_t*>(w_sh_down), static_cast<uint16_t*>(Y), h, I, E,
+                           static_cast<hipStream_t>(stream)),
           "down launch");
   return Q38MOE_OK;
 }
@@ -304,6 +330,7 @@ int q38moe_shared_expert(const void* x, const void* w_gate, const void* w_up,
   Q38_CHECK(check_dim(h, "h"));
   Q38_CHECK(check_dim(Is, "Is"));
   if (T == 0) return Q38MOE_OK;
+  Q38_CHECK(check_rows(T, h, 0));
   Q38_CHECK(check_ptr(x, "x"));
   Q38_CHECK(check_ptr(w_gate, "w_gate"));
   Q38_CHECK(check_ptr(w_up, "w_up"));
@@ -312,36 +339,37 @@ int q38moe_shared_expert(const void* x, const void* w_gate, const void* w_up,
   Q38_CHECK(check_ptr(out, "out"));
   (void)hipGetLastError();
   hipStream_t st = static_cast<hipStream_t>(stream);
-  Q38_HIP(q38::launch_gate_up(static_cast<const uint16_t*>(x), nullptr, nullptr, 0,
+  Q38_HIP(q38::launch_gate_up(static_cast<const uint16_t*>(x), nullptr, nullptr, nullptr, 0, T, 0, nullptr,
                               static_cast<const uint16_t*>(w_gate), static_cast<const uint16_t*>(w_up),
-                              0, static_cast<uint16_t*>(Hs), T, Is, h, 1, st),
+                              static_cast<uint16_t*>(Hs), Is, h, 0, 1, st),
           "shared gate_up launch");
-  Q38_HIP(q38::launch_down(static_cast<const uint16_t*>(Hs), nullptr, nullptr, 0,
-                           static_cast<const uint16_t*>(w_down), 0, nullptr,
-                           static_cast<uint16_t*>(out), T, h, Is, st),
+  Q38_HIP(q38::launch_down(static_cast<const uint16_t*>(Hs), nullptr, nullptr, 0, T, nullptr,
+                           static_cast<const uint16_t*>(w_down), static_cast<uint16_t*>(out), h, Is, 0, st),
           "shared down launch");
   return Q38MOE_OK;
 }
 
-int q38moe_combine(const void* y, const void* topk_idx, int32_t idx_is_int64,
-                   const void* shared_out, const void* shared_gate_logit, void* out, int64_t T,
-                   int32_t h, int32_t E, int32_t k, int32_t dtype, void* stream) {
+int q38moe_combine(const void* Y, const int32_t* inv, const void* topk_idx, int32_t idx_is_int64,
+                   const void* topk_w, const void* shared_out, const void* shared_gate_logit,
+                   void* out, int64_t T, int32_t h, int32_t E, int32_t k, int32_t dtype,
+                   void* stream) {
   g_err[0] = 0;
   Q38_CHECK(check_dtype(dtype));
   Q38_CHECK(check_routing(T, E, k));
   Q38_CHECK(check_dim(h, "h"));
   if (T == 0) return Q38MOE_OK;
-  Q38_CHECK(check_ptr(y, "y"));
+  Q38_CHECK(check_rows(T, h, k));
+  Q38_CHECK(check_ptr(Y, "Y"));
   Q38_CHECK(check_ptr(out, "out"));
   Q38_CHECK(check_opt_ptr(shared_out, "shared_out"));
+  if (inv == nullptr || topk_w == nullptr) return fail(Q38MOE_EINVAL, "inv and topk_w must not be NULL");
   if (shared_out != nullptr && shared_gate_logit == nullptr)
     return fail(Q38MOE_EINVAL, "shared_out requires shared_gate_logit");
   (void)hipGetLastError();
-  Q38_HIP(q38::launch_combine(static_cast<const uint16_t*>(y), topk_idx, idx_is_int64 != 0,
-                              static_cast<const uint16_t*>(shared_out),
-                              static_cast<const uint16_t*>(shared_gate_logit),
-                              static_cast<uint16_t*>(out), T, h, E, k,
-                              static_cast<hipStream_t>(stream)),
+  Q38_HIP(q38::launch_combine(static_cast<const uint16_t*>(Y), inv, topk_idx, idx_is_int64 != 0,
+                              static_cast<const uint16_t*>(topk_w), static_cast<const uint16_t*>(shared_out),
+                              static_cast<const uint16_t*>(shared_gate_logit), static_cast<uint16_t*>(out), T, h,
+                              E, k, static_cast<hipStream_t>(stream)),
           "combine launch");
   return Q38MOE_OK;
 }
@@ -353,7 +381,7 @@ int q38moe_experts_workspace_bytes(int64_t T, int32_t h, int32_t E, int32_t k, i
   Q38_CHECK(check_dim(h, "h"));
   Q38_CHECK(check_dim(I, "I"));
   if (bytes == nullptr) return fail(Q38MOE_EINVAL, "bytes must not be NULL");
-  *bytes = experts_layout(T, h, E, k, I).end;
+  *bytes = experts_layout(T, h, E, k, I, 0).end;
   return Q38MOE_OK;
 }
 
@@ -367,19 +395,20 @@ int q38moe_experts_forward(const void* x, const void* topk_idx, int32_t idx_is_i
   Q38_CHECK(check_dim(h, "h"));
   Q38_CHECK(check_dim(I, "I"));
   if (T == 0) return Q38MOE_OK;
+  Q38_CHECK(check_rows(T, h, k));
   Q38_CHECK(check_ptr(x, "x"));
   Q38_CHECK(check_ptr(w_gate_up, "w_gate_up"));
   Q38_CHECK(check_ptr(w_down, "w_down"));
   Q38_CHECK(check_ptr(out, "out"));
   if (topk_idx == nullptr || topk_w == nullptr) return fail(Q38MOE_EINVAL, "topk_idx and topk_w must not be NULL");
-  const ExpertsWs L = experts_layout(T, h, E, k, I);
+  const ExpertsWs L = experts_layout(T, h, E, k, I, 0);
   if (workspace == nullptr || workspace_bytes < L.end)
     return fail(Q38MOE_EWORKSPACE, "workspace needs %zu bytes (got %zu)", L.end, workspace_bytes);
   if (reinterpret_cast<uintptr_t>(workspace) % kAlign != 0)
     return fail(Q38MOE_EINVAL, "workspace must be 256-byte aligned");
   (void)hipGetLastError();
-  return run_experts(x, topk_idx, idx_is_int64 != 0, static_cast<const uint16_t*>(topk_w),
-                     w_gate_up, w_down, nullptr, nullptr, out, T, h, E, k, I, nullptr, workspace, L,
+  return run_experts(x, topk_idx, idx_is_int64 != 0, static_cast<const uint16_t*>(topk_w), w_gate_up, w_down,
+                     nullptr, nullptr, nullptr, nullptr, nullptr, out, T, h, E, k, I, 0, nullptr, workspace, L,
                      static_cast<hipStream_t>(stream));
 }
 
@@ -409,6 +438,7 @@ int q38moe_block_forward(const void* x, const void* w_router, const void* w_gate
   Q38_CHECK(check_dim(I, "I"));
   Q38_CHECK(check_dim(Is, "Is"));
   if (T == 0) return Q38MOE_OK;
+  Q38_CHECK(check_rows(T, h, k));
   Q38_CHECK(check_ptr(x, "x"));
   Q38_CHECK(check_ptr(w_router, "w_router"));
   Q38_CHECK(check_ptr(w_gate_up, "w_gate_up"));
@@ -428,25 +458,32 @@ int q38moe_block_forward(const void* x, const void* w_router, const void* w_gate
   int32_t* idx = topk_idx != nullptr ? topk_idx : at<int32_t>(workspace, L.idx);
   uint16_t* w = topk_w != nullptr ? static_cast<uint16_t*>(topk_w) : at<uint16_t>(workspace, L.w);
   uint16_t* gate = at<uint16_t>(workspace, L.gate);
-  uint16_t* Hs = at<uint16_t>(workspace, L.Hs);
-  uint16_t* sh = at<uint16_t>(workspace, L.sh);
   int32_t* hist = at<int32_t>(workspace, L.ex.hist);
   const uint16_t* xb = static_cast<const uint16_t*>(x);
-  // Shared expert (modeling:827).
-  Q38_HIP(q38::launch_gate_up(xb, nullptr, nullptr, 0, static_cast<const uint16_t*>(w_sh_gate),
-                              static_cast<const uint16_t*>(w_sh_up), 0, Hs, T, Is, h, 1, st),
-          "shared gate_up launch");
-  Q38_HIP(q38::launch_down(Hs, nullptr, nullptr, 0, static_cast<const uint16_t*>(w_sh_down), 0,
-                           nullptr, sh, T, h, Is, st),
-          "shared down launch");
+  const uint16_t* sh_out = nullptr;
+  if (!L.fused) {
+    // Shared expert (modeling:827) as its own dense GEMMs when its width differs from I.
+    uint16_t* Hs = at<uint16_t>(workspace, L.Hs);
+    uint16_t* sh = at<uint16_t>(workspace, L.sh);
+    Q38_HIP(q38::launch_gate_up(xb, nullptr, nullptr, nullptr, 0, T, 0, nullptr,
+                                static_cast<const uint16_t*>(w_sh_gate), static_cast<const uint16_t*>(w_sh_up), Hs,
+                                Is, h, E, 1, st),
+            "shared gate_up launch");
+    Q38_HIP(q38::launch_down(Hs, nullptr, nullptr, 0, T, nullptr, static_cast<const uint16_t*>(w_sh_down), sh, h,
+                             Is, E, st),
+            "shared down launch");
+    sh_out = sh;
+  }
   // Router + shared gate logit + histogram (modeling:828, 831).
-  Q38_HIP(q38::launch_route(xb, static_cast<const uint16_t*>(w_router),
-                            static_cast<const uint16_t*>(w_sh_gate_proj), nullptr, logit_bias,
-                            static_cast<uint16_t*>(logits), idx, w, gate, hist, T, h, E, k, st),
+  Q38_HIP(q38::launch_route(xb, static_cast<const uint16_t*>(w_router), static_cast<const uint16_t*>(w_sh_gate_proj),
+                            nullptr, logit_bias, static_cast<uint16_t*>(logits), idx, w, gate, hist, T, h, E, k, st),
           "route launch");
-  // Routed experts and the gated sum (modeling:829, 831-833).
-  return run_experts(x, idx, false, w, w_gate_up, w_down, sh, gate, out, T, h, E, k, I, hist,
-                     workspace, L.ex, st);
+  // Routed experts (+ the shared expert inside the same GEMMs) and the gated sum (modeling:829-833).
+  return run_experts(x, idx, false, w, w_gate_up, w_down,
+                     L.fused ? static_cast<const uint16_t*>(w_sh_gate) : nullptr,
+                     L.fused ? static_cast<const uint16_t*>(w_sh_up) : nullptr,
+                     L.fused ? static_cast<const uint16_t*>(w_sh_down) : nullptr, sh_out, gate, out, T, h, E, k, I,
+                     L.fused ? T : 0, hist, workspace, L.ex, st);
 }
 
 }  // extern "C"

@@ -51,4 +51,14 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c)
 
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
 
+// Asynchronous 16-byte global -> LDS copy (gfx950 global_load_lds_dwordx4): lane l of the wave
+// writes LDS bytes [lds_wave_base + 16*l, +16). lds_wave_base must be wave-uniform. Completion is
+// tracked by vmcnt; wait with wait_vmcnt0() before a barrier that publishes the data.
+__device__ __forceinline__ void load_lds16(const void* gsrc, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)gsrc,
+                                   (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0); }
+
 }  // namespace q38

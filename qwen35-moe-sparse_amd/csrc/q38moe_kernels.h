@@ -14,21 +14,30 @@ hipError_t launch_histogram(const void* idx, bool idx64, int32_t* hist, int64_t 
                             hipStream_t stream);
 
 hipError_t launch_permute(const void* idx, bool idx64, const int32_t* hist, int32_t* counts,
-                          int32_t* starts, int32_t* perm, int4* tiles, int block_m,
-                          int max_tiles, int64_t T, int E, int k, hipStream_t stream);
+                          int32_t* starts, int32_t* perm, int32_t* inv, int4* tiles,
+                          int32_t* tile_count, int block_m, int max_tiles, int shared_rows,
+                          int64_t T, int E, int k, hipStream_t stream);
 
+// Rows per grouped-GEMM tile.
 int gemm_block_m();
 
-hipError_t launch_gate_up(const uint16_t* x, const int32_t* perm, const int4* tiles, int ntiles,
-                          const uint16_t* w_gate, const uint16_t* w_up, int64_t estride,
-                          uint16_t* H, int64_t M, int N, int K, int topk, hipStream_t stream);
-
-hipError_t launch_down(const uint16_t* H, const int32_t* perm, const int4* tiles, int ntiles,
-                       const uint16_t* w_down, int64_t estride, const uint16_t* rw, uint16_t* y,
-                       int64_t M, int N, int K, hipStream_t stream);
-
-hipError_t launch_combine(const uint16_t* y, const void* idx, bool idx64, const uint16_t* shared,
-                          const uint16_t* gate, uint16_t* out, int64_t T, int h, int E, int k,
+// Grouped gate/up + SwiGLU. tiles != nullptr: routed (+ shared, group E) tiles from permute, at
+// most max_mtiles, the used count in *ntiles_dev; rows [0, P) gather x via perm, rows >= P are
+// shared-expert tokens r - P. tiles == nullptr: dense shared expert over M_dense rows.
+hipError_t launch_gate_up(const uint16_t* x, const int32_t* perm, const int4* tiles,
+                          const int32_t* ntiles_dev, int max_mtiles, int64_t M_dense, int P,
+                          const uint16_t* w_gate_up, const uint16_t* ws_gate,
+                          const uint16_t* ws_up, uint16_t* H, int N, int K, int E, int topk,
                           hipStream_t stream);
+
+// Grouped down projection: Y[r] = bf16(H[r] . W^T) for the same tiles (or dense rows).
+hipError_t launch_down(const uint16_t* H, const int4* tiles, const int32_t* ntiles_dev,
+                       int max_mtiles, int64_t M_dense, const uint16_t* w_down,
+                       const uint16_t* ws_down, uint16_t* Y, int N, int K, int E,
+                       hipStream_t stream);
+
+hipError_t launch_combine(const uint16_t* Y, const int32_t* inv, const void* idx, bool idx64,
+                          const uint16_t* w, const uint16_t* shared, const uint16_t* gate,
+                          uint16_t* out, int64_t T, int h, int E, int k, hipStream_t stream);
 
 }  // namespace q38

@@ -1,5 +1,5 @@
 // Token->expert permutation (R3-R4): per-block histogram, expert prefix sums and a stable
-// counting-sort scatter, plus the padded tile table of the grouped GEMMs.
+// counting-sort scatter (perm and its inverse), plus the padded tile table of the grouped GEMMs.
 //
 // Reference semantics (q38/inference.py:163-171, 39-50, 174-183): perm is
 // torch.sort(ids, stable=True).indices over the flattened pair ids (pair p = t*k + j),
@@ -37,7 +37,8 @@ template <typename IdxT>
 __global__ __launch_bounds__(256) void permute_kernel(
     const IdxT* __restrict__ idx, const int32_t* __restrict__ hist, int64_t T, int E, int k,
     int nblk, int32_t* __restrict__ counts, int32_t* __restrict__ starts,
-    int32_t* __restrict__ perm, int4* __restrict__ tiles, int block_m, int max_tiles) {
+    int32_t* __restrict__ perm, int32_t* __restrict__ inv, int4* __restrict__ tiles,
+    int32_t* __restrict__ tile_count, int block_m, int max_tiles, int shared_rows) {
   __shared__ int s_tot[4][64];
   __shared__ int s_bef[4][64];
   __shared__ int s_base[64];
@@ -50,10 +51,23 @@ __global__ __launch_bounds__(256) void permute_kernel(
   const int tid = threadIdx.x, e = tid & 63, part = tid >> 6;
   const int b = blockIdx.x;
 
-  // Expert totals over all blocks and the counts of the blocks before this one.
+  // Expert totals over all blocks and the counts of the blocks before this one. Thread `tid`
+  // sums column e = tid & 63 over rows part, part + 4, ...; eight independent loads are in flight
+  // per step.
   int tot = 0, bef = 0;
   if (e < E) {
-    for (int bb = part; bb < nblk; bb += 4) {
+    int bb = part;
+    for (; bb + 28 < nblk; bb += 32) {
+      int c[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) c[u] = hist[(int64_t)(bb + 4 * u) * E + e];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        tot += c[u];
+        if (bb + 4 * u < b) bef += c[u];
+      }
+    }
+    for (; bb < nblk; bb += 4) {
       const int c = hist[(int64_t)bb * E + e];
       tot += c;
       if (bb < b) bef += c;
@@ -115,17 +129,28 @@ __global__ __launch_bounds__(256) void permute_kernel(
     const int64_t cap = T * k;
     for (int i = s0; i < s1; ++i) {
       if (s_ids[i] == e) {
-        if (off < cap) perm[off] = (int32_t)(p0 + i);
+        if (off < cap) {
+          perm[off] = (int32_t)(p0 + i);
+          if (inv != nullptr) inv[p0 + i] = off;
+        }
         ++off;
       }
     }
   }
 
   if (b == 0 && tiles != nullptr) {
-    const int total_tiles = s_tile0[63] + s_ntile[63];
+    // Routed tiles by expert, then the shared-expert rows [P, P + shared_rows) in block_m tiles
+    // (group id E), then unused entries {-1, 0, 0, 0}.
+    const int routed_tiles = s_tile0[63] + s_ntile[63];
+    const int shared_tiles = (shared_rows + block_m - 1) / block_m;
+    const int64_t P = T * k;
+    if (tid == 0 && tile_count != nullptr) *tile_count = routed_tiles + shared_tiles;
     for (int i = tid; i < max_tiles; i += 256) {
       int4 ti = make_int4(-1, 0, 0, 0);
-      if (i < total_tiles) {
+      if (i >= routed_tiles && i < routed_tiles + shared_tiles) {
+        const int s = i - routed_tiles;
+        ti = make_int4(E, (int)P + s * block_m, min(block_m, shared_rows - s * block_m), 0);
+      } else if (i < routed_tiles) {
         int lo = 0;
         // Largest expert whose first tile is <= i and that owns at least one tile.
         for (int ee = 0; ee < E; ++ee) {
@@ -154,19 +179,20 @@ hipError_t launch_histogram(const void* idx, bool idx64, int32_t* hist, int64_t 
 }
 
 hipError_t launch_permute(const void* idx, bool idx64, const int32_t* hist, int32_t* counts,
-                          int32_t* starts, int32_t* perm, int4* tiles, int block_m,
-                          int max_tiles, int64_t T, int E, int k, hipStream_t stream) {
+                          int32_t* starts, int32_t* perm, int32_t* inv, int4* tiles,
+                          int32_t* tile_count, int block_m, int max_tiles, int shared_rows,
+                          int64_t T, int E, int k, hipStream_t stream) {
   // At least one block, so T == 0 still writes zero counts and an empty tile table.
   const int64_t nblk = (T + PERM_TOKENS - 1) / PERM_TOKENS;
   const unsigned grid = (unsigned)(nblk > 0 ? nblk : 1);
   if (idx64)
     hipLaunchKernelGGL(permute_kernel<int64_t>, dim3(grid), dim3(256), 0, stream,
-                       (const int64_t*)idx, hist, T, E, k, (int)nblk, counts, starts, perm, tiles,
-                       block_m, max_tiles);
+                       (const int64_t*)idx, hist, T, E, k, (int)nblk, counts, starts, perm, inv,
+                       tiles, tile_count, block_m, max_tiles, shared_rows);
   else
     hipLaunchKernelGGL(permute_kernel<int32_t>, dim3(grid), dim3(256), 0, stream,
-                       (const int32_t*)idx, hist, T, E, k, (int)nblk, counts, starts, perm, tiles,
-                       block_m, max_tiles);
+                       (const int32_t*)idx, hist, T, E, k, (int)nblk, counts, starts, perm, inv,
+                       tiles, tile_count, block_m, max_tiles, shared_rows);
   return hipGetLastError();
 }
 

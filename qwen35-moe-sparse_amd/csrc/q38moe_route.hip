@@ -52,30 +52,28 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
   return k;
 }
 
-// Position of the i-th (0-based) set bit of m, or 64 when m has no such bit.
-__device__ __forceinline__ int select_bit(uint64_t m, int i) {
-  if (i < 0 || i >= __popcll(m)) return 64;
-  int pos = 0;
-#pragma unroll
-  for (int w = 32; w >= 1; w >>= 1) {
-    const uint64_t low = m & ((1ull << w) - 1ull);
-    const int c = __popcll(low);
-    if (i >= c) {
-      i -= c;
-      m >>= w;
-      pos += w;
-    } else {
-      m = low;
-    }
-  }
-  return pos;
+// Wave-uniform broadcast of lane `src`'s value (v_readlane; src must be wave-uniform).
+__device__ __forceinline__ float lane_f(float v, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+__device__ __forceinline__ int lane_i(int v, int src) { return __builtin_amdgcn_readlane(v, src); }
+
+// Number of set bits of m below the calling lane (v_mbcnt).
+__device__ __forceinline__ int bits_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-// Swap queue slots a and b (lanes).
+// Swap queue slots a and b (wave-uniform).
 __device__ __forceinline__ void swap_slots(float& qv, int& qi, int lane, int a, int b) {
-  const int src = lane == a ? b : (lane == b ? a : lane);
-  qv = __shfl(qv, src);
-  qi = __shfl(qi, src);
+  const float va = lane_f(qv, a), vb = lane_f(qv, b);
+  const int ia = lane_i(qi, a), ib = lane_i(qi, b);
+  if (lane == a) {
+    qv = vb;
+    qi = ib;
+  } else if (lane == b) {
+    qv = va;
+    qi = ia;
+  }
 }
 
 // libstdc++ __insertion_sort (a stable insertion sort) of slots [lo, hi), hi - lo <= KMAX.
@@ -87,8 +85,8 @@ __device__ void insertion_sort_slots(float& qv, int& qi, int lane, int lo, int h
 #pragma unroll
   for (int j = 0; j < KMAX; ++j) {
     const int src = min(lo + j, 63);
-    v[j] = __shfl(qv, src);
-    id[j] = __shfl(qi, src);
+    v[j] = lane_f(qv, src);
+    id[j] = lane_i(qi, src);
   }
 #pragma unroll
   for (int i = 1; i < KMAX; ++i) {
@@ -195,6 +193,8 @@ __device__ void heap_select_slots(float& qv, int& qi, int lane, int first, int m
 // std::nth_element(q, q+k-1, q+n, cmp) then std::sort(q, q+k-1, cmp), with queue slot = lane.
 __device__ void nth_element_then_sort(float& qv, int& qi, int lane, int n, int k, float* sv,
                                       int* si) {
+  int* lpos = si;                          // rank-compacted stop positions (wave-private LDS)
+  int* rpos = reinterpret_cast<int*>(sv);
   const int nth = k - 1;
   int first = 0, last = n;
   int depth = 2 * (31 - __clz(n));
@@ -208,7 +208,7 @@ __device__ void nth_element_then_sort(float& qv, int& qi, int lane, int n, int k
     --depth;
     // __unguarded_partition_pivot: median of (first+1, mid, last-1) moved to first.
     const int mid = first + (last - first) / 2;
-    const float a = __shfl(qv, first + 1), b = __shfl(qv, mid), c = __shfl(qv, last - 1);
+    const float a = lane_f(qv, first + 1), b = lane_f(qv, mid), c = lane_f(qv, last - 1);
     int s;
     if (cmp_gt(a, b)) {
       if (cmp_gt(b, c)) s = mid;
@@ -222,35 +222,43 @@ __device__ void nth_element_then_sort(float& qv, int& qi, int lane, int n, int k
       s = mid;
     }
     swap_slots(qv, qi, lane, first, s);
-    const float pv = __shfl(qv, first);
+    const float pv = lane_f(qv, first);
     // __unguarded_partition(first+1, last, pivot=first): the i-th left stop (slot holding a value
     // not cmp-greater than the pivot) swaps with the i-th right stop (value the pivot is not
-    // cmp-greater than; the pivot slot itself guards the scan) while left < right.
-    const uint64_t le = ballot64(lane > first && lane < last && !cmp_gt(qv, pv));
-    const uint64_t ge = ballot64(lane >= first && lane < last && !cmp_gt(pv, qv));
+    // cmp-greater than; the pivot slot itself guards the scan) while left < right. Stop
+    // positions are compacted into LDS by rank: lpos[i] = i-th left stop, rpos[i] = i-th right
+    // stop counted from the right.
+    const bool isl = lane > first && lane < last && !cmp_gt(qv, pv);
+    const bool isg = lane >= first && lane < last && !cmp_gt(pv, qv);
+    const uint64_t le = ballot64(isl);
+    const uint64_t ge = ballot64(isg);
     const int nl = __popcll(le), nr = __popcll(ge);
-    const int li = lane < nl ? select_bit(le, lane) : 64;
-    const int ri = lane < nr ? select_bit(ge, nr - 1 - lane) : -1;
+    const int lrank = bits_below(le);
+    const int grank = nr - 1 - bits_below(ge);
+    if (isl) lpos[lrank] = lane;
+    if (isg) rpos[grank] = lane;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int li = lane < nl ? lpos[lane] : 64;
+    const int ri = lane < nr ? rpos[lane] : -1;
     const int sw = __popcll(ballot64(lane < nl && lane < nr && li < ri));
     int cut;
     if (sw == 0) {
-      cut = select_bit(le, 0);
+      cut = lane_i(li, 0);
     } else {
-      const int l_next = sw < nl ? select_bit(le, sw) : (1 << 20);
-      const int r_last = select_bit(ge, nr - sw);
+      const int l_next = sw < nl ? lane_i(li, sw) : (1 << 20);
+      const int r_last = lane_i(ri, sw - 1);
       cut = min(l_next, r_last);
     }
     int src = lane;
-    if ((le >> lane) & 1ull) {
-      const int lr = __popcll(le & ((1ull << lane) - 1ull));
-      if (lr < sw) src = select_bit(ge, nr - 1 - lr);
-    }
-    if (src == lane && ((ge >> lane) & 1ull)) {
-      const int rr = __popcll(ge >> lane) - 1;
-      if (rr < sw) src = select_bit(le, rr);
-    }
+    if (isl && lrank < sw) src = rpos[lrank];
+    else if (isg && grank < sw) src = lpos[grank];
     qv = __shfl(qv, src & 63);
     qi = __shfl(qi, src & 63);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (cut <= nth) first = cut;
     else last = cut;
   }
@@ -261,7 +269,7 @@ __device__ void nth_element_then_sort(float& qv, int& qi, int lane, int n, int k
 
 // Route one token held by the calling wave. z: selection value of expert `lane` (lanes >= E
 // ignored). Lane r < k receives the r-th selected expert and its renormalised weight.
-__device__ void route_token(float z, int lane, int E, int k, int& out_idx, float& out_w,
+__device__ void route_token(float z, int lane, int E, int k, bool known_tie, int& out_idx, float& out_w,
                             float* sv, int* si) {
   const bool valid = lane < E;
   z = z + 0.0f;  // -0 -> +0: the comparator treats them as equal
@@ -290,8 +298,8 @@ __device__ void route_token(float z, int lane, int E, int k, int& out_idx, float
     }
     qi = best;
   } else {
-    bool tie = all_nan;
-    if (!all_nan) {
+    bool tie = all_nan || known_tie;
+    if (!tie) {
       const int rounds = min(k + 1, E);
       uint64_t key = valid ? ((uint64_t)order_key(sel) << 32) | (uint32_t)(63 - lane) : 0ull;
       uint32_t prev_key = 0;
@@ -320,60 +328,165 @@ __device__ void route_token(float z, int lane, int E, int k, int& out_idx, float
   // Renormalise over the selected probabilities, summed in selection order.
   const float pr = __shfl(p, qi & 63);
   float s = 0.0f;
-  for (int r = 0; r < k; ++r) s += __shfl(pr, r);
+  for (int r = 0; r < k; ++r) s += lane_f(pr, r);
   out_idx = qi;
   out_w = pr / s;
 }
 
-constexpr int ROUTE_TOKENS = 64;  // per block: 4 waves x 16 tokens
+constexpr int ROUTE_TOKENS = 64;   // per block: 4 waves x 16 tokens
+constexpr int ROUTE_KCHUNK = 1024; // router-weight K columns staged in LDS at a time
+constexpr int ROUTE_WROWS = 65;    // 64 expert rows + the shared-expert gate row
 
-// Logits tile per block on 16x16x32 MFMA: columns 0..E-1 are experts, column 64 is the
-// shared-expert gate projection (when given).
+// Router weight chunk in LDS: row n (expert, or 64 = shared gate), 16-byte chunk c of the
+// current K chunk stored at slot c ^ (n & 15): the 16 rows of a B fragment read distinct banks.
+__device__ __forceinline__ int wr_slot(int n, int c) { return n * (ROUTE_KCHUNK / 8) + (c ^ (n & 15)); }
+
+// Per-token selection by one lane: top-(KP1) insertion list over the token's E values. Returns
+// false when the k+1 largest values are not all distinct (or the row has NaN / non-finite max);
+// such tokens need the libstdc++ replay.
+template <int KP1>
+__device__ __forceinline__ bool lane_select(const float* row, const float* bias, int E, int k,
+                                            int* out_idx, float* out_w) {
+  float v[KP1];
+  int id[KP1];
+#pragma unroll
+  for (int r = 0; r < KP1; ++r) {
+    v[r] = -INFINITY;
+    id[r] = -1;
+  }
+  bool nan = false;
+  for (int e = 0; e < E; ++e) {
+    float z = row[e] + (bias != nullptr ? bias[e] : 0.0f);
+    z = z + 0.0f;
+    nan |= __builtin_isnan(z);
+    if (z > v[KP1 - 1]) {
+      v[KP1 - 1] = z;
+      id[KP1 - 1] = e;
+#pragma unroll
+      for (int r = KP1 - 1; r > 0; --r) {
+        if (v[r] > v[r - 1]) {
+          const float tv = v[r];
+          v[r] = v[r - 1];
+          v[r - 1] = tv;
+          const int ti = id[r];
+          id[r] = id[r - 1];
+          id[r - 1] = ti;
+        }
+      }
+    }
+  }
+  const float m = v[0];
+  if (nan || !__builtin_isfinite(m)) return false;
+  const bool partial = k * 64 <= E;  // std::partial_sort path: lowest-index maximum (k == 1)
+  if (!partial) {
+    const int lim = min(k, E - 1);
+#pragma unroll
+    for (int r = 0; r < KP1 - 1; ++r)
+      if (r < lim && v[r] == v[r + 1]) return false;
+  }
+  float s = 0.0f;
+  for (int e = 0; e < E; ++e) {
+    const float z = row[e] + (bias != nullptr ? bias[e] : 0.0f);
+    s += expf(z - m);
+  }
+  const float inv = 1.0f / s;
+  float pr[KP1];
+  float tot = 0.0f;
+#pragma unroll
+  for (int r = 0; r < KP1 - 1; ++r) {
+    pr[r] = expf(v[r] - m) * inv;
+    if (r < k) tot += pr[r];
+  }
+#pragma unroll
+  for (int r = 0; r < KP1 - 1; ++r) {
+    if (r < k) {
+      out_idx[r] = id[r];
+      out_w[r] = pr[r] / tot;
+    }
+  }
+  return true;
+}
+
+__device__ bool lane_select_k(const float* row, const float* bias, int E, int k, int* oi, float* ow) {
+  switch (k) {
+    case 1: return lane_select<2>(row, bias, E, k, oi, ow);
+    case 2: return lane_select<3>(row, bias, E, k, oi, ow);
+    case 3: return lane_select<4>(row, bias, E, k, oi, ow);
+    case 4: return lane_select<5>(row, bias, E, k, oi, ow);
+    case 5: return lane_select<6>(row, bias, E, k, oi, ow);
+    case 6: return lane_select<7>(row, bias, E, k, oi, ow);
+    case 7: return lane_select<8>(row, bias, E, k, oi, ow);
+    default: return lane_select<9>(row, bias, E, k, oi, ow);
+  }
+}
+
+// One block = 64 tokens. Phase 1: logits on 16x16x32 MFMA, router weights (+ the shared-expert
+// gate row as column 64) staged in LDS per 1024-wide K chunk, each wave's 16 x rows loaded
+// straight into registers with the whole chunk in flight. Phase 2: bf16-rounded logits to LDS.
+// Phase 3: one lane per token selects top-k (unique answer when the k+1 largest values are
+// distinct). Phase 4: tokens with ties are replayed wave-parallel through libstdc++'s algorithm.
 __global__ __launch_bounds__(256) void route_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
     const uint16_t* __restrict__ wsg, const uint16_t* __restrict__ logits_in,
     const float* __restrict__ bias, uint16_t* __restrict__ logits_out,
     int32_t* __restrict__ idx_out, uint16_t* __restrict__ w_out,
     uint16_t* __restrict__ gate_out, int32_t* __restrict__ hist, int64_t T, int h, int E, int k) {
+  __shared__ __attribute__((aligned(16))) u32x4_t s_w[ROUTE_WROWS * (ROUTE_KCHUNK / 8)];
   __shared__ float s_logit[ROUTE_TOKENS][65];
+  __shared__ float s_bias[64];
   __shared__ int s_hist[64];
+  __shared__ int s_ties[ROUTE_TOKENS];
+  __shared__ int s_nties;
   __shared__ float s_sv[4][64];
   __shared__ int s_si[4][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t tb = (int64_t)blockIdx.x * ROUTE_TOKENS;
-  if (tid < 64) s_hist[tid] = 0;
+  if (tid < 64) {
+    s_hist[tid] = 0;
+    s_bias[tid] = (bias != nullptr && tid < E) ? bias[tid] : 0.0f;
+  }
+  if (tid == 0) s_nties = 0;
 
   if (logits_in == nullptr) {
     const int ntile = (E + 15) >> 4;
+    const bool gate_tile = wsg != nullptr;
+    const int nrows_w = gate_tile ? ROUTE_WROWS : 64;
     f32x4_t acc[5];
 #pragma unroll
     for (int j = 0; j < 5; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const int64_t trow = tb + wave * 16 + (lane & 15);
-    const bool tvalid = trow < T;
-    const int kc = 8 * (lane >> 4);
-    const uint16_t* xa = x + (tvalid ? trow : 0) * (int64_t)h + kc;
-    const uint16_t* wb[5];
+    const uint16_t* xa = x + (trow < T ? trow : T - 1) * (int64_t)h + 8 * (lane >> 4);
+    for (int k0 = 0; k0 < h; k0 += ROUTE_KCHUNK) {
+      const int kc = min(ROUTE_KCHUNK, h - k0);  // multiple of 64
+      __syncthreads();                            // previous chunk fully consumed
+      // This wave's x rows for the chunk: all loads in flight before the MFMAs.
+      u32x4_t a[32];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = 16 * j + (lane & 15);
-      wb[j] = col < E ? wr + (int64_t)col * h + kc : nullptr;
-    }
-    wb[4] = ((lane & 15) == 0 && wsg != nullptr) ? wsg + kc : nullptr;
-    const bool gate_tile = wsg != nullptr;
-    const u32x4_t zero = {0u, 0u, 0u, 0u};
-#pragma unroll 2
-    for (int k0 = 0; k0 < h; k0 += 32) {
-      const u32x4_t av = tvalid ? ld16(xa + k0) : zero;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j < ntile) {
-          const u32x4_t bv = wb[j] ? ld16(wb[j] + k0) : zero;
-          acc[j] = mfma16x16x32(av, bv, acc[j]);
+      for (int s = 0; s < 32; ++s)
+        if (s * 32 < kc) a[s] = ld16(xa + k0 + s * 32);
+      // Router weights -> LDS by asynchronous copies: one wave instruction fills 64 slots
+      // (1 KiB) of a row; lane l takes the 16-byte chunk that the swizzle puts in slot l.
+      // A chunk narrower than 512 columns leaves slots past kc/8 unused; their lanes copy chunk 0.
+      const int halves = (kc + 511) / 512;        // 1 KiB row segments in this chunk
+      for (int q = wave; q < nrows_w * halves; q += 4) {
+        const int n = q / halves, part = q - n * halves;
+        const uint16_t* src = n < 64 ? (n < E ? wr + (int64_t)n * h : nullptr) : wsg;
+        if (src != nullptr) {
+          const int c = (part * 64 + lane) ^ (n & 15);
+          load_lds16(src + k0 + (c < kc / 8 ? c : 0) * 8, &s_w[n * (ROUTE_KCHUNK / 8) + part * 64]);
         }
       }
-      if (gate_tile) {
-        const u32x4_t bv = wb[4] ? ld16(wb[4] + k0) : zero;
-        acc[4] = mfma16x16x32(av, bv, acc[4]);
+      wait_vmcnt0();
+      __syncthreads();
+#pragma unroll
+      for (int s = 0; s < 32; ++s) {
+        if (s * 32 < kc) {
+          const int c = 4 * s + (lane >> 4);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (j < ntile) acc[j] = mfma16x16x32(a[s], s_w[wr_slot(16 * j + (lane & 15), c)], acc[j]);
+          if (gate_tile) acc[4] = mfma16x16x32(a[s], s_w[wr_slot(64, c)], acc[4]);
+        }
       }
     }
 #pragma unroll
@@ -411,15 +524,34 @@ __global__ __launch_bounds__(256) void route_kernel(
     if (t < T) gate_out[t] = (uint16_t)f32_to_bf16_rne(s_logit[tid][64]);
   }
 
-  const float b = (bias != nullptr && lane < E) ? bias[lane] : 0.0f;
-  for (int tt = 0; tt < 16; ++tt) {
-    const int tl = wave * 16 + tt;
+  // Phase 3: one lane per token.
+  if (wave == 0) {
+    const int64_t t = tb + lane;
+    if (t < T) {
+      int oi[KMAX];
+      float ow[KMAX];
+      if (lane_select_k(s_logit[lane], bias != nullptr ? s_bias : nullptr, E, k, oi, ow)) {
+        for (int r = 0; r < k; ++r) {
+          idx_out[t * k + r] = oi[r];
+          w_out[t * k + r] = (uint16_t)f32_to_bf16_rne(ow[r]);
+          atomicAdd(&s_hist[oi[r]], 1);
+        }
+      } else {
+        s_ties[atomicAdd(&s_nties, 1)] = lane;
+      }
+    }
+  }
+  __syncthreads();
+
+  // Phase 4: tied tokens, one wave each.
+  const int nties = s_nties;
+  for (int q = wave; q < nties; q += 4) {
+    const int tl = s_ties[q];
     const int64_t t = tb + tl;
-    if (t >= T) break;
-    const float z = lane < E ? s_logit[tl][lane] + b : -INFINITY;
+    const float z = lane < E ? s_logit[tl][lane] + s_bias[lane] : -INFINITY;
     int oi;
     float ow;
-    route_token(z, lane, E, k, oi, ow, s_sv[wave], s_si[wave]);
+    route_token(z, lane, E, k, true, oi, ow, s_sv[wave], s_si[wave]);
     if (lane < k) {
       idx_out[t * k + lane] = oi;
       w_out[t * k + lane] = (uint16_t)f32_to_bf16_rne(ow);

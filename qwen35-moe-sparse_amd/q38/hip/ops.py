@@ -48,8 +48,8 @@ def gemm_block_m():
     return int(lib.q38moe_gemm_block_m())
 
 
-def max_tiles(T, E, k, block_m=None):
-    return int(lib.q38moe_max_tiles(T, E, k, gemm_block_m() if block_m is None else block_m))
+def max_tiles(T, E, k, shared_rows=0):
+    return int(lib.q38moe_max_tiles(T, E, k, shared_rows))
 
 
 def route(x, w_router, k, w_shared_gate=None, logit_bias=None, want_logits=False, want_hist=False):
@@ -106,24 +106,31 @@ def histogram(idx, E):
     return hist
 
 
-def permute(idx, hist, E, block_m=None):
-    """Stable counting sort of pairs by expert (inference.py:163-171): (counts, starts, perm, tiles)."""
+def permute(idx, hist, E, shared_rows=0):
+    """Stable counting sort of pairs by expert (inference.py:163-171).
+
+    Returns (counts [E], starts [E], perm [T*k], inv [T*k], tiles [max_tiles, 4], tile_count [1]);
+    with shared_rows > 0 the tile table ends with the shared-expert rows T*k .. T*k+shared_rows.
+    """
     _need(idx, "topk_idx", dtype=None, ndim=2)
     _need(hist, "hist", dtype=torch.int32, ndim=2)
     T, k = idx.shape
-    bm = gemm_block_m() if block_m is None else int(block_m)
     dev = idx.device
     counts = torch.empty(E, dtype=torch.int32, device=dev)
     starts = torch.empty(E, dtype=torch.int32, device=dev)
     perm = torch.empty(T * k, dtype=torch.int32, device=dev)
-    tiles = torch.empty(max_tiles(T, E, k, bm), 4, dtype=torch.int32, device=dev)
+    inv = torch.empty(T * k, dtype=torch.int32, device=dev)
+    tiles = torch.empty(max_tiles(T, E, k, shared_rows), 4, dtype=torch.int32, device=dev)
+    tile_count = torch.empty(1, dtype=torch.int32, device=dev)
     check(lib.q38moe_permute(_ptr(idx), _idx_flag(idx), _ptr(hist), _ptr(counts), _ptr(starts), _ptr(perm),
-                             _ptr(tiles), bm, T, E, k, _stream(dev)), "q38moe_permute")
-    return counts, starts, perm, tiles
+                             _ptr(inv), _ptr(tiles), _ptr(tile_count), shared_rows, T, E, k, _stream(dev)),
+          "q38moe_permute")
+    return counts, starts, perm, inv, tiles, tile_count
 
 
-def gate_up(x, w_gate_up, perm, tiles, k):
-    """Grouped gate/up GEMM + SwiGLU (inference.py:60-96): H [T*k, I] bf16 in sorted order."""
+def gate_up(x, w_gate_up, perm, tiles, tile_count, k, shared_weights=None, shared_rows=0):
+    """Grouped gate/up GEMM + SwiGLU (inference.py:60-96): H [T*k + shared_rows, I] bf16, rows in
+    expert-sorted order then the shared-expert rows (shared_weights = (gate_proj.weight, up_proj.weight))."""
     _need(x, "x", ndim=2)
     _need(w_gate_up, "w_gate_up", ndim=3)
     _need(perm, "perm", dtype=torch.int32)
@@ -133,31 +140,37 @@ def gate_up(x, w_gate_up, perm, tiles, k):
     if hh != h or twoI % 2:
         raise ValueError(f"w_gate_up {tuple(w_gate_up.shape)} does not match hidden {h}")
     I = twoI // 2
-    if tiles.shape[0] != max_tiles(T, E, k):
-        raise ValueError("tiles was not built for this shape and the GEMM tile height")
-    H = torch.empty(T * k, I, dtype=torch.bfloat16, device=x.device)
-    check(lib.q38moe_gate_up(_ptr(x), _ptr(w_gate_up), _ptr(perm), _ptr(tiles), _ptr(H), T, h, E, k, I, BF16,
-                             _stream(x.device)), "q38moe_gate_up")
+    if tiles.shape[0] != max_tiles(T, E, k, shared_rows):
+        raise ValueError("tiles was not built for this shape")
+    wg = wu = None
+    if shared_rows:
+        wg, wu = shared_weights
+        _need(wg, "shared gate_proj", ndim=2)
+        _need(wu, "shared up_proj", ndim=2)
+        if wg.shape != (I, h) or wu.shape != (I, h):
+            raise ValueError("the shared expert runs inside the grouped GEMM only when its width equals I")
+    H = torch.empty(T * k + shared_rows, I, dtype=torch.bfloat16, device=x.device)
+    check(lib.q38moe_gate_up(_ptr(x), _ptr(w_gate_up), _ptr(wg), _ptr(wu), _ptr(perm), _ptr(tiles), _ptr(tile_count),
+                             shared_rows, _ptr(H), T, h, E, k, I, BF16, _stream(x.device)), "q38moe_gate_up")
     return H
 
 
-def down(H, w_down, perm, tiles, topk_w):
-    """Grouped down GEMM x routing weight (inference.py:99-130): y [T*k, h] bf16 in pair order."""
+def down(H, w_down, tiles, tile_count, T, k, w_shared_down=None, shared_rows=0):
+    """Grouped down GEMM (inference.py:99-127, routing weight left to combine): Y [rows, h] bf16."""
     _need(H, "H", ndim=2)
     _need(w_down, "w_down", ndim=3)
-    _need(perm, "perm", dtype=torch.int32)
     _need(tiles, "tiles", dtype=torch.int32, ndim=2)
-    _need(topk_w, "topk_w", ndim=2)
-    T, k = topk_w.shape
     E, h, I = w_down.shape
-    if H.shape != (T * k, I):
-        raise ValueError(f"H {tuple(H.shape)} does not match ({T * k}, {I})")
-    if tiles.shape[0] != max_tiles(T, E, k):
-        raise ValueError("tiles was not built for this shape and the GEMM tile height")
-    y = torch.empty(T * k, h, dtype=torch.bfloat16, device=H.device)
-    check(lib.q38moe_down(_ptr(H), _ptr(w_down), _ptr(perm), _ptr(tiles), _ptr(topk_w), _ptr(y), T, h, E, k, I,
-                          BF16, _stream(H.device)), "q38moe_down")
-    return y
+    if H.shape != (T * k + shared_rows, I):
+        raise ValueError(f"H {tuple(H.shape)} does not match ({T * k + shared_rows}, {I})")
+    if tiles.shape[0] != max_tiles(T, E, k, shared_rows):
+        raise ValueError("tiles was not built for this shape")
+    if shared_rows:
+        _need(w_shared_down, "shared down_proj", ndim=2)
+    Y = torch.empty(T * k + shared_rows, h, dtype=torch.bfloat16, device=H.device)
+    check(lib.q38moe_down(_ptr(H), _ptr(w_down), _ptr(w_shared_down), _ptr(tiles), _ptr(tile_count), shared_rows,
+                          _ptr(Y), T, h, E, k, I, BF16, _stream(H.device)), "q38moe_down")
+    return Y
 
 
 def shared_expert(x, w_gate, w_up, w_down):
@@ -176,11 +189,14 @@ def shared_expert(x, w_gate, w_up, w_down):
     return out
 
 
-def combine(y, k, E, idx=None, shared_out=None, shared_gate_logit=None):
-    """routed = bf16(sum_j y[t*k+j]) (inference.py:199), optionally + sigmoid-gated shared output."""
-    _need(y, "y", ndim=2)
-    P, h = y.shape
-    T = P // k
+def combine(Y, inv, topk_w, E, idx=None, shared_out=None, shared_gate_logit=None):
+    """out[t] = bf16(sum_j bf16(Y[inv[t*k+j]] * w[t,j])) (inference.py:128-130,199), optionally plus
+    the sigmoid-gated shared-expert row (modeling:831-833)."""
+    _need(Y, "Y", ndim=2)
+    _need(inv, "inv", dtype=torch.int32)
+    _need(topk_w, "topk_w", ndim=2)
+    T, k = topk_w.shape
+    h = Y.shape[1]
     flag = 0
     if idx is not None:
         _need(idx, "topk_idx", dtype=None, ndim=2)
@@ -188,9 +204,10 @@ def combine(y, k, E, idx=None, shared_out=None, shared_gate_logit=None):
     if shared_out is not None:
         _need(shared_out, "shared_out", ndim=2)
         _need(shared_gate_logit, "shared_gate_logit")
-    out = torch.empty(T, h, dtype=torch.bfloat16, device=y.device)
-    check(lib.q38moe_combine(_ptr(y), _ptr(idx), flag, _ptr(shared_out), _ptr(shared_gate_logit), _ptr(out), T, h,
-                             E, k, BF16, _stream(y.device)), "q38moe_combine")
+    out = torch.empty(T, h, dtype=torch.bfloat16, device=Y.device)
+    check(lib.q38moe_combine(_ptr(Y), _ptr(inv), _ptr(idx), flag, _ptr(topk_w), _ptr(shared_out),
+                             _ptr(shared_gate_logit), _ptr(out), T, h, E, k, BF16, _stream(Y.device)),
+          "q38moe_combine")
     return out
 
 

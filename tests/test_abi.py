@@ -32,15 +32,17 @@ def test_header_symbols_exported():
 
 def test_abi_version():
     m = _lib()
-    assert m.lib.q38moe_abi_version() == m.ABI_VERSION == 1
+    assert m.lib.q38moe_abi_version() == m.ABI_VERSION == 2
 
 
 def test_max_tiles_and_block_m():
     m = _lib()
     bm = m.lib.q38moe_gemm_block_m()
     assert bm in (64, 128, 256)
-    assert m.lib.q38moe_max_tiles(16384, 64, 5, 128) == (16384 * 5 + 127) // 128 + 64
-    assert m.lib.q38moe_max_tiles(-1, 64, 5, 128) == -1
+    cd = lambda a, b: (a + b - 1) // b  # noqa: E731
+    assert m.lib.q38moe_max_tiles(16384, 64, 5, 0) == cd(16384 * 5, bm) + 64
+    assert m.lib.q38moe_max_tiles(16384, 64, 5, 16384) == cd(16384 * 5, bm) + 64 + cd(16384, bm)
+    assert m.lib.q38moe_max_tiles(-1, 64, 5, 0) == -1
 
 
 def test_workspace_sizes():

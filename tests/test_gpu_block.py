@@ -31,27 +31,55 @@ def test_gate_up_down_stages(gpu, name, T):
     wl, x, params, _ = _setup(name, T)
     k = wl.topk
     _, _, ridx, rw = orc.router(x, params["gate.weight"], k)
-    ref_out, ref_y, ref_H = orc.experts_grouped(x, ridx, rw, params["experts.gate_up_proj"],
-                                                params["experts.down_proj"])
+    ref_out, ref_y, ref_H, ref_Y = orc.experts_grouped(x, ridx, rw, params["experts.gate_up_proj"],
+                                                       params["experts.down_proj"], return_sorted=True)
     dx, didx, dw = x.to(gpu), ridx.to(gpu), rw.to(gpu)
     wgu, wdn = params["experts.gate_up_proj"].to(gpu), params["experts.down_proj"].to(gpu)
     hist = ops.histogram(didx, wl.experts)
-    counts, starts, perm, tiles = ops.permute(didx, hist, wl.experts)
-    H = ops.gate_up(dx, wgu, perm, tiles, k)
+    counts, starts, perm, inv, tiles, tcount = ops.permute(didx, hist, wl.experts)
+    H = ops.gate_up(dx, wgu, perm, tiles, tcount, k)
     torch.cuda.synchronize()
     # H in sorted order: bf16 results of identical roundings; fp32 accumulation order differs.
     assert_bf16_close(H.cpu(), ref_H, what="H (gate/up + SwiGLU)")
     assert float((bf16_ulp_diff(H.cpu(), ref_H) > 1).float().mean()) < 1e-3
-    y = ops.down(H, wdn, perm, tiles, dw)
+    Y = ops.down(H, wdn, tiles, tcount, T, k)
     torch.cuda.synchronize()
-    assert_bf16_close(y.cpu(), ref_y, what="y (down x weight)")
+    assert_bf16_close(Y.cpu(), ref_Y, what="Y (down projection, sorted rows)")
     # Down alone on the oracle's H: isolates the down GEMM.
-    y2 = ops.down(ref_H.to(gpu), wdn, perm, tiles, dw)
+    Y2 = ops.down(ref_H.to(gpu), wdn, tiles, tcount, T, k)
     torch.cuda.synchronize()
-    assert float((bf16_ulp_diff(y2.cpu(), ref_y) > 1).float().mean()) < 1e-3
-    out = ops.combine(y, k, wl.experts)
+    assert float((bf16_ulp_diff(Y2.cpu(), ref_Y) > 1).float().mean()) < 1e-3
+    # Combine on the oracle's sorted rows: weight, k-sum and rounding exactly as the oracle.
+    out_exact = ops.combine(ref_Y.to(gpu), inv, dw, wl.experts)
+    torch.cuda.synchronize()
+    assert float((bf16_ulp_diff(out_exact.cpu(), ref_out) > 1).float().mean()) < 1e-3
+    out = ops.combine(Y, inv, dw, wl.experts)
     torch.cuda.synchronize()
     assert_bf16_close(out.cpu(), ref_out, what="routed experts output")
+
+
+def test_fused_shared_rows(gpu):
+    """Routed and shared-expert rows in one grouped launch equal the separate computations."""
+    ops = _ops()
+    wl, x, params, _ = _setup("c2", 1500)
+    T, k = x.shape[0], wl.topk
+    _, _, ridx, rw = orc.router(x, params["gate.weight"], k)
+    d = {n: p.to(gpu) for n, p in params.items()}
+    didx = ridx.to(gpu)
+    hist = ops.histogram(didx, wl.experts)
+    counts, starts, perm, inv, tiles, tcount = ops.permute(didx, hist, wl.experts, shared_rows=T)
+    H = ops.gate_up(x.to(gpu), d["experts.gate_up_proj"], perm, tiles, tcount, k,
+                    shared_weights=(d["shared_expert.gate_proj.weight"], d["shared_expert.up_proj.weight"]),
+                    shared_rows=T)
+    Y = ops.down(H, d["experts.down_proj"], tiles, tcount, T, k, w_shared_down=d["shared_expert.down_proj.weight"],
+                 shared_rows=T)
+    torch.cuda.synchronize()
+    ref_sh = orc.shared_expert(x, params["shared_expert.gate_proj.weight"], params["shared_expert.up_proj.weight"],
+                               params["shared_expert.down_proj.weight"])
+    assert_bf16_close(Y[T * k:].cpu(), ref_sh, what="shared rows of the fused launch")
+    _, _, ref_H, ref_Y = orc.experts_grouped(x, ridx, rw, params["experts.gate_up_proj"],
+                                             params["experts.down_proj"], return_sorted=True)
+    assert_bf16_close(Y[:T * k].cpu(), ref_Y, what="routed rows of the fused launch")
 
 
 @pytest.mark.parametrize("name,T", [("c1", 2048), ("c2", 4096), ("c2", 333)])

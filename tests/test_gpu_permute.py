@@ -15,27 +15,34 @@ def _ops():
     return ops
 
 
-def _check(idx, E, gpu, block_m=None):
+def _check(idx, E, gpu, shared_rows=0):
     ops = _ops()
     T, k = idx.shape
     didx = idx.to(gpu)
     hist = ops.histogram(didx, E)
-    counts, starts, perm, tiles = ops.permute(didx, hist, E, block_m=block_m)
+    counts, starts, perm, inv, tiles, tile_count = ops.permute(didx, hist, E, shared_rows=shared_rows)
     torch.cuda.synchronize()
     rc, rs, rp = orc.permute_cpu(idx.numpy(), E)
     assert np.array_equal(counts.cpu().numpy(), rc)
     assert np.array_equal(starts.cpu().numpy(), rs)
     n = rp.size
     assert np.array_equal(perm.cpu().numpy()[:n], rp)
-    # Tile table: experts ascending, rows tile each expert's segment exactly, padding per expert.
-    bm = ops.gemm_block_m() if block_m is None else block_m
+    # inv is the inverse permutation on the valid pairs.
+    inv_np = inv.cpu().numpy()
+    assert np.array_equal(inv_np[rp], np.arange(n))
+    # Tile table: experts ascending, rows tile each expert's segment exactly (padding per expert),
+    # then the shared-expert rows.
+    bm = ops.gemm_block_m()
     tl = tiles.cpu().numpy()
     used = tl[tl[:, 0] >= 0]
+    assert int(tile_count.item()) == len(used)
     assert (tl[len(used):, 0] == -1).all(), "unused tiles must follow the used ones"
     expect = []
     for e in range(E):
         for r0 in range(0, int(rc[e]), bm):
             expect.append((e, int(rs[e]) + r0, min(bm, int(rc[e]) - r0)))
+    for r0 in range(0, shared_rows, bm):
+        expect.append((E, T * k + r0, min(bm, shared_rows - r0)))
     assert [tuple(map(int, t[:3])) for t in used] == expect
     return counts, starts, perm
 
@@ -67,20 +74,21 @@ def test_permute_out_of_range_dropped(gpu):
     _check(idx, 8, gpu)
 
 
-def test_permute_block_m(gpu):
+def test_permute_shared_tiles(gpu):
+    """Shared-expert rows appended to the tile table (the fused grouped-GEMM launch)."""
     g = torch.Generator().manual_seed(11)
     idx = torch.randint(0, 64, (3000, 5), generator=g).to(torch.int32)
-    _check(idx, 64, gpu, block_m=16)
+    _check(idx, 64, gpu, shared_rows=3000)
 
 
 def test_permute_empty(gpu):
     ops = _ops()
     idx = torch.empty(0, 5, dtype=torch.int32, device=gpu)
     hist = ops.histogram(idx, 64)
-    counts, starts, perm, tiles = ops.permute(idx, hist, 64)
+    counts, starts, perm, inv, tiles, tile_count = ops.permute(idx, hist, 64)
     torch.cuda.synchronize()
     assert int(counts.sum()) == 0 and int(starts.abs().sum()) == 0
-    assert (tiles.cpu()[:, 0] == -1).all()
+    assert (tiles.cpu()[:, 0] == -1).all() and int(tile_count.item()) == 0
 
 
 def test_permute_deterministic(gpu):
