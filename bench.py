@@ -91,35 +91,46 @@ def kernel_breakdown(wl, x, d, bias, iters, stream):
     return out
 
 
-def cpu_baseline(wl, budget_s=15.0):
-    """The reference block's own op sequence (eager experts loop) in bf16 on this host's CPU, on the
-    first `tokens` tokens of the same workload (all of them when they fit the time budget)."""
+def cpu_baseline(wl, budget_s=12.0, max_runs=400):
+    """The reference block's own op sequence (eager experts loop) in bf16 on this host's CPU over the
+    same workload: whole block forwards over the first `tokens` tokens (all of them unless one run
+    would exceed the budget), repeated until about `budget_s` seconds of CPU work are done."""
     import torch
     from oracle import moe_oracle
     from q38 import workloads
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
-    x_all, params, _ = workloads.make(wl)
+    x_all, params, bias = workloads.make(wl)
     tokens = min(1024, wl.tokens)
     with torch.inference_mode():
         t0 = time.perf_counter()
-        moe_oracle.reference_block_forward(x_all[:tokens], params, wl.topk)  # warmup + size probe
+        moe_oracle.reference_block_forward(x_all[:tokens], params, wl.topk, logit_bias=bias)  # warmup + probe
         per_tok = (time.perf_counter() - t0) / tokens
-        # Size the sample so the 3 timed runs take about budget_s (whole workload if it fits).
         tokens = int(max(1024, min(wl.tokens, budget_s / 3 / max(per_tok, 1e-9))))
         x = x_all[:tokens]
         times = []
-        for _ in range(3):
+        start = time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - start < budget_s and len(times) < max_runs):
             t0 = time.perf_counter()
-            moe_oracle.reference_block_forward(x, params, wl.topk)
+            moe_oracle.reference_block_forward(x, params, wl.topk, logit_bias=bias)
             times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[1]
+    total = sum(times)
+    med = sorted(times)[len(times) // 2]
+    cpu = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     return dict(value=round(tokens / med, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
-                sample=f"{tokens} of the {wl.tokens} tokens of {wl.name} (h={wl.hidden}, E={wl.experts}, k={wl.topk}, "
-                       f"I={wl.inter}), bf16 torch CPU, reference op sequence with the eager experts loop "
-                       f"(modeling_qwen3_8_moe.py:769-793,805-813,824-835), median of 3 after 1 warmup",
-                seconds=[round(t, 3) for t in times])
+                sample=f"{len(times)} block forwards over {tokens} of the {wl.tokens} tokens of {wl.name} "
+                       f"(h={wl.hidden}, E={wl.experts}, k={wl.topk}, I={wl.inter}), {total:.1f} s of CPU work; "
+                       f"bf16 torch CPU running the reference op sequence with the eager experts loop "
+                       f"(modeling_qwen3_8_moe.py:769-793,805-813,824-835); value = tokens / median run",
+                runs=len(times), seconds_total=round(total, 2), seconds_median=round(med, 4),
+                os_cpu_count=os.cpu_count(), cpu_model=cpu)
 
 
 def main():

@@ -192,11 +192,14 @@ def block(x, params, k, logit_bias=None):
                      gate_logit=gate_logit)
 
 
-def reference_block_forward(x, params, k):
+def reference_block_forward(x, params, k, logit_bias=None):
     """The reference block's own op sequence (modeling:805-813, 769-793, 751-753, 824-835) in the
-    dtype of the inputs, eager experts loop. This is the CPU baseline that bench.py times."""
+    dtype of the inputs, eager experts loop. This is the CPU baseline that bench.py times. The
+    optional fp32 ``logit_bias`` [E] (routing-skew workload) is added to the logits before the
+    softmax."""
     logits = F.linear(x, params["gate.weight"])
-    probs = torch.softmax(logits, dtype=torch.float, dim=-1)
+    z = logits if logit_bias is None else logits.float() + logit_bias.float()
+    probs = torch.softmax(z, dtype=torch.float, dim=-1)
     top, idx = torch.topk(probs, k, dim=-1)
     top /= top.sum(dim=-1, keepdim=True)
     w = top.to(logits.dtype)

@@ -79,9 +79,10 @@ WORKLOADS = {
                    dtype="fp32"),
     # Headline configuration: 4 x 4096 packed tokens, bf16.
     "c2": Workload("c2", hidden=1024, experts=64, topk=5, inter=256, shared_inter=256, batch=4, seq=4096),
-    # Routing skew: C2 plus a per-expert Zipf(1.2) logit bias.
+    # Routing skew: C2 plus a per-expert Zipf(1.2) logit bias. alpha = 0.24 is calibrated on these
+    # seeded inputs for a ~20x span of expert loads: max 7620 / min 369 pairs (20.7x).
     "c3": Workload("c3", hidden=1024, experts=64, topk=5, inter=256, shared_inter=256, batch=4, seq=4096,
-                   zipf_s=1.2, zipf_alpha=1.0),
+                   zipf_s=1.2, zipf_alpha=0.24),
     # FP8 expert path shape (bf16 here until the fp8 kernels exist).
     "c4": Workload("c4", hidden=2048, experts=64, topk=5, inter=512, shared_inter=512, batch=8, seq=4096,
                    dtype="fp8"),

@@ -149,3 +149,19 @@ def test_shared_expert_matches_linear_chain():
     ref = F.linear(F.silu(F.linear(x, wg)) * F.linear(x, wu), wd)
     diff = (orc.shared_expert(x, wg, wu, wd).float() - ref.float()).abs()
     assert float(diff.max()) < 2e-2
+
+
+def test_skew_workload_load_span():
+    """The routing-skew workload's logit bias gives the ~20x span of expert loads it stands for
+    (max/min pair count over experts on its seeded inputs), and the bias is a Zipf law in rank."""
+    from q38 import workloads
+    wl = workloads.get("c3")
+    x, p, bias = workloads.make(wl)
+    b = bias.double().numpy()
+    ranks = np.argsort(np.argsort(-b)) + 1   # rank 1 = largest bias
+    assert np.allclose(b, -wl.zipf_alpha * wl.zipf_s * np.log(ranks), atol=1e-6)
+    logits = orc.bf16(x.float() @ p["gate.weight"].float().T)
+    _, _, idx, _ = orc.router(x, p["gate.weight"], wl.topk, logit_bias=bias, logits=logits)
+    c = np.bincount(idx.reshape(-1).numpy(), minlength=wl.experts)
+    assert c.sum() == wl.tokens * wl.topk
+    assert 15 <= c.max() / c.min() <= 30, (c.max(), c.min())
