@@ -133,6 +133,45 @@ def cpu_baseline(wl, budget_s=12.0, max_runs=400):
                 os_cpu_count=os.cpu_count(), cpu_model=cpu)
 
 
+# Kernel symbol of each stage, as rocprofv3 names it (for the committed PMC byte counts).
+KERNEL_SYMBOLS = {
+    "route": "q38::route_kernel",
+    "permute": "q38::permute_kernel",
+    "gate_up": "q38::grouped_gemm_kernel<0>",
+    "down": "q38::grouped_gemm_kernel<1>",
+    "combine": "q38::combine_kernel",
+}
+TRAFFIC_FILE = REPO / "profiles" / "hbm_traffic.json"
+
+
+def hbm_traffic(workload, stage):
+    """HBM bytes per launch of `stage` from the committed rocprofv3 PMC summary: FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch), each scaled by the factor a plain copy of known size gives those
+    counters on the same device. None when no summary for this workload and kernel exists."""
+    try:
+        data = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = data.get("workloads", {}).get(workload, {}).get(KERNEL_SYMBOLS.get(stage, stage))
+    if not entry:
+        return None
+    f = data["copy_calibration"]
+    return round(entry["FETCH_SIZE_KiB"] * f["fetch_factor"] * 1024 + entry["WRITE_SIZE_KiB"] * f["write_factor"] * 1024)
+
+
+def copy_probe(mib):
+    """One device-to-device copy of `mib` MiB: the known-size reference for the FETCH_SIZE and
+    WRITE_SIZE counters in a PMC run of this script."""
+    import torch
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] copy probe: {mib} MiB read, {mib} MiB written")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -141,6 +180,8 @@ def main():
     ap.add_argument("--workload", default="c2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=20)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="end with one copy of this many MiB (PMC byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this benchmark measures one GPU only; the MoE block is data-parallel "
@@ -211,7 +252,7 @@ def main():
                    "tokens": T, "hidden": h, "experts": wl.experts, "top_k": k, "expert_inter": wl.inter,
                    "shared_inter": wl.shared_inter, "routing_skew": wl.zipf_s, "parallelism": "single GPU"},
         "roofline": {"kernel": dom, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
-                     "unit": dk["unit"], "frac": dk["frac"], "traffic": None,
+                     "unit": dk["unit"], "frac": dk["frac"], "traffic": hbm_traffic(wl.name, dom),
                      "work_per_launch": dk["work"]},
         # Routed + shared expert GEMM FLOPs over the two grouped launches that compute them.
         "mfma_frac_expert_gemms": round(expert_fl / (expert_us * 1e-6) / PEAK_BF16, 4),
@@ -222,6 +263,8 @@ def main():
         log("[bench] timing the CPU baseline")
         res["cpu_baseline"] = cpu_baseline(wl)
         log(f"[bench] cpu baseline: {res['cpu_baseline']['value']} tokens/s")
+    if args.copy_probe_mib > 0:
+        copy_probe(args.copy_probe_mib)
     print(json.dumps(res), flush=True)
 
 
