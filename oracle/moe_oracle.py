@@ -10,6 +10,7 @@ modeling_qwen3_8_moe.py, "inference" = q38/inference.py):
                   in q38_oracle.cpp (liboracle.so) that calls libstdc++'s nth_element/sort.
   permute_cpu     stable counting sort = torch.sort(ids, stable=True) + searchsorted,
                   inference:163-171 (C, q38_oracle.cpp).
+  tile_table      the per-expert BM-row blocks of inference:39-50,174-183 in the GEMM's order.
   router          Qwen3_8MoeTopKRouter.forward, modeling:805-813 (fp32 matmul rounded once to
                   bf16 stands for the bf16 F.linear; softmax fp32; torch CPU topk; renorm).
   experts_grouped routed experts with the rounding sequence of inference:60-130,199 (also that
@@ -87,6 +88,27 @@ def permute_cpu(ids, E):
     perm = np.empty(valid, np.int32)
     _load().oracle_permute(a.ctypes.data, a.size, E, counts.ctypes.data, starts.ctypes.data, perm.ctypes.data)
     return counts, starts, perm
+
+
+def tile_table(counts, starts, block_m, shared_rows=0, P=None):
+    """Tile list of the grouped GEMMs as (group, row0, rows) tuples, in walking order.
+
+    The reference splits each expert's sorted segment into cdiv(count, BM) row blocks
+    (inference:39-50, 174-183); the same blocks are listed here with the full ones first (by
+    expert, then the shared-expert rows [P, P + shared_rows) as group E), then the partial ones by
+    falling row count (ties: lower group first).
+    """
+    E = len(counts)
+    P = int(np.sum(counts)) if P is None else P
+    full, partial = [], []
+    segs = [(e, int(starts[e]), int(counts[e])) for e in range(E)] + [(E, P, int(shared_rows))]
+    for g, r0, n in segs:
+        for i in range(n // block_m):
+            full.append((g, r0 + i * block_m, block_m))
+        if n % block_m:
+            partial.append((g, r0 + (n // block_m) * block_m, n % block_m))
+    partial.sort(key=lambda t: (-t[2], t[0]))
+    return full + partial
 
 
 def bf16(t):

@@ -27,6 +27,18 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_rne(f)); }
 
+// Two floats -> two bf16 (a in the low half) with one v_cvt_pk_bf16_f32 (round to nearest even,
+// as f32_to_bf16_rne for every non-NaN input; a NaN stays a NaN).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+__device__ __forceinline__ void unpack_bf16x2(uint32_t v, float& a, float& b) {
+  a = __uint_as_float(v << 16);
+  b = __uint_as_float(v & 0xffff0000u);
+}
+
 // SiLU / sigmoid evaluated in fp32 as x / (1 + exp(-x)) and 1 / (1 + exp(-x)).
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
@@ -57,6 +69,20 @@ __device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
 __device__ __forceinline__ void load_lds16(const void* gsrc, void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)gsrc,
                                    (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
+}
+
+// Same for 4 bytes per lane (global_load_lds_dword): lane l writes [lds_wave_base + 4*l, +4).
+__device__ __forceinline__ void load_lds4(const void* gsrc, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)gsrc,
+                                   (__attribute__((address_space(3))) void*)lds_wave_base, 4, 0, 0);
+}
+
+// Load through the constant address space: for a wave-uniform address the compiler emits a scalar
+// load (lgkmcnt), which keeps it out of the vmcnt queue that tracks the async LDS copies. Only
+// for data no kernel writes while the reading kernel runs.
+template <typename T>
+__device__ __forceinline__ T load_uniform(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)(p);
 }
 
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0); }

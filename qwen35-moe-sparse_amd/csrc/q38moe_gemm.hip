@@ -9,32 +9,40 @@
 // tokens; outputs are stored row-contiguous in that order (no scatter).
 //
 // Weights are [N, K] row-major (experts.gate_up_proj[e], experts.down_proj[e], nn.Linear), so
-// both MFMA operands are K-contiguous. Tile: 256 activation rows x 128 weight rows, K in 32-wide
-// slices. 4 waves (2x2), each 128 x 64 = 4x2 tiles of 32x32x16 MFMA with the weight fragment as
-// the first operand, so lane = activation row and each lane holds runs of 4 consecutive output
-// columns. For gate/up, a wave's 64 weight rows are [32 gate | 32 up] of the same 32 output
-// columns, so SwiGLU runs in registers. 128 accumulator registers and 72 KiB of LDS per workgroup
-// let two workgroups share a CU, so one's prologue/epilogue overlaps the other's MFMA loop.
+// both MFMA operands are K-contiguous. A tile is 256 activation rows x 256 weight rows; K runs in
+// 32-wide slices. One 512-thread workgroup per CU (8 waves, two per SIMD); wave w owns activation
+// rows 64*(w/2).. and weight rows 128*(w%2).., i.e. 2x4 blocks of mfma_f32_32x32x16_bf16 with the
+// weight fragment as the first operand, so lane = activation row and each lane holds runs of 4
+// consecutive output columns. For gate/up a wave's 128 weight rows are [64 gate | 64 up] of the
+// same 64 output columns, so SwiGLU runs in registers. Waves whose 64 rows are all past the
+// tile's row count skip their MFMAs; rows are paired across SIMDs (waves 0-3 hold rows 0-127), so
+// a tile of <= 128 rows costs half a full one.
 //
-// K-slices are copied global -> LDS asynchronously (global_load_lds_dwordx4) two slices ahead
-// into a 3-deep ring; slices are XOR-swizzled (16-byte chunk c of row r at slot
-// c ^ ((r >> 2) & 3): conflict-free fragment reads). The epilogue stages 32-row slabs in LDS and
-// stores whole 16-byte row chunks. Tiles are spread over the 8 XCDs in contiguous runs
-// (workgroup b runs on XCD b % 8 and takes logical tile (b % 8) * per + b / 8), so an expert's
-// weights and gathered rows stay in one XCD's L2.
+// The kernel is persistent: workgroup b walks tiles slot(b), slot(b) + G, ... (G = grid size) of a
+// list the permutation orders full tiles first and partial tiles by falling row count, and its
+// async copy stream (global_load_lds_dwordx4 into a 4-deep LDS ring, three slices ahead) runs on
+// across tile boundaries, so the next tile's first slices load during this tile's epilogue. The
+// next tile's tile entry and row gather indices are fetched one tile ahead. Slots are spread over
+// the 8 XCDs in contiguous runs (workgroup b runs on XCD b % 8 and takes slot (b % 8) * G/8 + b/8),
+// so tiles that share an expert's weights or gathered rows run in one XCD's L2 at the same time.
+//
+// Slices are XOR-swizzled (16-byte chunk c of row r at slot c ^ ((r >> 2) & 3): conflict-free
+// fragment reads). The epilogue stores from registers after a cross-lane swap (16-byte stores).
 #include "q38moe_common.h"
 #include "q38moe_kernels.h"
 
 namespace q38 {
 
-constexpr int BM = 256;  // activation rows per tile
-constexpr int BN = 128;  // weight rows per tile
-constexpr int BK = 32;   // K slice
-constexpr int NTHREADS = 256;
-constexpr int NSTAGE = 3;                    // LDS ring of K-slices
-constexpr int STAGE_ELEMS = (BM + BN) * BK;  // bf16 elements per slice
-constexpr int NCOPY = (BM + BN) / 16 / 4;    // async copies per wave per slice (16 rows each)
-constexpr int EPI_PITCH = 72;                // epilogue slab row pitch (elements): 64 + 8 pad
+constexpr int BM = 256;        // activation rows per tile
+constexpr int BW = 256;        // weight rows per tile
+constexpr int BK = 32;         // K slice
+constexpr int NTHREADS = 512;  // 8 waves
+constexpr int NSTAGE = 4;      // LDS ring of K-slices
+constexpr int AHEAD = 3;       // slices in flight ahead of the one being multiplied
+constexpr int SLICE_ELEMS = (BM + BW) * BK;  // bf16 elements per slice (32 KiB)
+constexpr int NCOPY = (BM + BW) / 16 / 8;    // async copies per lane per slice (16 rows each)
+static_assert(NCOPY == 4, "the vmcnt immediates below assume 4 copies per slice");
+static_assert(AHEAD < NSTAGE, "a slot is refilled only after the barrier that retires it");
 
 enum { MODE_GATE_UP = 0, MODE_DOWN = 1 };
 
@@ -51,195 +59,326 @@ struct GemmParams {
   uint16_t* C;                // output rows [*, N]
   int P;                      // first shared-expert row of the row space
   int N, K, E, topk;
-  int ntiles_n;               // weight-row tiles per row tile
+  int ntiles_n;               // output-column tiles per row tile
 };
 
 __device__ __forceinline__ int swz(int r, int c) { return r * BK + ((c ^ ((r >> 2) & 3)) << 3); }
 
-template <int MODE>
-__global__ __launch_bounds__(NTHREADS, 2) void grouped_gemm_kernel(GemmParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t ring[NSTAGE * STAGE_ELEMS];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int lr = lane & 31, lh = lane >> 5;
-
-  // XCD-aware logical tile.
-  const int used_m = p.tiles != nullptr ? *p.ntiles_dev : p.ntiles_host;
-  const int used = used_m * p.ntiles_n;
-  const int per = (used + 7) >> 3;
-  const int jb = (int)(blockIdx.x >> 3);
-  if (jb >= per) return;
-  const int logical = (int)(blockIdx.x & 7) * per + jb;
-  if (logical >= used) return;
-  const int mt = logical / p.ntiles_n;
-  constexpr int BN_OUT = MODE == MODE_GATE_UP ? BN / 2 : BN;
-  const int n0 = (logical - mt * p.ntiles_n) * BN_OUT;
-
-  int grp, row0, nrows;
+// Tile-table entry as scalar loads (x2 + x1: there is no 3-dword scalar load, and a 3-dword vector
+// load would join the copy queue).
+__device__ __forceinline__ int4 tile_entry(const GemmParams& p, int mt) {
   if (p.tiles != nullptr) {
-    const int4 ti = p.tiles[mt];
-    grp = ti.x;
-    row0 = ti.y;
-    nrows = ti.z;
-  } else {
-    grp = p.E;
-    row0 = mt * BM;
-    nrows = (int)min((int64_t)BM, p.M - (int64_t)row0);
+    const uint64_t xy = load_uniform(reinterpret_cast<const uint64_t*>(p.tiles + mt));
+    const int z = load_uniform(reinterpret_cast<const int*>(p.tiles + mt) + 2);
+    return make_int4((int)(uint32_t)xy, (int)(uint32_t)(xy >> 32), z, 0);
   }
-  if (nrows <= 0) return;
-  const int K = p.K, N = p.N;
-  const bool shared_grp = grp >= p.E;
+  const int row0 = mt * BM;
+  return make_int4(p.E, row0, (int)min((int64_t)BM, p.M - (int64_t)row0), 0);
+}
 
-  // Async copy sources. Copy instruction j = NCOPY*wave + q fills 16 rows (1 KiB) of the slice:
-  // j < 16 -> activation rows 16j.., else weight rows 16(j-16)... Lane l lands in slot l: row
-  // r0 + l/4, position l%4, i.e. 16-byte chunk (l%4) ^ ((row >> 2) & 3). Rows past the tile (or
-  // weight rows past N) read a clamped in-bounds row; their results only reach outputs that are
-  // never stored.
-  const uint16_t* src[NCOPY];
-  int prow[NCOPY];
-#pragma unroll
-  for (int q = 0; q < NCOPY; ++q) {  // gather indices first: one load latency, not NCOPY
-    const int j = NCOPY * wave + q;
-    const int r = 16 * j + (lane >> 2);
-    const int rr = row0 + (r < nrows ? r : 0);
-    prow[q] = (j < 16 && MODE == MODE_GATE_UP && !shared_grp) ? p.perm[rr] : rr;
-  }
+// True when the activation rows of tile `ti` are gathered through perm (routed gate/up rows).
+template <int MODE>
+__device__ __forceinline__ bool gathered(const GemmParams& p, int4 ti) {
+  return MODE == MODE_GATE_UP && ti.x < p.E;
+}
+
+// Row index behind each of this lane's activation copies (only activation-copying waves use it):
+// the pair of a routed gate/up row, else the row itself. Rows past the tile read row 0 of the
+// tile; their products only reach outputs that are never stored.
+__device__ __forceinline__ void plain_rows(int4 ti, int wave, int lane, int (&rows)[NCOPY]) {
 #pragma unroll
   for (int q = 0; q < NCOPY; ++q) {
-    const int j = NCOPY * wave + q;
-    if (j < 16) {
-      const int r = 16 * j + (lane >> 2);
-      const int c = (lane & 3) ^ ((r >> 2) & 3);
-      int64_t arow = prow[q];
-      if (MODE == MODE_GATE_UP) arow = shared_grp ? (int64_t)(prow[q] - p.P) : (int64_t)(prow[q] / p.topk);
+    const int r = 64 * wave + 16 * q + (lane >> 2);
+    rows[q] = ti.y + (r < ti.z ? r : 0);
+  }
+}
+
+template <int MODE>
+__device__ __forceinline__ void gather_rows(const GemmParams& p, int4 ti, int wave, int lane,
+                                            int (&rows)[NCOPY]) {
+  plain_rows(ti, wave, lane, rows);
+  if (gathered<MODE>(p, ti)) {
+#pragma unroll
+    for (int q = 0; q < NCOPY; ++q) rows[q] = p.perm[rows[q]];
+  }
+}
+
+// Global source of each of this lane's copies for tile `ti`, output-column tile `nt`. Copy q of
+// wave w fills slice rows 64w + 16q + lane/4 (rows < 256: activations, else weights); lane l
+// lands in 16-byte slot l % 4 of its row, which holds chunk (l % 4) ^ ((row >> 2) & 3).
+template <int MODE>
+__device__ __forceinline__ void copy_sources(const GemmParams& p, int4 ti, int nt, int wave,
+                                             int lane, const int (&rows)[NCOPY],
+                                             const uint16_t* (&src)[NCOPY]) {
+  const int K = p.K, N = p.N;
+  const bool shared_grp = ti.x >= p.E;
+#pragma unroll
+  for (int q = 0; q < NCOPY; ++q) {
+    const int r = 64 * wave + 16 * q + (lane >> 2);
+    const int c = (lane & 3) ^ ((r >> 2) & 3);
+    if (wave < 4) {
+      int64_t arow = rows[q];
+      if (MODE == MODE_GATE_UP) arow = shared_grp ? (int64_t)(rows[q] - p.P) : (int64_t)(rows[q] / p.topk);
       src[q] = p.A + arow * K + c * 8;
     } else {
-      const int r = 16 * (j - 16) + (lane >> 2);
-      const int c = (lane & 3) ^ ((r >> 2) & 3);
+      const int rb = r - BM;
       const uint16_t* base;
       int col;
       if (MODE == MODE_GATE_UP) {
-        // Weight rows of wave column w: [32 gate | 32 up] for output columns n0 + 32w + 0..31.
-        const int half = r >> 6, within = r & 63;
-        const bool up = within >= 32;
-        col = n0 + 32 * half + (within & 31);
+        // Weight rows 128 * half + [0, 64): gate, + [64, 128): up, of output columns
+        // nt * 128 + 64 * half + [0, 64).
+        const int half = rb >> 7, within = rb & 127;
+        const bool up = within >= 64;
+        col = nt * 128 + 64 * half + (within & 63);
         if (shared_grp) base = up ? p.Ws_b : p.Ws_a;
-        else base = p.W + (int64_t)grp * 2 * N * K + (up ? (int64_t)N * K : 0);
+        else base = p.W + (int64_t)ti.x * 2 * N * K + (up ? (int64_t)N * K : 0);
       } else {
-        col = n0 + r;
-        base = shared_grp ? p.Ws_a : p.W + (int64_t)grp * N * K;
+        col = nt * BW + rb;
+        base = shared_grp ? p.Ws_a : p.W + (int64_t)ti.x * N * K;
       }
       src[q] = base + (int64_t)(col < N ? col : 0) * K + c * 8;
     }
   }
-  const int dst0 = NCOPY * wave * 16 * BK;  // element offset of this wave's first copy
+}
 
-  f32x16_t acc[2][4];
-#pragma unroll
-  for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[ni][mi][i] = 0.0f;
+// Async global -> LDS copies issued from inline asm: lane l copies 16 (or 4) bytes from gsrc to
+// LDS [lds_wave_base + 16*l] (or + 4*l); M0 holds the wave's LDS base. The compiler's wait
+// analysis mistakes the copy's address register for a destination (its builtin form is followed
+// by vmcnt(0) wherever the register allocator reuses that register) and, for the 4-byte form,
+// treats it as a write to any LDS address; from asm the copies are invisible to it. Their
+// completion is ordered by the explicit vmcnt waits of the slice pipeline (vector memory loads
+// complete in order); a compiler-generated wait for one of its own loads can only count them as
+// further outstanding operations, i.e. wait longer. The s_nop covers the M0-write hazard.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
+}
+__device__ __forceinline__ void dma16(const void* gsrc, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(gsrc)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* gsrc, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 1\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(gsrc)
+               : "memory", "m0");
+}
 
-  const int nk = K / BK;
-#define Q38_ISSUE(KT)                                                                 \
-  do {                                                                                \
-    uint16_t* st_ = ring + ((KT) % NSTAGE) * STAGE_ELEMS + dst0;                      \
-    const int ko_ = (KT) * BK;                                                        \
-    _Pragma("unroll") for (int q_ = 0; q_ < NCOPY; ++q_)                              \
-      load_lds16(src[q_] + ko_, st_ + q_ * 16 * BK);                                  \
+template <int MODE, bool ASYNC_ROWS>
+__global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t ring[NSTAGE * SLICE_ELEMS];
+  // Gather indices of the next tile (perm[row0 + r], r < 256), copied asynchronously with the
+  // slices; activation wave w copies and reads entries [64w, 64w + 64) only.
+  __shared__ __attribute__((aligned(16))) int32_t next_rows[BM];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches, SGPR M0
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lr = lane & 31, lh = lane >> 5;
+
+  const int G = (int)gridDim.x, b = (int)blockIdx.x;
+  const int slot = (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
+  const int used_m = p.tiles != nullptr ? load_uniform(p.ntiles_dev) : p.ntiles_host;
+  const int used = used_m * p.ntiles_n;
+  int L = slot;
+  if (L >= used) return;
+  const int nk = p.K / BK;
+  const int ahead = nk < AHEAD ? nk : AHEAD;  // <= nk: copies run at most one tile ahead
+  // ASYNC_ROWS (K >= 5 slices): the next tile's gather indices are copied to LDS at its
+  // predecessor's slice 0, before that slice's successors, so the in-order wait of slice 2
+  // completes them; they are first read at slice nk - ahead >= 2. Otherwise they are plain loads
+  // (which the compiler waits for, draining the copies in flight): a separate instantiation, so
+  // the main one carries no such load.
+  constexpr bool async_rows = ASYNC_ROWS;
+
+  int4 ti = tile_entry(p, L / p.ntiles_n);
+  int Ln = L + G;
+  int4 tin = Ln < used ? tile_entry(p, Ln / p.ntiles_n) : make_int4(0, 0, 0, 0);
+  int rows[NCOPY], rows_n[NCOPY];
+  const uint16_t* src[NCOPY];
+  const uint16_t* src_n[NCOPY];
+  gather_rows<MODE>(p, ti, wave, lane, rows);
+  // Retire these loads on every path (waves >= 4 never read them); a load left pending in the
+  // compiler's bookkeeping makes it wait for all copies wherever its register is reused.
+  wait_vmcnt0();
+  copy_sources<MODE>(p, ti, L % p.ntiles_n, wave, lane, rows, src);
+#pragma unroll
+  for (int q = 0; q < NCOPY; ++q) {
+    rows_n[q] = 0;
+    src_n[q] = src[q];
+  }
+
+  const int dst0 = 64 * wave * BK;  // element offset of this wave's first copy in a slice
+  const uint32_t ring_lds = lds_addr(ring) + 2 * dst0;
+#define Q38_ISSUE(SLOT, SRC, KS)                                                         \
+  do {                                                                                   \
+    const uint32_t st_ = ring_lds + (uint32_t)(SLOT) * (2 * SLICE_ELEMS);                \
+    const int ko_ = (KS) * BK;                                                           \
+    _Pragma("unroll") for (int q_ = 0; q_ < NCOPY; ++q_)                                 \
+      dma16((SRC)[q_] + ko_, st_ + q_ * (2 * 16 * BK));                                  \
   } while (0)
 
-  // Step kt: wait for this wave's copies of slice kt, barrier (publishes slice kt, retires the
-  // slot of slice kt-1; raw s_barrier, as __syncthreads() would also drain the copy still in
-  // flight), copy slice kt+2 into that slot, multiply slice kt.
-  Q38_ISSUE(0);
-  if (nk > 1) Q38_ISSUE(1);
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    if (kt + 2 < nk) Q38_ISSUE(kt + 2);
-    const uint16_t* as_ = ring + (kt % NSTAGE) * STAGE_ELEMS;
-    const uint16_t* bs_ = as_ + BM * BK;
-    u32x4_t wf[2][2], af[2][4];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int c = 2 * kk + lh;
-#pragma unroll
-      for (int t = 0; t < 2; ++t) wf[kk][t] = ld16(bs_ + swz(64 * wn + 32 * t + lr, c));
-#pragma unroll
-      for (int t = 0; t < 4; ++t) af[kk][t] = ld16(as_ + swz(128 * wm + 32 * t + lr, c));
-    }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi) acc[ni][mi] = mfma32x32x16(wf[kk][ni], af[kk][mi], acc[ni][mi]);
-  }
-#undef Q38_ISSUE
-  __syncthreads();
+  int g = 0;  // this workgroup's running slice number; ring slot g % NSTAGE
+  for (int d = 0; d < ahead; ++d) Q38_ISSUE(d, src, d);
 
-  // Epilogue: per 32-row slab (mi), lanes write runs of 4 columns to a wave-private LDS slab,
-  // then the wave stores whole 16-byte row chunks.
-  constexpr int NW = MODE == MODE_GATE_UP ? 32 : 64;  // output columns per wave
-  constexpr int NT_OUT = NW / 32;                      // 32-column output tiles per wave
-  constexpr int CPR = NW / 8;                          // 16-byte chunks per slab row
-  constexpr int RPI = 64 / CPR;                        // slab rows per store instruction
-  uint16_t* slab = ring + wave * (32 * EPI_PITCH);
-  const int col_wave = n0 + NW * wn;
+  f32x16_t acc[4][2];
+  for (;;) {
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int nt = 0; nt < NT_OUT; ++nt) {
+      for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        uint32_t packed[2];
+        for (int i = 0; i < 16; ++i) acc[t][mi][i] = 0.0f;
+    const bool has_next = Ln < used;
+    const int Lnn = Ln + G;
+    int4 tinn = make_int4(0, 0, 0, 0);
+    const bool active = 64 * wm < ti.z;
+
+    // One tile ahead: the next tile's gather indices; two ahead: its successor's entry. Issued
+    // before slice 0's wait, so in the in-order queue they precede slice 3's copies and the wait
+    // of slice 2 completes them.
+    if (has_next) {
+      if (wave < 4 && gathered<MODE>(p, tin) && async_rows) {
+        const int r = 64 * wave + lane;
+        dma4(p.perm + tin.y + (r < tin.z ? r : 0), lds_addr(next_rows + 64 * wave));
+      }
+      if (Lnn < used) tinn = tile_entry(p, Lnn / p.ntiles_n);
+    }
+
+    // Slice step: wait for this wave's copies of slice g (copies of later slices may stay in
+    // flight: loads complete in order), then barrier: publishes slice g and retires the slot of
+    // slice g - 1, which the next copy refills. Raw s_barrier: __syncthreads() would also drain
+    // the copies in flight. `later` = copies of later slices already issued, in slices.
+#define Q38_WAIT_BARRIER(LATER)                                                            \
+  do {                                                                                     \
+    if ((LATER) >= 2) asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");        \
+    else if ((LATER) == 1) asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");   \
+    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");                     \
+  } while (0)
+#define Q38_COMPUTE()                                                                      \
+  do {                                                                                     \
+    if (active) {                                                                          \
+      const uint16_t* as_ = ring + (g % NSTAGE) * SLICE_ELEMS;                             \
+      const uint16_t* bs_ = as_ + BM * BK;                                                 \
+      u32x4_t wf[2][4], af[2][2];                                                          \
+      _Pragma("unroll") for (int kk = 0; kk < 2; ++kk) {                                   \
+        const int c = 2 * kk + lh;                                                         \
+        _Pragma("unroll") for (int t = 0; t < 4; ++t)                                      \
+          wf[kk][t] = ld16(bs_ + swz(128 * wn + 32 * t + lr, c));                           \
+        _Pragma("unroll") for (int mi = 0; mi < 2; ++mi)                                   \
+          af[kk][mi] = ld16(as_ + swz(64 * wm + 32 * mi + lr, c));                          \
+      }                                                                                    \
+      _Pragma("unroll") for (int kk = 0; kk < 2; ++kk)                                     \
+        _Pragma("unroll") for (int t = 0; t < 4; ++t)                                      \
+          _Pragma("unroll") for (int mi = 0; mi < 2; ++mi)                                 \
+            acc[t][mi] = mfma32x32x16(wf[kk][t], af[kk][mi], acc[t][mi]);                  \
+    }                                                                                      \
+  } while (0)
+
+    // Phase 1: the copy issued at each step is this tile's slice kt + ahead (here ahead == 3,
+    // since nk > ahead).
+    int kt = 0;
+    for (; kt < nk - ahead; ++kt, ++g) {
+      Q38_WAIT_BARRIER(2);
+      Q38_ISSUE((g + ahead) % NSTAGE, src, kt + ahead);
+      Q38_COMPUTE();
+    }
+    // Phase 2 (the last `ahead` slices): the copies run on into the next tile, whose sources
+    // are complete now, or the stream drains after the last tile.
+    if (has_next) {
+      if (async_rows && gathered<MODE>(p, tin)) {
 #pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          uint32_t v2 = 0;
+        for (int q = 0; q < NCOPY; ++q) rows_n[q] = next_rows[(64 * wave + 16 * q + (lane >> 2)) & (BM - 1)];
+      } else if (async_rows) {
+        plain_rows(tin, wave, lane, rows_n);
+      } else {
+        gather_rows<MODE>(p, tin, wave, lane, rows_n);
+      }
+      copy_sources<MODE>(p, tin, Ln % p.ntiles_n, wave, lane, rows_n, src_n);
+    }
+    for (; kt < nk; ++kt, ++g) {
+      Q38_WAIT_BARRIER(has_next ? ahead - 1 : nk - 1 - kt);
+      if (has_next) Q38_ISSUE((g + ahead) % NSTAGE, src_n, kt + ahead - nk);
+      Q38_COMPUTE();
+    }
+#undef Q38_WAIT_BARRIER
+#undef Q38_COMPUTE
+
+    // Epilogue straight from registers. In a 32x32 block lane l holds row l % 32 and 4-column
+    // runs at 8*gq + 4*(l / 32); one permlane32_swap per register pair gives each lane two
+    // 8-column runs (16-byte stores, 32 contiguous bytes per row and instruction). No LDS: an LDS
+    // access here would make the compiler wait for the next tile's copies already in flight.
+    if (active) {
+      constexpr int NT_OUT = MODE == MODE_GATE_UP ? 2 : 4;  // 32-column output blocks per wave
+      const int nt = L % p.ntiles_n;
+      const int col_wave = MODE == MODE_GATE_UP ? nt * 128 + 64 * wn : nt * BW + 128 * wn;
 #pragma unroll
-          for (int e2 = 0; e2 < 2; ++e2) {
-            const int i = 4 * q + 2 * h2 + e2;
-            float v;
-            if (MODE == MODE_GATE_UP) {
-              const float g = round_bf16(acc[0][mi][i]);
-              const float u = round_bf16(acc[1][mi][i]);
-              v = round_bf16(g * __builtin_amdgcn_rcpf(1.0f + __expf(-g))) * u;
-            } else {
-              v = acc[nt][mi][i];
+      for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+        for (int to = 0; to < NT_OUT; ++to) {
+          uint32_t v[4][2];
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+              const int i = 4 * gq + 2 * h2;
+              if (MODE == MODE_GATE_UP) {
+                // Reference rounding (inference.py:90-96): bf16 gate and up, bf16 silu(gate),
+                // bf16 product; each bf16 rounding is one packed RNE conversion of two values.
+                float g0, g1, u0, u1, s0, s1;
+                unpack_bf16x2(pack_bf16x2(acc[to][mi][i], acc[to][mi][i + 1]), g0, g1);
+                unpack_bf16x2(pack_bf16x2(acc[to + 2][mi][i], acc[to + 2][mi][i + 1]), u0, u1);
+                unpack_bf16x2(pack_bf16x2(g0 * __builtin_amdgcn_rcpf(1.0f + __expf(-g0)),
+                                          g1 * __builtin_amdgcn_rcpf(1.0f + __expf(-g1))), s0, s1);
+                v[gq][h2] = pack_bf16x2(s0 * u0, s1 * u1);
+              } else {
+                v[gq][h2] = pack_bf16x2(acc[to][mi][i], acc[to][mi][i + 1]);
+              }
             }
-            v2 |= f32_to_bf16_rne(v) << (16 * e2);
           }
-          packed[h2] = v2;
+          // Lanes 0-31 keep runs gq = 0, 2 and take the upper lanes' (columns +4); lanes 32-63
+          // keep runs gq = 1, 3 and take the lower lanes' (columns -4).
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const auto s01 = __builtin_amdgcn_permlane32_swap(v[0][h2], v[1][h2], false, false);
+            v[0][h2] = s01[0];
+            v[1][h2] = s01[1];
+            const auto s23 = __builtin_amdgcn_permlane32_swap(v[2][h2], v[3][h2], false, false);
+            v[2][h2] = s23[0];
+            v[3][h2] = s23[1];
+          }
+          const int r = 64 * wm + 32 * mi + lr;
+          const int col = col_wave + 32 * to + 8 * lh;
+          if (r < ti.z) {
+            uint16_t* dst = p.C + (int64_t)(ti.y + r) * p.N + col;
+            if (col < p.N) st16(dst, u32x4_t{v[0][0], v[0][1], v[1][0], v[1][1]});
+            if (col + 16 < p.N) st16(dst + 16, u32x4_t{v[2][0], v[2][1], v[3][0], v[3][1]});
+          }
         }
-        const int col = 32 * nt + 8 * q + 4 * lh;
-        *reinterpret_cast<uint2*>(slab + lr * EPI_PITCH + col) = make_uint2(packed[0], packed[1]);
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (!has_next) break;
+    L = Ln;
+    ti = tin;
+    Ln = Lnn;
+    tin = tinn;
 #pragma unroll
-    for (int s = 0; s < 32 / RPI; ++s) {
-      const int rl = s * RPI + lane / CPR;
-      const int cc = (lane % CPR) * 8;
-      const int r = 128 * wm + 32 * mi + rl;
-      const u32x4_t v = ld16(slab + rl * EPI_PITCH + cc);
-      if (r < nrows && col_wave + cc < N) st16(p.C + (int64_t)(row0 + r) * N + col_wave + cc, v);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int q = 0; q < NCOPY; ++q) src[q] = src_n[q];
   }
+#undef Q38_ISSUE
 }
 
 int gemm_block_m() { return BM; }
 
+// One workgroup per CU (the kernel is persistent), never more than there are tiles.
 static unsigned grid_for(int max_mtiles, int ntiles_n) {
-  const int64_t g = (int64_t)max_mtiles * ntiles_n;
-  return (unsigned)((g + 7) / 8 * 8);
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  const int64_t tiles = (int64_t)max_mtiles * ntiles_n;
+  return (unsigned)(tiles < cus[dev] ? tiles : cus[dev]);
 }
 
 hipError_t launch_gate_up(const uint16_t* x, const int32_t* perm, const int4* tiles,
@@ -263,11 +402,15 @@ hipError_t launch_gate_up(const uint16_t* x, const int32_t* perm, const int4* ti
   p.K = K;
   p.E = E;
   p.topk = topk;
-  p.ntiles_n = (N + BN / 2 - 1) / (BN / 2);
+  p.ntiles_n = (N + 127) / 128;
   const int mt = tiles != nullptr ? max_mtiles : p.ntiles_host;
   if (mt == 0) return hipSuccess;
-  hipLaunchKernelGGL(grouped_gemm_kernel<MODE_GATE_UP>, dim3(grid_for(mt, p.ntiles_n)),
-                     dim3(NTHREADS), 0, stream, p);
+  if (K / BK - AHEAD >= 2)
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, true>), dim3(grid_for(mt, p.ntiles_n)),
+                       dim3(NTHREADS), 0, stream, p);
+  else
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, false>), dim3(grid_for(mt, p.ntiles_n)),
+                       dim3(NTHREADS), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -291,11 +434,11 @@ hipError_t launch_down(const uint16_t* H, const int4* tiles, const int32_t* ntil
   p.K = K;
   p.E = E;
   p.topk = 1;
-  p.ntiles_n = (N + BN - 1) / BN;
+  p.ntiles_n = (N + BW - 1) / BW;
   const int mt = tiles != nullptr ? max_mtiles : p.ntiles_host;
   if (mt == 0) return hipSuccess;
-  hipLaunchKernelGGL(grouped_gemm_kernel<MODE_DOWN>, dim3(grid_for(mt, p.ntiles_n)), dim3(NTHREADS),
-                     0, stream, p);
+  hipLaunchKernelGGL((grouped_gemm_kernel<MODE_DOWN, false>), dim3(grid_for(mt, p.ntiles_n)),
+                     dim3(NTHREADS), 0, stream, p);
   return hipGetLastError();
 }
 

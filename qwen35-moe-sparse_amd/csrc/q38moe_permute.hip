@@ -47,6 +47,7 @@ __global__ __launch_bounds__(256) void permute_kernel(
   __shared__ int s_tile0[64];
   __shared__ int s_ntile[64];
   __shared__ int s_wcnt[4][64];
+  __shared__ int s_rem[256];
   __shared__ int s_ids[PERM_TOKENS * PERM_KMAX];
   const int tid = threadIdx.x, e = tid & 63, part = tid >> 6;
   const int b = blockIdx.x;
@@ -98,8 +99,9 @@ __global__ __launch_bounds__(256) void permute_kernel(
     s_start[tid] = st;
     s_total[tid] = t;
     s_base[tid] = st + bf;
-    // Padded tiles per expert and their prefix (the blk_cum of inference.py:176).
-    const int nt = (tid < E) ? (t + block_m - 1) / block_m : 0;
+    // Full tiles per expert and their prefix (the blk_cum of inference.py:176 splits into these
+    // and one partial tile per expert with a remainder).
+    const int nt = (tid < E) ? t / block_m : 0;
     int tincl = nt;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -139,26 +141,47 @@ __global__ __launch_bounds__(256) void permute_kernel(
   }
 
   if (b == 0 && tiles != nullptr) {
-    // Routed tiles by expert, then the shared-expert rows [P, P + shared_rows) in block_m tiles
-    // (group id E), then unused entries {-1, 0, 0, 0}.
-    const int routed_tiles = s_tile0[63] + s_ntile[63];
-    const int shared_tiles = (shared_rows + block_m - 1) / block_m;
+    // Tile table, in the order the persistent grouped GEMM walks it: every full tile (block_m
+    // rows) by expert, then the shared-expert rows [P, P + shared_rows) (group id E), then one
+    // partial tile per group with a remainder, by falling row count (ties: lower group first),
+    // then unused entries {-1, 0, 0, 0}. Cost falls along the list, so round-robin assignment
+    // balances the workgroups.
+    const int routed_full = s_tile0[63] + s_ntile[63];
+    const int shared_full = shared_rows / block_m;
+    const int full = routed_full + shared_full;
     const int64_t P = T * k;
-    if (tid == 0 && tile_count != nullptr) *tile_count = routed_tiles + shared_tiles;
+    // Partial tiles: group g < E from the routed counts, g == E the shared rows.
+    const int g = tid;
+    int rem = 0, row_start = 0;
+    if (g < E) {
+      rem = s_total[g] % block_m;
+      row_start = s_start[g] + s_ntile[g] * block_m;
+    } else if (g == E) {
+      rem = shared_rows % block_m;
+      row_start = (int)P + shared_full * block_m;
+    }
+    s_rem[g] = rem;  // tid < 256 covers g <= E <= 64
+    __syncthreads();
+    int rank = 0, npartial = 0;
+    for (int h = 0; h <= E; ++h) {
+      const int rh = s_rem[h];
+      npartial += rh > 0;
+      rank += rh > 0 && (rh > rem || (rh == rem && h < g));
+    }
+    if (rem > 0) tiles[full + rank] = make_int4(g, row_start, rem, 0);
+    if (tid == 0 && tile_count != nullptr) *tile_count = full + npartial;
     for (int i = tid; i < max_tiles; i += 256) {
+      if (i >= full && i < full + npartial) continue;
       int4 ti = make_int4(-1, 0, 0, 0);
-      if (i >= routed_tiles && i < routed_tiles + shared_tiles) {
-        const int s = i - routed_tiles;
-        ti = make_int4(E, (int)P + s * block_m, min(block_m, shared_rows - s * block_m), 0);
-      } else if (i < routed_tiles) {
+      if (i < routed_full) {
         int lo = 0;
-        // Largest expert whose first tile is <= i and that owns at least one tile.
+        // Largest expert whose first full tile is <= i and that owns at least one.
         for (int ee = 0; ee < E; ++ee) {
           if (s_ntile[ee] > 0 && s_tile0[ee] <= i) lo = ee;
         }
-        const int local = i - s_tile0[lo];
-        const int row0 = s_start[lo] + local * block_m;
-        ti = make_int4(lo, row0, min(block_m, s_total[lo] - local * block_m), 0);
+        ti = make_int4(lo, s_start[lo] + (i - s_tile0[lo]) * block_m, block_m, 0);
+      } else if (i < full) {
+        ti = make_int4(E, (int)P + (i - routed_full) * block_m, block_m, 0);
       }
       tiles[i] = ti;
     }

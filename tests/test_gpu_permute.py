@@ -30,19 +30,14 @@ def _check(idx, E, gpu, shared_rows=0):
     # inv is the inverse permutation on the valid pairs.
     inv_np = inv.cpu().numpy()
     assert np.array_equal(inv_np[rp], np.arange(n))
-    # Tile table: experts ascending, rows tile each expert's segment exactly (padding per expert),
-    # then the shared-expert rows.
+    # Tile table: the BM-row blocks of every expert segment and of the shared rows, full blocks
+    # first, then partial ones by falling size (the oracle's order, bit-exact).
     bm = ops.gemm_block_m()
     tl = tiles.cpu().numpy()
     used = tl[tl[:, 0] >= 0]
     assert int(tile_count.item()) == len(used)
     assert (tl[len(used):, 0] == -1).all(), "unused tiles must follow the used ones"
-    expect = []
-    for e in range(E):
-        for r0 in range(0, int(rc[e]), bm):
-            expect.append((e, int(rs[e]) + r0, min(bm, int(rc[e]) - r0)))
-    for r0 in range(0, shared_rows, bm):
-        expect.append((E, T * k + r0, min(bm, shared_rows - r0)))
+    expect = orc.tile_table(rc, rs, bm, shared_rows, P=T * k)
     assert [tuple(map(int, t[:3])) for t in used] == expect
     return counts, starts, perm
 

@@ -165,3 +165,29 @@ def test_skew_workload_load_span():
     c = np.bincount(idx.reshape(-1).numpy(), minlength=wl.experts)
     assert c.sum() == wl.tokens * wl.topk
     assert 15 <= c.max() / c.min() <= 30, (c.max(), c.min())
+
+
+@pytest.mark.parametrize("seed,bm,shared", [(0, 256, 0), (1, 256, 3000), (2, 64, 17), (3, 128, 256)])
+def test_tile_table_blocks(seed, bm, shared):
+    """tile_table lists exactly the reference's per-expert blocks (inference.py:39-50: block j of
+    expert e covers sorted rows starts[e] + j*BM .. min(+BM, starts[e] + counts[e])), plus the
+    shared rows' blocks, with full blocks first and partial blocks by non-increasing size."""
+    rs = np.random.RandomState(seed)
+    E = 64
+    counts = rs.randint(0, 3 * bm, size=E).astype(np.int32)
+    counts[rs.rand(E) < 0.1] = 0
+    starts = (np.cumsum(counts) - counts).astype(np.int32)
+    P = int(counts.sum())
+    tl = orc.tile_table(counts, starts, bm, shared, P=P)
+    ref = []
+    for e in range(E):
+        for j in range(-(-int(counts[e]) // bm)):
+            r0 = int(starts[e]) + j * bm
+            ref.append((e, r0, min(bm, int(starts[e] + counts[e]) - r0)))
+    for j in range(-(-shared // bm)):
+        ref.append((E, P + j * bm, min(bm, shared - j * bm)))
+    assert sorted(tl) == sorted(ref)
+    sizes = [t[2] for t in tl]
+    nfull = sum(s == bm for s in sizes)
+    assert all(s == bm for s in sizes[:nfull])
+    assert all(a >= b for a, b in zip(sizes[nfull:], sizes[nfull + 1:]))
