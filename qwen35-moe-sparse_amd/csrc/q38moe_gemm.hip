@@ -19,9 +19,10 @@
 // a tile of <= 128 rows costs half a full one.
 //
 // The kernel is persistent: workgroup b walks tiles slot(b), slot(b) + G, ... (G = grid size) of a
-// list the permutation orders full tiles first and partial tiles by falling row count, and its
-// async copy stream (global_load_lds_dwordx4 into a 4-deep LDS ring, three slices ahead) runs on
-// across tile boundaries, so the next tile's first slices load during this tile's epilogue. The
+// list the permutation orders full tiles first and partial tiles by falling row count. Its async
+// copy streams (global_load_lds_dwordx4 into LDS rings: activation rows 5 slices ahead in a
+// 6-slot ring, copied by waves 0-3; weight rows 2 slices ahead in a 3-slot ring, waves 4-7) run
+// on across tile boundaries, so the next tile's first slices load during this tile's epilogue. The
 // next tile's tile entry and row gather indices are fetched one tile ahead. Slots are spread over
 // the 8 XCDs in contiguous runs (workgroup b runs on XCD b % 8 and takes slot (b % 8) * G/8 + b/8),
 // so tiles that share an expert's weights or gathered rows run in one XCD's L2 at the same time.
@@ -36,13 +37,16 @@ namespace q38 {
 constexpr int BM = 256;        // activation rows per tile
 constexpr int BW = 256;        // weight rows per tile
 constexpr int BK = 32;         // K slice
-constexpr int NTHREADS = 512;  // 8 waves
-constexpr int NSTAGE = 4;      // LDS ring of K-slices
-constexpr int AHEAD = 3;       // slices in flight ahead of the one being multiplied
-constexpr int SLICE_ELEMS = (BM + BW) * BK;  // bf16 elements per slice (32 KiB)
-constexpr int NCOPY = (BM + BW) / 16 / 8;    // async copies per lane per slice (16 rows each)
-static_assert(NCOPY == 4, "the vmcnt immediates below assume 4 copies per slice");
-static_assert(AHEAD < NSTAGE, "a slot is refilled only after the barrier that retires it");
+constexpr int NTHREADS = 512;  // 8 waves: 0-3 copy activation rows, 4-7 weight rows
+constexpr int NA = 6;          // activation ring slots: copies run 5 slices ahead
+constexpr int NW = 3;          // weight ring slots: copies run 2 slices ahead
+constexpr int SLOT_ELEMS = 256 * BK;  // one ring slot: 256 rows of one K slice (16 KiB)
+constexpr int NCOPY = 4;       // async copies per lane per slice (16 rows each, 64 rows per wave)
+
+// Destination of the epilogue stores of lanes outside the output (rows past a partial tile,
+// columns past N): garbage, never read. External linkage on purpose: stores into a file-local
+// array nobody reads are dead code to the optimizer, and the slice waits count every one.
+__device__ __attribute__((aligned(16))) u32x4_t q38moe_gemm_store_sink[8 * 64];
 
 enum { MODE_GATE_UP = 0, MODE_DOWN = 1 };
 
@@ -162,16 +166,36 @@ __device__ __forceinline__ void dma4(const void* gsrc, uint32_t lds) {
                : "memory", "m0");
 }
 
+// s_waitcnt vmcnt(n) + s_barrier for a wave-uniform n in [0, 48] (vmcnt takes an immediate).
+__device__ __forceinline__ void wait_vmcnt_barrier(int n) {
+#define Q38_W(N) case N: asm volatile("s_waitcnt vmcnt(" #N ")\n\ts_barrier" ::: "memory"); break;
+  switch (n) {
+    Q38_W(1) Q38_W(2) Q38_W(3) Q38_W(4) Q38_W(5) Q38_W(6) Q38_W(7) Q38_W(8) Q38_W(9) Q38_W(10)
+    Q38_W(11) Q38_W(12) Q38_W(13) Q38_W(14) Q38_W(15) Q38_W(16) Q38_W(17) Q38_W(18) Q38_W(19)
+    Q38_W(20) Q38_W(21) Q38_W(22) Q38_W(23) Q38_W(24) Q38_W(25) Q38_W(26) Q38_W(27) Q38_W(28)
+    Q38_W(29) Q38_W(30) Q38_W(31) Q38_W(32) Q38_W(33) Q38_W(34) Q38_W(35) Q38_W(36) Q38_W(37)
+    Q38_W(38) Q38_W(39) Q38_W(40) Q38_W(41) Q38_W(42) Q38_W(43) Q38_W(44) Q38_W(45) Q38_W(46)
+    Q38_W(47) Q38_W(48)
+    default: asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory"); break;
+  }
+#undef Q38_W
+}
+
 template <int MODE, bool ASYNC_ROWS>
 __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t ring[NSTAGE * SLICE_ELEMS];
-  // Gather indices of the next tile (perm[row0 + r], r < 256), copied asynchronously with the
-  // slices; activation wave w copies and reads entries [64w, 64w + 64) only.
+  // 16-byte stores per wave and tile: 2 per 32x32 output block, 2 x 2 (gate/up) or 2 x 4 blocks.
+  constexpr int EPI_STORES = MODE == MODE_GATE_UP ? 8 : 16;
+  constexpr int NT_OUT = MODE == MODE_GATE_UP ? 2 : 4;  // 32-column output blocks per wave
+  __shared__ __attribute__((aligned(16))) uint16_t ring_a[NA * SLOT_ELEMS];
+  __shared__ __attribute__((aligned(16))) uint16_t ring_w[NW * SLOT_ELEMS];
+  // Gather indices of the next tile (perm[row0 + r], r < 256), copied asynchronously; activation
+  // wave w copies and reads entries [64w, 64w + 64) only.
   __shared__ __attribute__((aligned(16))) int32_t next_rows[BM];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches, SGPR M0
   const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
+  const bool is_a = wave < 4;
 
   const int G = (int)gridDim.x, b = (int)blockIdx.x;
   const int slot = (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
@@ -180,10 +204,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
   int L = slot;
   if (L >= used) return;
   const int nk = p.K / BK;
-  const int ahead = nk < AHEAD ? nk : AHEAD;  // <= nk: copies run at most one tile ahead
-  // ASYNC_ROWS (K >= 5 slices): the next tile's gather indices are copied to LDS at its
-  // predecessor's slice 0, before that slice's successors, so the in-order wait of slice 2
-  // completes them; they are first read at slice nk - ahead >= 2. Otherwise they are plain loads
+  // This wave's copy distance and ring: activation rows (gathered, farther away in the memory
+  // hierarchy) run 5 slices ahead, weight rows (shared by the concurrent tiles of an expert,
+  // mostly L2 hits) 2. Each wave waits only for its own copies (vmcnt counts per wave), so the
+  // two streams do not hold each other up.
+  const int ring_n = is_a ? NA : NW;
+  const int dist = min(ring_n - 1, nk);  // <= nk: copies run at most one tile ahead
+  // ASYNC_ROWS (K >= 11 slices): the next tile's gather indices are copied to LDS before this
+  // tile's slice-0 wait, behind the copies of slices 0-4, so the in-order wait of slice 5
+  // completes them; they are read after the wait of slice nk - 6 >= 5. Otherwise they are plain
+  // loads there
   // (which the compiler waits for, draining the copies in flight): a separate instantiation, so
   // the main one carries no such load.
   constexpr bool async_rows = ASYNC_ROWS;
@@ -205,20 +235,23 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
     src_n[q] = src[q];
   }
 
-  const int dst0 = 64 * wave * BK;  // element offset of this wave's first copy in a slice
-  const uint32_t ring_lds = lds_addr(ring) + 2 * dst0;
+  // This wave's 64 rows of a slot: activation rows 64w.. of ring_a, weight rows 64(w-4).. of ring_w.
+  const uint32_t my_ring = is_a ? lds_addr(ring_a) + 2 * 64 * wave * BK : lds_addr(ring_w) + 2 * 64 * (wave - 4) * BK;
 #define Q38_ISSUE(SLOT, SRC, KS)                                                         \
   do {                                                                                   \
-    const uint32_t st_ = ring_lds + (uint32_t)(SLOT) * (2 * SLICE_ELEMS);                \
+    const uint32_t st_ = my_ring + (uint32_t)(SLOT) * (2 * SLOT_ELEMS);                  \
     const int ko_ = (KS) * BK;                                                           \
     _Pragma("unroll") for (int q_ = 0; q_ < NCOPY; ++q_)                                 \
       dma16((SRC)[q_] + ko_, st_ + q_ * (2 * 16 * BK));                                  \
   } while (0)
 
-  int g = 0;  // this workgroup's running slice number; ring slot g % NSTAGE
-  for (int d = 0; d < ahead; ++d) Q38_ISSUE(d, src, d);
+  uint16_t* const sink = reinterpret_cast<uint16_t*>(q38moe_gemm_store_sink + 64 * wave + lane);
+  for (int d = 0; d < dist; ++d) Q38_ISSUE(d, src, d);
+  int fill = dist;  // ring slot of the next copy: (slice + dist) % ring_n
+  int ra = 0, rw = 0;  // ring_a / ring_w slots of the slice being multiplied
 
   f32x16_t acc[4][2];
+  int stores_prev = 0;  // epilogue stores this wave issued at the previous tile's end
   for (;;) {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -230,33 +263,43 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
     const int Lnn = Ln + G;
     int4 tinn = make_int4(0, 0, 0, 0);
     const bool active = 64 * wm < ti.z;
+    const bool next_async = has_next && async_rows && gathered<MODE>(p, tin);
 
-    // One tile ahead: the next tile's gather indices; two ahead: its successor's entry. Issued
-    // before slice 0's wait, so in the in-order queue they precede slice 3's copies and the wait
-    // of slice 2 completes them.
+    // One tile ahead: the next tile's gather indices; two ahead: its successor's entry.
     if (has_next) {
-      if (wave < 4 && gathered<MODE>(p, tin) && async_rows) {
+      if (next_async && is_a) {
         const int r = 64 * wave + lane;
         dma4(p.perm + tin.y + (r < tin.z ? r : 0), lds_addr(next_rows + 64 * wave));
       }
       if (Lnn < used) tinn = tile_entry(p, Lnn / p.ntiles_n);
     }
 
-    // Slice step: wait for this wave's copies of slice g (copies of later slices may stay in
-    // flight: loads complete in order), then barrier: publishes slice g and retires the slot of
-    // slice g - 1, which the next copy refills. Raw s_barrier: __syncthreads() would also drain
-    // the copies in flight. `later` = copies of later slices already issued, in slices.
-#define Q38_WAIT_BARRIER(LATER)                                                            \
+    // Step: wait until at most N of this wave's vector-memory operations are outstanding, which
+    // completes its copies of the current slice (loads complete in order; N counts what was
+    // issued after them: 4 per later slice already copied, plus, during the first `dist` steps,
+    // the previous tile's epilogue stores, which follow those copies in the queue; the next
+    // tile's gather-index copy is one more, not counted: a longer wait), then barrier: publishes
+    // the slice and retires the slots of the previous one, which the next copies refill. Raw
+    // s_barrier: __syncthreads() would also drain the copies in flight.
+#define Q38_STORES_AFTER(KT) ((KT) < dist ? stores_prev : 0)
+#define Q38_WAIT_BARRIER(N) wait_vmcnt_barrier(N)
+#define Q38_NEXT_SOURCES()                                                                 \
   do {                                                                                     \
-    if ((LATER) >= 2) asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");        \
-    else if ((LATER) == 1) asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");   \
-    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");                     \
+    if (is_a && next_async) {                                                              \
+      _Pragma("unroll") for (int q = 0; q < NCOPY; ++q)                                    \
+        rows_n[q] = next_rows[(64 * wave + 16 * q + (lane >> 2)) & (BM - 1)];              \
+    } else if (!is_a || async_rows || !gathered<MODE>(p, tin)) {                           \
+      plain_rows(tin, wave, lane, rows_n);                                                 \
+    } else {                                                                               \
+      gather_rows<MODE>(p, tin, wave, lane, rows_n);                                       \
+    }                                                                                      \
+    copy_sources<MODE>(p, tin, Ln % p.ntiles_n, wave, lane, rows_n, src_n);                \
   } while (0)
 #define Q38_COMPUTE()                                                                      \
   do {                                                                                     \
     if (active) {                                                                          \
-      const uint16_t* as_ = ring + (g % NSTAGE) * SLICE_ELEMS;                             \
-      const uint16_t* bs_ = as_ + BM * BK;                                                 \
+      const uint16_t* as_ = ring_a + ra * SLOT_ELEMS;                                      \
+      const uint16_t* bs_ = ring_w + rw * SLOT_ELEMS;                                      \
       u32x4_t wf[2][4], af[2][2];                                                          \
       _Pragma("unroll") for (int kk = 0; kk < 2; ++kk) {                                   \
         const int c = 2 * kk + lh;                                                         \
@@ -270,45 +313,45 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
           _Pragma("unroll") for (int mi = 0; mi < 2; ++mi)                                 \
             acc[t][mi] = mfma32x32x16(wf[kk][t], af[kk][mi], acc[t][mi]);                  \
     }                                                                                      \
+    ra = ra + 1 == NA ? 0 : ra + 1;                                                        \
+    rw = rw + 1 == NW ? 0 : rw + 1;                                                        \
+    fill = fill + 1 == ring_n ? 0 : fill + 1;                                              \
   } while (0)
 
-    // Phase 1: the copy issued at each step is this tile's slice kt + ahead (here ahead == 3,
-    // since nk > ahead).
+    // Phase 1: this wave's copy at step kt is this tile's slice kt + dist.
+    const int p1 = nk - dist;
+    const int head = min(dist, p1);
     int kt = 0;
-    for (; kt < nk - ahead; ++kt, ++g) {
-      Q38_WAIT_BARRIER(2);
-      Q38_ISSUE((g + ahead) % NSTAGE, src, kt + ahead);
+    for (; kt < head; ++kt) {
+      Q38_WAIT_BARRIER(4 * (dist - 1) + Q38_STORES_AFTER(kt));
+      Q38_ISSUE(fill, src, kt + dist);
       Q38_COMPUTE();
     }
-    // Phase 2 (the last `ahead` slices): the copies run on into the next tile, whose sources
-    // are complete now, or the stream drains after the last tile.
-    if (has_next) {
-      if (async_rows && gathered<MODE>(p, tin)) {
-#pragma unroll
-        for (int q = 0; q < NCOPY; ++q) rows_n[q] = next_rows[(64 * wave + 16 * q + (lane >> 2)) & (BM - 1)];
-      } else if (async_rows) {
-        plain_rows(tin, wave, lane, rows_n);
-      } else {
-        gather_rows<MODE>(p, tin, wave, lane, rows_n);
-      }
-      copy_sources<MODE>(p, tin, Ln % p.ntiles_n, wave, lane, rows_n, src_n);
+    for (; kt < p1; ++kt) {
+      Q38_WAIT_BARRIER(4 * (dist - 1));
+      Q38_ISSUE(fill, src, kt + dist);
+      Q38_COMPUTE();
     }
-    for (; kt < nk; ++kt, ++g) {
-      Q38_WAIT_BARRIER(has_next ? ahead - 1 : nk - 1 - kt);
-      if (has_next) Q38_ISSUE((g + ahead) % NSTAGE, src_n, kt + ahead - nk);
+    // Phase 2 (this wave's last `dist` steps): the copies run on into the next tile, or the
+    // stream drains after the last tile.
+    if (has_next) Q38_NEXT_SOURCES();
+    for (; kt < nk; ++kt) {
+      Q38_WAIT_BARRIER(4 * (has_next ? dist - 1 : nk - 1 - kt) + Q38_STORES_AFTER(kt));
+      if (has_next) Q38_ISSUE(fill, src_n, kt + dist - nk);
       Q38_COMPUTE();
     }
 #undef Q38_WAIT_BARRIER
+#undef Q38_STORES_AFTER
+#undef Q38_NEXT_SOURCES
 #undef Q38_COMPUTE
 
     // Epilogue straight from registers. In a 32x32 block lane l holds row l % 32 and 4-column
     // runs at 8*gq + 4*(l / 32); one permlane32_swap per register pair gives each lane two
     // 8-column runs (16-byte stores, 32 contiguous bytes per row and instruction). No LDS: an LDS
     // access here would make the compiler wait for the next tile's copies already in flight.
+    const int nt = L % p.ntiles_n;
+    const int col_wave = MODE == MODE_GATE_UP ? nt * 128 + 64 * wn : nt * BW + 128 * wn;
     if (active) {
-      constexpr int NT_OUT = MODE == MODE_GATE_UP ? 2 : 4;  // 32-column output blocks per wave
-      const int nt = L % p.ntiles_n;
-      const int col_wave = MODE == MODE_GATE_UP ? nt * 128 + 64 * wn : nt * BW + 128 * wn;
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
@@ -344,16 +387,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
             v[2][h2] = s23[0];
             v[3][h2] = s23[1];
           }
+          // Every lane stores (lanes past the tile's rows or columns into the sink), so each
+          // wave issues exactly EPI_STORES stores per tile, which the slice waits count.
           const int r = 64 * wm + 32 * mi + lr;
           const int col = col_wave + 32 * to + 8 * lh;
-          if (r < ti.z) {
-            uint16_t* dst = p.C + (int64_t)(ti.y + r) * p.N + col;
-            if (col < p.N) st16(dst, u32x4_t{v[0][0], v[0][1], v[1][0], v[1][1]});
-            if (col + 16 < p.N) st16(dst + 16, u32x4_t{v[2][0], v[2][1], v[3][0], v[3][1]});
-          }
+          uint16_t* dst = p.C + (int64_t)(ti.y + r) * p.N + col;
+          st16(r < ti.z && col < p.N ? dst : sink, u32x4_t{v[0][0], v[0][1], v[1][0], v[1][1]});
+          st16(r < ti.z && col + 16 < p.N ? dst + 16 : sink, u32x4_t{v[2][0], v[2][1], v[3][0], v[3][1]});
         }
       }
     }
+    stores_prev = active ? EPI_STORES : 0;
     if (!has_next) break;
     L = Ln;
     ti = tin;
@@ -363,6 +407,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
     for (int q = 0; q < NCOPY; ++q) src[q] = src_n[q];
   }
 #undef Q38_ISSUE
+  // No LDS copy may still be landing when the workgroup's LDS is released.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 int gemm_block_m() { return BM; }
@@ -405,12 +451,11 @@ hipError_t launch_gate_up(const uint16_t* x, const int32_t* perm, const int4* ti
   p.ntiles_n = (N + 127) / 128;
   const int mt = tiles != nullptr ? max_mtiles : p.ntiles_host;
   if (mt == 0) return hipSuccess;
-  if (K / BK - AHEAD >= 2)
-    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, true>), dim3(grid_for(mt, p.ntiles_n)),
-                       dim3(NTHREADS), 0, stream, p);
+  const dim3 grid(grid_for(mt, p.ntiles_n));
+  if (K / BK >= 2 * (NA - 1) + 1)
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, true>), grid, dim3(NTHREADS), 0, stream, p);
   else
-    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, false>), dim3(grid_for(mt, p.ntiles_n)),
-                       dim3(NTHREADS), 0, stream, p);
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, false>), grid, dim3(NTHREADS), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -437,8 +482,8 @@ hipError_t launch_down(const uint16_t* H, const int4* tiles, const int32_t* ntil
   p.ntiles_n = (N + BW - 1) / BW;
   const int mt = tiles != nullptr ? max_mtiles : p.ntiles_host;
   if (mt == 0) return hipSuccess;
-  hipLaunchKernelGGL((grouped_gemm_kernel<MODE_DOWN, false>), dim3(grid_for(mt, p.ntiles_n)),
-                     dim3(NTHREADS), 0, stream, p);
+  const dim3 grid(grid_for(mt, p.ntiles_n));
+  hipLaunchKernelGGL((grouped_gemm_kernel<MODE_DOWN, false>), grid, dim3(NTHREADS), 0, stream, p);
   return hipGetLastError();
 }
 
