@@ -39,31 +39,32 @@ __global__ __launch_bounds__(256) void permute_kernel(
     int nblk, int32_t* __restrict__ counts, int32_t* __restrict__ starts,
     int32_t* __restrict__ perm, int32_t* __restrict__ inv, int4* __restrict__ tiles,
     int32_t* __restrict__ tile_count, int block_m, int max_tiles, int shared_rows) {
+  constexpr int NCHUNK = PERM_TOKENS * PERM_KMAX / 64;  // 64-pair chunks per block (<= 8)
   __shared__ int s_tot[4][64];
   __shared__ int s_bef[4][64];
-  __shared__ int s_base[64];
   __shared__ int s_start[64];
   __shared__ int s_total[64];
   __shared__ int s_tile0[64];
   __shared__ int s_ntile[64];
-  __shared__ int s_wcnt[4][64];
+  __shared__ int s_ccnt[NCHUNK][64];  // pairs per expert in each chunk, then the chunk's offsets
   __shared__ int s_rem[256];
-  __shared__ int s_ids[PERM_TOKENS * PERM_KMAX];
   const int tid = threadIdx.x, e = tid & 63, part = tid >> 6;
+  const int lane = e, wave = part;
   const int b = blockIdx.x;
+  for (int i = tid; i < NCHUNK * 64; i += 256) (&s_ccnt[0][0])[i] = 0;
 
   // Expert totals over all blocks and the counts of the blocks before this one. Thread `tid`
-  // sums column e = tid & 63 over rows part, part + 4, ...; eight independent loads are in flight
-  // per step.
+  // sums column e over rows part, part + 4, ...; 16 independent loads are in flight per step
+  // (a wave's load is one contiguous 256-byte row).
   int tot = 0, bef = 0;
   if (e < E) {
     int bb = part;
-    for (; bb + 28 < nblk; bb += 32) {
-      int c[8];
+    for (; bb + 60 < nblk; bb += 64) {
+      int c[16];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) c[u] = hist[(int64_t)(bb + 4 * u) * E + e];
+      for (int u = 0; u < 16; ++u) c[u] = hist[(int64_t)(bb + 4 * u) * E + e];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < 16; ++u) {
         tot += c[u];
         if (bb + 4 * u < b) bef += c[u];
       }
@@ -76,13 +77,38 @@ __global__ __launch_bounds__(256) void permute_kernel(
   }
   s_tot[part][e] = tot;
   s_bef[part][e] = bef;
+
+  // This block's pairs in chunks of 64 (pair p0 + 64c + lane), chunk c on wave c % 4. A pair's
+  // rank among the earlier pairs of its chunk with the same expert is a popcount of the lanes
+  // below it in the mask of equal ids, built from one ballot per id bit (ids 0..63, 64 = dropped:
+  // out of range or past the block's pairs, like transformers' grouped_mm, moe.py:405-420).
   const int64_t t0 = (int64_t)b * PERM_TOKENS;
   const int64_t t1 = min(t0 + PERM_TOKENS, T);
   const int np = (int)((t1 - t0) * k);
   const int64_t p0 = t0 * k;
-  for (int i = tid; i < np; i += 256) {
-    const int64_t v = (int64_t)idx[p0 + i];
-    s_ids[i] = (v >= 0 && v < E) ? (int)v : -1;
+  const int nchunk = (np + 63) / 64;
+  int cv[2], crank[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = wave + 4 * j;
+    cv[j] = 64;
+    crank[j] = 0;
+    if (c < nchunk) {  // wave-uniform
+      const int i = 64 * c + lane;
+      if (i < np) {
+        const int64_t v = (int64_t)idx[p0 + i];
+        if (v >= 0 && v < E) cv[j] = (int)v;
+      }
+      uint64_t same = ~0ull;
+#pragma unroll
+      for (int bit = 0; bit < 7; ++bit) {
+        const bool on = (cv[j] >> bit) & 1;
+        const uint64_t m = ballot64(on);
+        same &= on ? m : ~m;
+      }
+      crank[j] = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
+      if (cv[j] < 64 && crank[j] == 0) s_ccnt[c][cv[j]] = __popcll(same);
+    }
   }
   __syncthreads();
 
@@ -98,7 +124,14 @@ __global__ __launch_bounds__(256) void permute_kernel(
     const int st = incl - t;
     s_start[tid] = st;
     s_total[tid] = t;
-    s_base[tid] = st + bf;
+    // Offset of each chunk's first pair of expert tid: this block's base (the stable counting
+    // sort's position), plus the pairs of the block's earlier chunks.
+    int off = st + bf;
+    for (int c = 0; c < nchunk; ++c) {
+      const int n = s_ccnt[c][tid];
+      s_ccnt[c][tid] = off;
+      off += n;
+    }
     // Full tiles per expert and their prefix (the blk_cum of inference.py:176 splits into these
     // and one partial tile per expert with a remainder).
     const int nt = (tid < E) ? t / block_m : 0;
@@ -115,27 +148,20 @@ __global__ __launch_bounds__(256) void permute_kernel(
       starts[tid] = st;
     }
   }
-  // Stable scatter: wave `part` owns a contiguous segment of this block's pairs.
-  const int seg = (np + 3) / 4;
-  const int s0 = min(part * seg, np), s1 = min(s0 + seg, np);
-  int cnt = 0;
-  if (e < E) {
-    for (int i = s0; i < s1; ++i) cnt += (s_ids[i] == e);
-  }
-  s_wcnt[part][e] = cnt;
   __syncthreads();
-  if (e < E) {
-    int off = s_base[e];
-    for (int w = 0; w < part; ++w) off += s_wcnt[w][e];
-    // perm holds T*k entries; the bound only matters for a hist inconsistent with idx.
-    const int64_t cap = T * k;
-    for (int i = s0; i < s1; ++i) {
-      if (s_ids[i] == e) {
-        if (off < cap) {
-          perm[off] = (int32_t)(p0 + i);
-          if (inv != nullptr) inv[p0 + i] = off;
-        }
-        ++off;
+
+  // Scatter: perm[off] = pair, inv[pair] = off. perm holds T*k entries; the bound only matters
+  // for a hist inconsistent with idx.
+  const int64_t cap = T * k;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = wave + 4 * j;
+    if (c < nchunk && cv[j] < 64) {
+      const int off = s_ccnt[c][cv[j]] + crank[j];
+      const int64_t pair = p0 + 64 * c + lane;
+      if (off < cap) {
+        perm[off] = (int32_t)pair;
+        if (inv != nullptr) inv[pair] = off;
       }
     }
   }
@@ -170,21 +196,14 @@ __global__ __launch_bounds__(256) void permute_kernel(
     }
     if (rem > 0) tiles[full + rank] = make_int4(g, row_start, rem, 0);
     if (tid == 0 && tile_count != nullptr) *tile_count = full + npartial;
-    for (int i = tid; i < max_tiles; i += 256) {
-      if (i >= full && i < full + npartial) continue;
-      int4 ti = make_int4(-1, 0, 0, 0);
-      if (i < routed_full) {
-        int lo = 0;
-        // Largest expert whose first full tile is <= i and that owns at least one.
-        for (int ee = 0; ee < E; ++ee) {
-          if (s_ntile[ee] > 0 && s_tile0[ee] <= i) lo = ee;
-        }
-        ti = make_int4(lo, s_start[lo] + (i - s_tile0[lo]) * block_m, block_m, 0);
-      } else if (i < full) {
-        ti = make_int4(E, (int)P + (i - routed_full) * block_m, block_m, 0);
-      }
-      tiles[i] = ti;
+    // Expert g's full tiles.
+    if (g < E) {
+      for (int j = 0; j < s_ntile[g]; ++j)
+        tiles[s_tile0[g] + j] = make_int4(g, s_start[g] + j * block_m, block_m, 0);
     }
+    for (int i = routed_full + tid; i < full; i += 256)
+      tiles[i] = make_int4(E, (int)P + (i - routed_full) * block_m, block_m, 0);
+    for (int i = full + npartial + tid; i < max_tiles; i += 256) tiles[i] = make_int4(-1, 0, 0, 0);
   }
 }
 
