@@ -341,12 +341,38 @@ constexpr int ROUTE_WROWS = 65;    // 64 expert rows + the shared-expert gate ro
 // current K chunk stored at slot c ^ (n & 15): the 16 rows of a B fragment read distinct banks.
 __device__ __forceinline__ int wr_slot(int n, int c) { return n * (ROUTE_KCHUNK / 8) + (c ^ (n & 15)); }
 
-// Per-token selection by one lane: top-(KP1) insertion list over the token's E values. Returns
-// false when the k+1 largest values are not all distinct (or the row has NaN / non-finite max);
-// such tokens need the libstdc++ replay.
+// Insert (z, e) into a descending top-KP1 list (strictly greater values move up; equal values
+// stay behind the ones already there).
 template <int KP1>
-__device__ __forceinline__ bool lane_select(const float* row, const float* bias, int E, int k,
-                                            int* out_idx, float* out_w) {
+__device__ __forceinline__ void list_insert(float (&v)[KP1], int (&id)[KP1], float z, int e) {
+  if (z > v[KP1 - 1]) {
+    v[KP1 - 1] = z;
+    id[KP1 - 1] = e;
+#pragma unroll
+    for (int r = KP1 - 1; r > 0; --r) {
+      if (v[r] > v[r - 1]) {
+        const float tv = v[r];
+        v[r] = v[r - 1];
+        v[r - 1] = tv;
+        const int ti = id[r];
+        id[r] = id[r - 1];
+        id[r - 1] = ti;
+      }
+    }
+  }
+}
+
+constexpr int SEL_LANES = 4;  // lanes per token in the selection fast path
+
+// Per-token selection by a group of SEL_LANES lanes (lane s of the group holds experts s,
+// s + SEL_LANES, ...): a top-(KP1) list per lane, merged across the group by xor-shuffles.
+// Returns false when the k+1 largest values are not all distinct (or the row has NaN /
+// non-finite max); such tokens need the libstdc++ replay. Every lane of the group returns the
+// same answer.
+template <int KP1>
+__device__ __forceinline__ bool group_select(const float* row, const float* bias, int E, int k, int s,
+                                             int* out_idx, float* out_w) {
+  constexpr int PER = 64 / SEL_LANES;
   float v[KP1];
   int id[KP1];
 #pragma unroll
@@ -354,42 +380,44 @@ __device__ __forceinline__ bool lane_select(const float* row, const float* bias,
     v[r] = -INFINITY;
     id[r] = -1;
   }
-  bool nan = false;
-  for (int e = 0; e < E; ++e) {
-    float z = row[e] + (bias != nullptr ? bias[e] : 0.0f);
-    z = z + 0.0f;
-    nan |= __builtin_isnan(z);
-    if (z > v[KP1 - 1]) {
-      v[KP1 - 1] = z;
-      id[KP1 - 1] = e;
+  float z[PER];
+  int nan = 0;
 #pragma unroll
-      for (int r = KP1 - 1; r > 0; --r) {
-        if (v[r] > v[r - 1]) {
-          const float tv = v[r];
-          v[r] = v[r - 1];
-          v[r - 1] = tv;
-          const int ti = id[r];
-          id[r] = id[r - 1];
-          id[r - 1] = ti;
-        }
-      }
+  for (int j = 0; j < PER; ++j) {
+    const int e = s + SEL_LANES * j;
+    z[j] = -INFINITY;
+    if (e < E) {
+      z[j] = row[e] + (bias != nullptr ? bias[e] : 0.0f) + 0.0f;
+      nan |= __builtin_isnan(z[j]);
+      list_insert<KP1>(v, id, z[j], e);
     }
+  }
+#pragma unroll
+  for (int o = 1; o < SEL_LANES; o <<= 1) {
+    float ov[KP1];
+    int oid[KP1];
+#pragma unroll
+    for (int r = 0; r < KP1; ++r) {
+      ov[r] = __shfl_xor(v[r], o);
+      oid[r] = __shfl_xor(id[r], o);
+    }
+    nan |= __shfl_xor(nan, o);
+#pragma unroll
+    for (int r = 0; r < KP1; ++r) list_insert<KP1>(v, id, ov[r], oid[r]);
   }
   const float m = v[0];
   if (nan || !__builtin_isfinite(m)) return false;
-  const bool partial = k * 64 <= E;  // std::partial_sort path: lowest-index maximum (k == 1)
-  if (!partial) {
-    const int lim = min(k, E - 1);
+  const int lim = min(k, E - 1);
 #pragma unroll
-    for (int r = 0; r < KP1 - 1; ++r)
-      if (r < lim && v[r] == v[r + 1]) return false;
-  }
-  float s = 0.0f;
-  for (int e = 0; e < E; ++e) {
-    const float z = row[e] + (bias != nullptr ? bias[e] : 0.0f);
-    s += expf(z - m);
-  }
-  const float inv = 1.0f / s;
+  for (int r = 0; r < KP1 - 1; ++r)
+    if (r < lim && v[r] == v[r + 1]) return false;
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    if (s + SEL_LANES * j < E) sum += expf(z[j] - m);
+#pragma unroll
+  for (int o = 1; o < SEL_LANES; o <<= 1) sum += __shfl_xor(sum, o);
+  const float inv = 1.0f / sum;
   float pr[KP1];
   float tot = 0.0f;
 #pragma unroll
@@ -407,23 +435,23 @@ __device__ __forceinline__ bool lane_select(const float* row, const float* bias,
   return true;
 }
 
-__device__ bool lane_select_k(const float* row, const float* bias, int E, int k, int* oi, float* ow) {
+__device__ bool group_select_k(const float* row, const float* bias, int E, int k, int s, int* oi, float* ow) {
   switch (k) {
-    case 1: return lane_select<2>(row, bias, E, k, oi, ow);
-    case 2: return lane_select<3>(row, bias, E, k, oi, ow);
-    case 3: return lane_select<4>(row, bias, E, k, oi, ow);
-    case 4: return lane_select<5>(row, bias, E, k, oi, ow);
-    case 5: return lane_select<6>(row, bias, E, k, oi, ow);
-    case 6: return lane_select<7>(row, bias, E, k, oi, ow);
-    case 7: return lane_select<8>(row, bias, E, k, oi, ow);
-    default: return lane_select<9>(row, bias, E, k, oi, ow);
+    case 1: return group_select<2>(row, bias, E, k, s, oi, ow);
+    case 2: return group_select<3>(row, bias, E, k, s, oi, ow);
+    case 3: return group_select<4>(row, bias, E, k, s, oi, ow);
+    case 4: return group_select<5>(row, bias, E, k, s, oi, ow);
+    case 5: return group_select<6>(row, bias, E, k, s, oi, ow);
+    case 6: return group_select<7>(row, bias, E, k, s, oi, ow);
+    case 7: return group_select<8>(row, bias, E, k, s, oi, ow);
+    default: return group_select<9>(row, bias, E, k, s, oi, ow);
   }
 }
 
 // One block = 64 tokens. Phase 1: logits on 16x16x32 MFMA, router weights (+ the shared-expert
 // gate row as column 64) staged in LDS per 1024-wide K chunk, each wave's 16 x rows loaded
 // straight into registers with the whole chunk in flight. Phase 2: bf16-rounded logits to LDS.
-// Phase 3: one lane per token selects top-k (unique answer when the k+1 largest values are
+// Phase 3: four lanes per token select top-k (unique answer when the k+1 largest values are
 // distinct). Phase 4: tokens with ties are replayed wave-parallel through libstdc++'s algorithm.
 __global__ __launch_bounds__(256) void route_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
@@ -524,20 +552,25 @@ __global__ __launch_bounds__(256) void route_kernel(
     if (t < T) gate_out[t] = (uint16_t)f32_to_bf16_rne(s_logit[tid][64]);
   }
 
-  // Phase 3: one lane per token.
-  if (wave == 0) {
-    const int64_t t = tb + lane;
-    if (t < T) {
+  // Phase 3: SEL_LANES lanes per token (token wave * 16 + lane / SEL_LANES).
+  {
+    const int tl = wave * (64 / SEL_LANES) + lane / SEL_LANES;
+    const int64_t t = tb + tl;
+    if (t < T) {  // uniform over the token's lanes
       int oi[KMAX];
       float ow[KMAX];
-      if (lane_select_k(s_logit[lane], bias != nullptr ? s_bias : nullptr, E, k, oi, ow)) {
-        for (int r = 0; r < k; ++r) {
-          idx_out[t * k + r] = oi[r];
-          w_out[t * k + r] = (uint16_t)f32_to_bf16_rne(ow[r]);
-          atomicAdd(&s_hist[oi[r]], 1);
+      const bool ok = group_select_k(s_logit[tl], bias != nullptr ? s_bias : nullptr, E, k,
+                                     lane % SEL_LANES, oi, ow);
+      if (lane % SEL_LANES == 0) {
+        if (ok) {
+          for (int r = 0; r < k; ++r) {
+            idx_out[t * k + r] = oi[r];
+            w_out[t * k + r] = (uint16_t)f32_to_bf16_rne(ow[r]);
+            atomicAdd(&s_hist[oi[r]], 1);
+          }
+        } else {
+          s_ties[atomicAdd(&s_nties, 1)] = tl;
         }
-      } else {
-        s_ties[atomicAdd(&s_nties, 1)] = lane;
       }
     }
   }
