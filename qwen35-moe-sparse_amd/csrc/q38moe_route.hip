@@ -484,14 +484,18 @@ __global__ __launch_bounds__(256) void route_kernel(
     for (int j = 0; j < 5; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const int64_t trow = tb + wave * 16 + (lane & 15);
     const uint16_t* xa = x + (trow < T ? trow : T - 1) * (int64_t)h + 8 * (lane >> 4);
+    // Tiles of experts >= E (and the gate tile without wsg) multiply LDS rows that are never
+    // filled; their columns are never stored. Computing them keeps the MFMA loop branch-free.
     for (int k0 = 0; k0 < h; k0 += ROUTE_KCHUNK) {
       const int kc = min(ROUTE_KCHUNK, h - k0);  // multiple of 64
       __syncthreads();                            // previous chunk fully consumed
-      // This wave's x rows for the chunk: all loads in flight before the MFMAs.
+      const bool full = kc == ROUTE_KCHUNK;
+      // This wave's x rows for a full chunk: all loads in flight before the MFMAs.
       u32x4_t a[32];
+      if (full) {
 #pragma unroll
-      for (int s = 0; s < 32; ++s)
-        if (s * 32 < kc) a[s] = ld16(xa + k0 + s * 32);
+        for (int s = 0; s < 32; ++s) a[s] = ld16(xa + k0 + s * 32);
+      }
       // Router weights -> LDS by asynchronous copies: one wave instruction fills 64 slots
       // (1 KiB) of a row; lane l takes the 16-byte chunk that the swizzle puts in slot l.
       // A chunk narrower than 512 columns leaves slots past kc/8 unused; their lanes copy chunk 0.
@@ -506,14 +510,22 @@ __global__ __launch_bounds__(256) void route_kernel(
       }
       wait_vmcnt0();
       __syncthreads();
+      if (full) {
 #pragma unroll
-      for (int s = 0; s < 32; ++s) {
-        if (s * 32 < kc) {
+        for (int s = 0; s < 32; ++s) {
           const int c = 4 * s + (lane >> 4);
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (j < ntile) acc[j] = mfma16x16x32(a[s], s_w[wr_slot(16 * j + (lane & 15), c)], acc[j]);
-          if (gate_tile) acc[4] = mfma16x16x32(a[s], s_w[wr_slot(64, c)], acc[4]);
+          for (int j = 0; j < 4; ++j) acc[j] = mfma16x16x32(a[s], s_w[wr_slot(16 * j + (lane & 15), c)], acc[j]);
+          acc[4] = mfma16x16x32(a[s], s_w[wr_slot(64, c)], acc[4]);
+        }
+      } else {
+        // Narrow last chunk (h not a multiple of the chunk): one 32-wide slice at a time.
+        for (int s = 0; s < kc / 32; ++s) {
+          const u32x4_t as = ld16(xa + k0 + s * 32);
+          const int c = 4 * s + (lane >> 4);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[j] = mfma16x16x32(as, s_w[wr_slot(16 * j + (lane & 15), c)], acc[j]);
+          acc[4] = mfma16x16x32(as, s_w[wr_slot(64, c)], acc[4]);
         }
       }
     }
