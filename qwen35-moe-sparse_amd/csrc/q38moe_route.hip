@@ -333,7 +333,7 @@ __device__ void route_token(float z, int lane, int E, int k, bool known_tie, int
   out_w = pr / s;
 }
 
-constexpr int ROUTE_TOKENS = 64;   // per block: 4 waves x 16 tokens
+constexpr int ROUTE_TOKENS = 64;   // per block: 4 MFMA waves x 16 tokens
 constexpr int ROUTE_KCHUNK = 1024; // router-weight K columns staged in LDS at a time
 constexpr int ROUTE_WROWS = 65;    // 64 expert rows + the shared-expert gate row
 
@@ -362,7 +362,7 @@ __device__ __forceinline__ void list_insert(float (&v)[KP1], int (&id)[KP1], flo
   }
 }
 
-constexpr int SEL_LANES = 4;  // lanes per token in the selection fast path
+constexpr int SEL_LANES = 8;  // lanes per token in the selection fast path
 
 // Per-token selection by a group of SEL_LANES lanes (lane s of the group holds experts s,
 // s + SEL_LANES, ...): a top-(KP1) list per lane, merged across the group by xor-shuffles.
@@ -448,12 +448,15 @@ __device__ bool group_select_k(const float* row, const float* bias, int E, int k
   }
 }
 
-// One block = 64 tokens. Phase 1: logits on 16x16x32 MFMA, router weights (+ the shared-expert
-// gate row as column 64) staged in LDS per 1024-wide K chunk, each wave's 16 x rows loaded
-// straight into registers with the whole chunk in flight. Phase 2: bf16-rounded logits to LDS.
-// Phase 3: four lanes per token select top-k (unique answer when the k+1 largest values are
+// One block = 64 tokens, 8 waves. Phase 1: logits on 16x16x32 MFMA (waves 0-3, 16 tokens each),
+// router weights (+ the shared-expert gate row as column 64) staged in LDS per 1024-wide K chunk
+// by all waves, each multiplying wave's 16 x rows loaded straight into registers with the whole
+// chunk in flight. Phase 2: bf16-rounded logits to LDS.
+// Phase 3: eight lanes per token select top-k (unique answer when the k+1 largest values are
 // distinct). Phase 4: tokens with ties are replayed wave-parallel through libstdc++'s algorithm.
-__global__ __launch_bounds__(256) void route_kernel(
+constexpr int ROUTE_THREADS = 512;  // 8 waves: 0-3 multiply, all select and replay ties
+
+__global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
     const uint16_t* __restrict__ wsg, const uint16_t* __restrict__ logits_in,
     const float* __restrict__ bias, uint16_t* __restrict__ logits_out,
@@ -465,8 +468,8 @@ __global__ __launch_bounds__(256) void route_kernel(
   __shared__ int s_hist[64];
   __shared__ int s_ties[ROUTE_TOKENS];
   __shared__ int s_nties;
-  __shared__ float s_sv[4][64];
-  __shared__ int s_si[4][64];
+  __shared__ float s_sv[ROUTE_THREADS / 64][64];
+  __shared__ int s_si[ROUTE_THREADS / 64][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t tb = (int64_t)blockIdx.x * ROUTE_TOKENS;
   if (tid < 64) {
@@ -482,7 +485,8 @@ __global__ __launch_bounds__(256) void route_kernel(
     f32x4_t acc[5];
 #pragma unroll
     for (int j = 0; j < 5; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const int64_t trow = tb + wave * 16 + (lane & 15);
+    const bool mma = wave < 4;
+    const int64_t trow = tb + (wave & 3) * 16 + (lane & 15);
     const uint16_t* xa = x + (trow < T ? trow : T - 1) * (int64_t)h + 8 * (lane >> 4);
     // Tiles of experts >= E (and the gate tile without wsg) multiply LDS rows that are never
     // filled; their columns are never stored. Computing them keeps the MFMA loop branch-free.
@@ -492,7 +496,7 @@ __global__ __launch_bounds__(256) void route_kernel(
       const bool full = kc == ROUTE_KCHUNK;
       // This wave's x rows for a full chunk: all loads in flight before the MFMAs.
       u32x4_t a[32];
-      if (full) {
+      if (full && mma) {
 #pragma unroll
         for (int s = 0; s < 32; ++s) a[s] = ld16(xa + k0 + s * 32);
       }
@@ -500,7 +504,7 @@ __global__ __launch_bounds__(256) void route_kernel(
       // (1 KiB) of a row; lane l takes the 16-byte chunk that the swizzle puts in slot l.
       // A chunk narrower than 512 columns leaves slots past kc/8 unused; their lanes copy chunk 0.
       const int halves = (kc + 511) / 512;        // 1 KiB row segments in this chunk
-      for (int q = wave; q < nrows_w * halves; q += 4) {
+      for (int q = wave; q < nrows_w * halves; q += ROUTE_THREADS / 64) {
         const int n = q / halves, part = q - n * halves;
         const uint16_t* src = n < 64 ? (n < E ? wr + (int64_t)n * h : nullptr) : wsg;
         if (src != nullptr) {
@@ -510,7 +514,7 @@ __global__ __launch_bounds__(256) void route_kernel(
       }
       wait_vmcnt0();
       __syncthreads();
-      if (full) {
+      if (full && mma) {
 #pragma unroll
         for (int s = 0; s < 32; ++s) {
           const int c = 4 * s + (lane >> 4);
@@ -518,7 +522,7 @@ __global__ __launch_bounds__(256) void route_kernel(
           for (int j = 0; j < 4; ++j) acc[j] = mfma16x16x32(a[s], s_w[wr_slot(16 * j + (lane & 15), c)], acc[j]);
           acc[4] = mfma16x16x32(a[s], s_w[wr_slot(64, c)], acc[4]);
         }
-      } else {
+      } else if (mma) {
         // Narrow last chunk (h not a multiple of the chunk): one 32-wide slice at a time.
         for (int s = 0; s < kc / 32; ++s) {
           const u32x4_t as = ld16(xa + k0 + s * 32);
@@ -531,7 +535,7 @@ __global__ __launch_bounds__(256) void route_kernel(
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      if (j < ntile) {
+      if (mma && j < ntile) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int col = 16 * j + (lane & 15);
@@ -539,12 +543,12 @@ __global__ __launch_bounds__(256) void route_kernel(
         }
       }
     }
-    if (gate_tile && (lane & 15) == 0) {
+    if (mma && gate_tile && (lane & 15) == 0) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) s_logit[wave * 16 + 4 * (lane >> 4) + i][64] = round_bf16(acc[4][i]);
     }
   } else {
-    for (int i = tid; i < ROUTE_TOKENS * E; i += 256) {
+    for (int i = tid; i < ROUTE_TOKENS * E; i += ROUTE_THREADS) {
       const int tl = i / E, e = i - tl * E;
       const int64_t t = tb + tl;
       s_logit[tl][e] = t < T ? bf16_to_f32(logits_in[t * E + e]) : 0.0f;
@@ -553,7 +557,7 @@ __global__ __launch_bounds__(256) void route_kernel(
   __syncthreads();
 
   if (logits_out != nullptr && logits_in == nullptr) {
-    for (int i = tid; i < ROUTE_TOKENS * E; i += 256) {
+    for (int i = tid; i < ROUTE_TOKENS * E; i += ROUTE_THREADS) {
       const int tl = i / E, e = i - tl * E;
       const int64_t t = tb + tl;
       if (t < T) logits_out[t * E + e] = (uint16_t)f32_to_bf16_rne(s_logit[tl][e]);
@@ -564,7 +568,7 @@ __global__ __launch_bounds__(256) void route_kernel(
     if (t < T) gate_out[t] = (uint16_t)f32_to_bf16_rne(s_logit[tid][64]);
   }
 
-  // Phase 3: SEL_LANES lanes per token (token wave * 16 + lane / SEL_LANES).
+  // Phase 3: SEL_LANES lanes per token (token wave * 64 / SEL_LANES + lane / SEL_LANES).
   {
     const int tl = wave * (64 / SEL_LANES) + lane / SEL_LANES;
     const int64_t t = tb + tl;
@@ -590,7 +594,7 @@ __global__ __launch_bounds__(256) void route_kernel(
 
   // Phase 4: tied tokens, one wave each.
   const int nties = s_nties;
-  for (int q = wave; q < nties; q += 4) {
+  for (int q = wave; q < nties; q += ROUTE_THREADS / 64) {
     const int tl = s_ties[q];
     const int64_t t = tb + tl;
     const float z = lane < E ? s_logit[tl][lane] + s_bias[lane] : -INFINITY;
@@ -613,7 +617,7 @@ hipError_t launch_route(const uint16_t* x, const uint16_t* wr, const uint16_t* w
                         int64_t T, int h, int E, int k, hipStream_t stream) {
   const int64_t nblk = (T + ROUTE_TOKENS - 1) / ROUTE_TOKENS;
   if (nblk == 0) return hipSuccess;
-  hipLaunchKernelGGL(route_kernel, dim3((unsigned)nblk), dim3(256), 0, stream, x, wr, wsg,
+  hipLaunchKernelGGL(route_kernel, dim3((unsigned)nblk), dim3(ROUTE_THREADS), 0, stream, x, wr, wsg,
                      logits_in, bias, logits_out, idx_out, w_out, gate_out, hist, T, h, E, k);
   return hipGetLastError();
 }
