@@ -133,12 +133,13 @@ def cpu_baseline(wl, budget_s=12.0, max_runs=400):
                 os_cpu_count=os.cpu_count(), cpu_model=cpu)
 
 
-# Kernel symbol of each stage, as rocprofv3 names it (for the committed PMC byte counts).
+# Kernel symbol prefix of each stage, as rocprofv3 names it (the committed PMC byte counts are keyed
+# by stage and record the full kernel name they were read from).
 KERNEL_SYMBOLS = {
     "route": "q38::route_kernel",
     "permute": "q38::permute_kernel",
-    "gate_up": "q38::grouped_gemm_kernel<0>",
-    "down": "q38::grouped_gemm_kernel<1>",
+    "gate_up": "q38::grouped_gemm_kernel<0,",
+    "down": "q38::grouped_gemm_kernel<1,",
     "combine": "q38::combine_kernel",
 }
 TRAFFIC_FILE = REPO / "profiles" / "hbm_traffic.json"
@@ -147,12 +148,12 @@ TRAFFIC_FILE = REPO / "profiles" / "hbm_traffic.json"
 def hbm_traffic(workload, stage):
     """HBM bytes per launch of `stage` from the committed rocprofv3 PMC summary: FETCH_SIZE and
     WRITE_SIZE (KiB per dispatch), each scaled by the factor a plain copy of known size gives those
-    counters on the same device. None when no summary for this workload and kernel exists."""
+    counters on the same device. None when no summary for this workload and stage exists."""
     try:
         data = json.loads(TRAFFIC_FILE.read_text())
     except (OSError, ValueError):
         return None
-    entry = data.get("workloads", {}).get(workload, {}).get(KERNEL_SYMBOLS.get(stage, stage))
+    entry = data.get("workloads", {}).get(workload, {}).get(stage)
     if not entry:
         return None
     f = data["copy_calibration"]
