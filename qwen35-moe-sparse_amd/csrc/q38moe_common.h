@@ -47,6 +47,14 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_
 
 __device__ __forceinline__ u32x4_t ld16(const void* p) { return *reinterpret_cast<const u32x4_t*>(p); }
 __device__ __forceinline__ void st16(void* p, u32x4_t v) { *reinterpret_cast<u32x4_t*>(p) = v; }
+// Streaming (non-temporal) forms for data touched once: full cache lines per wave instruction
+// only, since non-temporal writes are not merged in the L2.
+__device__ __forceinline__ u32x4_t ld16_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+}
+__device__ __forceinline__ void st16_stream(void* p, u32x4_t v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(p));
+}
 
 // 32x32x16 bf16 MFMA: A fragment = row (lane % 32), k-chunk (lane / 32) of 8 elements;
 // B fragment = column (lane % 32), same k-chunk; D[i] of lane l = row 8*(i/4) + 4*(l/32) + i%4,

@@ -20,15 +20,16 @@
 //
 // The kernel is persistent: workgroup b walks tiles slot(b), slot(b) + G, ... (G = grid size) of a
 // list the permutation orders full tiles first and partial tiles by falling row count. Its async
-// copy streams (global_load_lds_dwordx4 into LDS rings: activation rows 5 slices ahead in a
-// 6-slot ring, copied by waves 0-3; weight rows 2 slices ahead in a 3-slot ring, waves 4-7) run
+// copy streams (global_load_lds_dwordx4 into LDS rings: activation rows 3 slices ahead in a
+// 4-slot ring, copied by waves 0-3; weight rows 2 slices ahead in a 3-slot ring, waves 4-7) run
 // on across tile boundaries, so the next tile's first slices load during this tile's epilogue. The
 // next tile's tile entry and row gather indices are fetched one tile ahead. Slots are spread over
 // the 8 XCDs in contiguous runs (workgroup b runs on XCD b % 8 and takes slot (b % 8) * G/8 + b/8),
 // so tiles that share an expert's weights or gathered rows run in one XCD's L2 at the same time.
 //
 // Slices are XOR-swizzled (16-byte chunk c of row r at slot c ^ ((r >> 2) & 3): conflict-free
-// fragment reads). The epilogue stores from registers after a cross-lane swap (16-byte stores).
+// fragment reads). The epilogue transposes each wave's output through a private LDS staging area so
+// that every store instruction writes whole 128-byte lines.
 #include "q38moe_common.h"
 #include "q38moe_kernels.h"
 
@@ -38,7 +39,7 @@ constexpr int BM = 256;        // activation rows per tile
 constexpr int BW = 256;        // weight rows per tile
 constexpr int BK = 32;         // K slice
 constexpr int NTHREADS = 512;  // 8 waves: 0-3 copy activation rows, 4-7 weight rows
-constexpr int NA = 6;          // activation ring slots: copies run 5 slices ahead
+constexpr int NA = 4;          // activation ring slots: copies run 3 slices ahead
 constexpr int NW = 3;          // weight ring slots: copies run 2 slices ahead
 constexpr int SLOT_ELEMS = 256 * BK;  // one ring slot: 256 rows of one K slice (16 KiB)
 constexpr int NCOPY = 4;       // async copies per lane per slice (16 rows each, 64 rows per wave)
@@ -191,6 +192,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
   // Gather indices of the next tile (perm[row0 + r], r < 256), copied asynchronously; activation
   // wave w copies and reads entries [64w, 64w + 64) only.
   __shared__ __attribute__((aligned(16))) int32_t next_rows[BM];
+  // Epilogue staging, private to each wave: 32 output rows x 64 columns (bf16, 128 bytes per row).
+  __shared__ __attribute__((aligned(16))) uint16_t epi_stage[8 * 32 * 64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches, SGPR M0
   const int wm = wave >> 1, wn = wave & 1;
@@ -205,17 +208,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
   if (L >= used) return;
   const int nk = p.K / BK;
   // This wave's copy distance and ring: activation rows (gathered, farther away in the memory
-  // hierarchy) run 5 slices ahead, weight rows (shared by the concurrent tiles of an expert,
-  // mostly L2 hits) 2. Each wave waits only for its own copies (vmcnt counts per wave), so the
-  // two streams do not hold each other up.
+  // hierarchy) run NA - 1 = 3 slices ahead, weight rows (shared by the concurrent tiles of an
+  // expert, mostly L2 hits) NW - 1 = 2. Each wave waits only for its own copies (vmcnt counts per
+  // wave), so the two streams do not hold each other up.
   const int ring_n = is_a ? NA : NW;
   const int dist = min(ring_n - 1, nk);  // <= nk: copies run at most one tile ahead
-  // ASYNC_ROWS (K >= 11 slices): the next tile's gather indices are copied to LDS before this
-  // tile's slice-0 wait, behind the copies of slices 0-4, so the in-order wait of slice 5
-  // completes them; they are read after the wait of slice nk - 6 >= 5. Otherwise they are plain
-  // loads there
-  // (which the compiler waits for, draining the copies in flight): a separate instantiation, so
-  // the main one carries no such load.
+  // ASYNC_ROWS (K >= 2 (NA - 1) + 1 slices): the next tile's gather indices are copied to LDS
+  // before this tile's slice-0 wait, behind the copies of slices 0 .. d-1 (d = NA - 1), so the
+  // in-order wait of slice d completes them; they are read after the wait of slice nk - d - 1 >= d.
+  // Otherwise they are plain loads there (which the compiler waits for, draining the copies in
+  // flight): a separate instantiation, so the main one carries no such load.
   constexpr bool async_rows = ASYNC_ROWS;
 
   int4 ti = tile_entry(p, L / p.ntiles_n);
@@ -345,55 +347,58 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
 #undef Q38_NEXT_SOURCES
 #undef Q38_COMPUTE
 
-    // Epilogue straight from registers. In a 32x32 block lane l holds row l % 32 and 4-column
-    // runs at 8*gq + 4*(l / 32); one permlane32_swap per register pair gives each lane two
-    // 8-column runs (16-byte stores, 32 contiguous bytes per row and instruction). No LDS: an LDS
-    // access here would make the compiler wait for the next tile's copies already in flight.
+    // Epilogue. In a 32x32 block lane l holds row l % 32 and 4-column runs at 8*gq + 4*(l / 32);
+    // each pair of blocks (32 rows x 64 columns) goes through this wave's LDS staging area (16-byte
+    // chunk c of row r at slot c ^ ((r >> 1) & 7): two-way bank conflicts on the 8-byte writes,
+    // none on the reads) and leaves as four 16-byte-per-lane stores that each cover 8 rows x 128
+    // contiguous bytes, i.e. whole cache lines. The staging area is the wave's own, so no barrier;
+    // the slice copies in flight never touch it.
     const int nt = L % p.ntiles_n;
     const int col_wave = MODE == MODE_GATE_UP ? nt * 128 + 64 * wn : nt * BW + 128 * wn;
+    uint8_t* const stage = reinterpret_cast<uint8_t*>(epi_stage + wave * (32 * 64));
     if (active) {
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
-        for (int to = 0; to < NT_OUT; ++to) {
-          uint32_t v[4][2];
+        for (int tp = 0; tp < NT_OUT / 2; ++tp) {
 #pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
+          for (int tt = 0; tt < 2; ++tt) {
+            const int to = 2 * tp + tt;
 #pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-              const int i = 4 * gq + 2 * h2;
-              if (MODE == MODE_GATE_UP) {
-                // Reference rounding (inference.py:90-96): bf16 gate and up, bf16 silu(gate),
-                // bf16 product; each bf16 rounding is one packed RNE conversion of two values.
-                float g0, g1, u0, u1, s0, s1;
-                unpack_bf16x2(pack_bf16x2(acc[to][mi][i], acc[to][mi][i + 1]), g0, g1);
-                unpack_bf16x2(pack_bf16x2(acc[to + 2][mi][i], acc[to + 2][mi][i + 1]), u0, u1);
-                unpack_bf16x2(pack_bf16x2(g0 * __builtin_amdgcn_rcpf(1.0f + __expf(-g0)),
-                                          g1 * __builtin_amdgcn_rcpf(1.0f + __expf(-g1))), s0, s1);
-                v[gq][h2] = pack_bf16x2(s0 * u0, s1 * u1);
-              } else {
-                v[gq][h2] = pack_bf16x2(acc[to][mi][i], acc[to][mi][i + 1]);
+            for (int gq = 0; gq < 4; ++gq) {
+              uint32_t v[2];
+#pragma unroll
+              for (int h2 = 0; h2 < 2; ++h2) {
+                const int i = 4 * gq + 2 * h2;
+                if (MODE == MODE_GATE_UP) {
+                  // Reference rounding (inference.py:90-96): bf16 gate and up, bf16 silu(gate),
+                  // bf16 product; each bf16 rounding is one packed RNE conversion of two values.
+                  float g0, g1, u0, u1, s0, s1;
+                  unpack_bf16x2(pack_bf16x2(acc[to][mi][i], acc[to][mi][i + 1]), g0, g1);
+                  unpack_bf16x2(pack_bf16x2(acc[to + 2][mi][i], acc[to + 2][mi][i + 1]), u0, u1);
+                  unpack_bf16x2(pack_bf16x2(g0 * __builtin_amdgcn_rcpf(1.0f + __expf(-g0)),
+                                            g1 * __builtin_amdgcn_rcpf(1.0f + __expf(-g1))), s0, s1);
+                  v[h2] = pack_bf16x2(s0 * u0, s1 * u1);
+                } else {
+                  v[h2] = pack_bf16x2(acc[to][mi][i], acc[to][mi][i + 1]);
+                }
               }
+              const int ch = 4 * tt + gq;
+              *reinterpret_cast<uint2*>(stage + lr * 128 + ((ch ^ ((lr >> 1) & 7)) << 4) + 8 * lh) =
+                  make_uint2(v[0], v[1]);
             }
-          }
-          // Lanes 0-31 keep runs gq = 0, 2 and take the upper lanes' (columns +4); lanes 32-63
-          // keep runs gq = 1, 3 and take the lower lanes' (columns -4).
-#pragma unroll
-          for (int h2 = 0; h2 < 2; ++h2) {
-            const auto s01 = __builtin_amdgcn_permlane32_swap(v[0][h2], v[1][h2], false, false);
-            v[0][h2] = s01[0];
-            v[1][h2] = s01[1];
-            const auto s23 = __builtin_amdgcn_permlane32_swap(v[2][h2], v[3][h2], false, false);
-            v[2][h2] = s23[0];
-            v[3][h2] = s23[1];
           }
           // Every lane stores (lanes past the tile's rows or columns into the sink), so each
           // wave issues exactly EPI_STORES stores per tile, which the slice waits count.
-          const int r = 64 * wm + 32 * mi + lr;
-          const int col = col_wave + 32 * to + 8 * lh;
-          uint16_t* dst = p.C + (int64_t)(ti.y + r) * p.N + col;
-          st16(r < ti.z && col < p.N ? dst : sink, u32x4_t{v[0][0], v[0][1], v[1][0], v[1][1]});
-          st16(r < ti.z && col + 16 < p.N ? dst + 16 : sink, u32x4_t{v[2][0], v[2][1], v[3][0], v[3][1]});
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int row = 8 * j + (lane >> 3), ch = lane & 7;
+            const u32x4_t d = *reinterpret_cast<const u32x4_t*>(stage + row * 128 + ((ch ^ ((row >> 1) & 7)) << 4));
+            const int r = 64 * wm + 32 * mi + row;
+            const int col = col_wave + 64 * tp + 8 * ch;
+            uint16_t* dst = p.C + (int64_t)(ti.y + r) * p.N + col;
+            st16(r < ti.z && col < p.N ? dst : sink, d);
+          }
         }
       }
     }
