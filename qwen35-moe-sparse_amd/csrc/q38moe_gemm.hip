@@ -167,7 +167,15 @@ __device__ __forceinline__ void dma4(const void* gsrc, uint32_t lds) {
                : "memory", "m0");
 }
 
-// s_waitcnt vmcnt(n) + s_barrier for a wave-uniform n in [0, 48] (vmcnt takes an immediate).
+// s_waitcnt vmcnt(N) + s_barrier for a compile-time N.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_barrier_imm() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// s_waitcnt vmcnt(n) + s_barrier for a wave-uniform n in [0, 48] (vmcnt takes an immediate): a
+// multi-level branch tree, used only off the steady state (drain after the last tile, K shorter
+// than a ring).
 __device__ __forceinline__ void wait_vmcnt_barrier(int n) {
 #define Q38_W(N) case N: asm volatile("s_waitcnt vmcnt(" #N ")\n\ts_barrier" ::: "memory"); break;
   switch (n) {
@@ -213,6 +221,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
   // wave), so the two streams do not hold each other up.
   const int ring_n = is_a ? NA : NW;
   const int dist = min(ring_n - 1, nk);  // <= nk: copies run at most one tile ahead
+  const bool steady = dist == ring_n - 1;
   // ASYNC_ROWS (K >= 2 (NA - 1) + 1 slices): the next tile's gather indices are copied to LDS
   // before this tile's slice-0 wait, behind the copies of slices 0 .. d-1 (d = NA - 1), so the
   // in-order wait of slice d completes them; they are read after the wait of slice nk - d - 1 >= d.
@@ -285,6 +294,18 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
     // s_barrier: __syncthreads() would also drain the copies in flight.
 #define Q38_STORES_AFTER(KT) ((KT) < dist ? stores_prev : 0)
 #define Q38_WAIT_BARRIER(N) wait_vmcnt_barrier(N)
+  // Steady state (dist == ring_n - 1): the count is a compile-time constant of the wave's role,
+  // plus EPI_STORES while the previous epilogue's stores follow the slice.
+#define Q38_WAIT_STEADY(STORES)                                                              \
+  do {                                                                                     \
+    if (is_a) {                                                                            \
+      if (STORES) wait_vmcnt_barrier_imm<4 * (NA - 2) + EPI_STORES>();                     \
+      else wait_vmcnt_barrier_imm<4 * (NA - 2)>();                                         \
+    } else {                                                                               \
+      if (STORES) wait_vmcnt_barrier_imm<4 * (NW - 2) + EPI_STORES>();                     \
+      else wait_vmcnt_barrier_imm<4 * (NW - 2)>();                                         \
+    }                                                                                      \
+  } while (0)
 #define Q38_NEXT_SOURCES()                                                                 \
   do {                                                                                     \
     if (is_a && next_async) {                                                              \
@@ -324,13 +345,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
     const int p1 = nk - dist;
     const int head = min(dist, p1);
     int kt = 0;
-    for (; kt < head; ++kt) {
-      Q38_WAIT_BARRIER(4 * (dist - 1) + Q38_STORES_AFTER(kt));
+    for (; kt < head; ++kt) {  // kt < dist: the previous epilogue's stores follow the slice
+      if (steady) Q38_WAIT_STEADY(stores_prev != 0);
+      else Q38_WAIT_BARRIER(4 * (dist - 1) + stores_prev);
       Q38_ISSUE(fill, src, kt + dist);
       Q38_COMPUTE();
     }
+    // Only reached with p1 > dist, i.e. steady: the count is the role's constant.
     for (; kt < p1; ++kt) {
-      Q38_WAIT_BARRIER(4 * (dist - 1));
+      Q38_WAIT_STEADY(false);
       Q38_ISSUE(fill, src, kt + dist);
       Q38_COMPUTE();
     }
@@ -338,11 +361,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
     // stream drains after the last tile.
     if (has_next) Q38_NEXT_SOURCES();
     for (; kt < nk; ++kt) {
-      Q38_WAIT_BARRIER(4 * (has_next ? dist - 1 : nk - 1 - kt) + Q38_STORES_AFTER(kt));
+      if (steady && has_next) Q38_WAIT_STEADY(kt < dist && stores_prev != 0);
+      else Q38_WAIT_BARRIER(4 * (has_next ? dist - 1 : nk - 1 - kt) + Q38_STORES_AFTER(kt));
       if (has_next) Q38_ISSUE(fill, src_n, kt + dist - nk);
       Q38_COMPUTE();
     }
 #undef Q38_WAIT_BARRIER
+#undef Q38_WAIT_STEADY
 #undef Q38_STORES_AFTER
 #undef Q38_NEXT_SOURCES
 #undef Q38_COMPUTE

@@ -341,45 +341,54 @@ constexpr int ROUTE_WROWS = 65;    // 64 expert rows + the shared-expert gate ro
 // current K chunk stored at slot c ^ (n & 15): the 16 rows of a B fragment read distinct banks.
 __device__ __forceinline__ int wr_slot(int n, int c) { return n * (ROUTE_KCHUNK / 8) + (c ^ (n & 15)); }
 
-// Insert (z, e) into a descending top-KP1 list (strictly greater values move up; equal values
-// stay behind the ones already there).
-template <int KP1>
-__device__ __forceinline__ void list_insert(float (&v)[KP1], int (&id)[KP1], float z, int e) {
-  if (z > v[KP1 - 1]) {
-    v[KP1 - 1] = z;
-    id[KP1 - 1] = e;
-#pragma unroll
-    for (int r = KP1 - 1; r > 0; --r) {
-      if (v[r] > v[r - 1]) {
-        const float tv = v[r];
-        v[r] = v[r - 1];
-        v[r - 1] = tv;
-        const int ti = id[r];
-        id[r] = id[r - 1];
-        id[r - 1] = ti;
-      }
-    }
-  }
-}
-
 constexpr int SEL_LANES = 8;  // lanes per token in the selection fast path
 
+// Compare-exchange for a descending list: afterwards v[i] >= v[j] (unless one is NaN; rows with a
+// NaN take the replay path, so their order here does not matter).
+__device__ __forceinline__ void cas_desc(float& vi, int& ii, float& vj, int& ij) {
+  const bool sw = vj > vi;
+  const float tv = sw ? vj : vi, bv = sw ? vi : vj;
+  const int ti = sw ? ij : ii, bi = sw ? ii : ij;
+  vi = tv; ii = ti; vj = bv; ij = bi;
+}
+
+// Sorts a bitonic list of NP (a power of two) into descending order: log2(NP) half-cleaner stages.
+template <int NP>
+__device__ __forceinline__ void bitonic_merge_desc(float (&v)[NP], int (&id)[NP]) {
+#pragma unroll
+  for (int d = NP / 2; d > 0; d >>= 1)
+#pragma unroll
+    for (int i = 0; i < NP; ++i)
+      if ((i & d) == 0) cas_desc(v[i], id[i], v[i + d], id[i + d]);
+}
+
+// Descending sort of 8 values (Batcher's odd-even merge sort network, 19 compare-exchanges).
+__device__ __forceinline__ void sort8_desc(float (&v)[8], int (&id)[8]) {
+#define Q38_CE(A, B) cas_desc(v[A], id[A], v[B], id[B])
+  Q38_CE(0, 1); Q38_CE(2, 3); Q38_CE(4, 5); Q38_CE(6, 7);
+  Q38_CE(0, 2); Q38_CE(1, 3); Q38_CE(4, 6); Q38_CE(5, 7);
+  Q38_CE(1, 2); Q38_CE(5, 6);
+  Q38_CE(0, 4); Q38_CE(1, 5); Q38_CE(2, 6); Q38_CE(3, 7);
+  Q38_CE(2, 4); Q38_CE(3, 5);
+  Q38_CE(1, 2); Q38_CE(3, 4); Q38_CE(5, 6);
+#undef Q38_CE
+}
+
 // Per-token selection by a group of SEL_LANES lanes (lane s of the group holds experts s,
-// s + SEL_LANES, ...): a top-(KP1) list per lane, merged across the group by xor-shuffles.
-// Returns false when the k+1 largest values are not all distinct (or the row has NaN /
-// non-finite max); such tokens need the libstdc++ replay. Every lane of the group returns the
-// same answer.
+// s + SEL_LANES, ...). Each lane sorts its 8 values; the groups' sorted lists of NP >= KP1 are
+// merged by xor-shuffle rounds, each keeping the NP largest of two lists (elementwise max of one
+// list and the other reversed is a bitonic sequence holding them) and re-sorting them with a
+// bitonic merge. Equal values are kept as often as they occur, so duplicates among the k+1
+// largest are seen. Returns false when the k+1 largest values are not all distinct (or the row
+// has NaN / non-finite max); such tokens need the libstdc++ replay. Every lane of the group
+// returns the same answer.
 template <int KP1>
 __device__ __forceinline__ bool group_select(const float* row, const float* bias, int E, int k, int s,
                                              int* out_idx, float* out_w) {
-  constexpr int PER = 64 / SEL_LANES;
-  float v[KP1];
-  int id[KP1];
-#pragma unroll
-  for (int r = 0; r < KP1; ++r) {
-    v[r] = -INFINITY;
-    id[r] = -1;
-  }
+  constexpr int PER = 64 / SEL_LANES;  // 8 values per lane
+  constexpr int NP = KP1 <= 8 ? 8 : 16;
+  float v[NP];
+  int id[NP];
   float z[PER];
   int nan = 0;
 #pragma unroll
@@ -389,28 +398,49 @@ __device__ __forceinline__ bool group_select(const float* row, const float* bias
     if (e < E) {
       z[j] = row[e] + (bias != nullptr ? bias[e] : 0.0f) + 0.0f;
       nan |= __builtin_isnan(z[j]);
-      list_insert<KP1>(v, id, z[j], e);
+    }
+  }
+  {
+    float lv[8];
+    int li[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      lv[j] = __builtin_isnan(z[j]) ? -INFINITY : z[j];
+      li[j] = s + SEL_LANES * j;
+    }
+    sort8_desc(lv, li);
+#pragma unroll
+    for (int r = 0; r < NP; ++r) {
+      v[r] = r < 8 ? lv[r & 7] : -INFINITY;
+      id[r] = r < 8 ? li[r & 7] : -1;
     }
   }
 #pragma unroll
   for (int o = 1; o < SEL_LANES; o <<= 1) {
-    float ov[KP1];
-    int oid[KP1];
+    float ov[NP];
+    int oid[NP];
 #pragma unroll
-    for (int r = 0; r < KP1; ++r) {
-      ov[r] = __shfl_xor(v[r], o);
-      oid[r] = __shfl_xor(id[r], o);
+    for (int r = 0; r < NP; ++r) {
+      ov[r] = __shfl_xor(v[NP - 1 - r], o);
+      oid[r] = __shfl_xor(id[NP - 1 - r], o);
     }
     nan |= __shfl_xor(nan, o);
 #pragma unroll
-    for (int r = 0; r < KP1; ++r) list_insert<KP1>(v, id, ov[r], oid[r]);
+    for (int r = 0; r < NP; ++r) {
+      const bool take = ov[r] > v[r];
+      v[r] = take ? ov[r] : v[r];
+      id[r] = take ? oid[r] : id[r];
+    }
+    bitonic_merge_desc<NP>(v, id);
   }
   const float m = v[0];
   if (nan || !__builtin_isfinite(m)) return false;
   const int lim = min(k, E - 1);
 #pragma unroll
-  for (int r = 0; r < KP1 - 1; ++r)
+  for (int r = 0; r < KP1 - 1; ++r) {
     if (r < lim && v[r] == v[r + 1]) return false;
+    if (r == k - 1 && v[r] == -INFINITY) return false;  // fewer than k finite values: replay
+  }
   float sum = 0.0f;
 #pragma unroll
   for (int j = 0; j < PER; ++j)
@@ -463,7 +493,9 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     int32_t* __restrict__ idx_out, uint16_t* __restrict__ w_out,
     uint16_t* __restrict__ gate_out, int32_t* __restrict__ hist, int64_t T, int h, int E, int k) {
   __shared__ __attribute__((aligned(16))) u32x4_t s_w[ROUTE_WROWS * (ROUTE_KCHUNK / 8)];
-  __shared__ float s_logit[ROUTE_TOKENS][65];
+  // Row stride 72 (= 8 mod 64 banks): the selection's 8 lanes x 8 tokens per wave read 64
+  // distinct banks.
+  __shared__ float s_logit[ROUTE_TOKENS][72];
   __shared__ float s_bias[64];
   __shared__ int s_hist[64];
   __shared__ int s_ties[ROUTE_TOKENS];
