@@ -24,16 +24,32 @@ __device__ __forceinline__ bool cmp_gt(float a, float b) {
   return (__builtin_isnan(a) && !__builtin_isnan(b)) || (a > b);
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+// Whole-wave reductions without LDS traffic: DPP within rows of 16 lanes (xor 1, xor 2, half-row
+// and row mirrors), then the gfx950 row-pair and half-wave swaps.
+__device__ __forceinline__ float dpp_f(float v, int ctrl) {
+  switch (ctrl) {  // ctrl must be an immediate
+    case 0xb1: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, false));
+    case 0x4e: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, false));
+    case 0x141: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));
+    default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false));
+  }
 }
-
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+  v = op(v, dpp_f(v, 0xb1));   // quad_perm [1,0,3,2]: lane ^ 1
+  v = op(v, dpp_f(v, 0x4e));   // quad_perm [2,3,0,1]: lane ^ 2
+  v = op(v, dpp_f(v, 0x141));  // row_half_mirror: quads of each 8 lanes
+  v = op(v, dpp_f(v, 0x140));  // row_mirror: halves of each row of 16
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+  v = op(__int_as_float(r16[0]), __int_as_float(r16[1]));  // rows 0|1 and 2|3
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return op(__int_as_float(r32[0]), __int_as_float(r32[1]));  // lanes 0-31 | 32-63
+}
+__device__ __forceinline__ float wave_max(float v) {
+  return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  return wave_reduce(v, [](float a, float b) { return a + b; });
 }
 
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -193,8 +209,6 @@ __device__ void heap_select_slots(float& qv, int& qi, int lane, int first, int m
 // std::nth_element(q, q+k-1, q+n, cmp) then std::sort(q, q+k-1, cmp), with queue slot = lane.
 __device__ void nth_element_then_sort(float& qv, int& qi, int lane, int n, int k, float* sv,
                                       int* si) {
-  int* lpos = si;                          // rank-compacted stop positions (wave-private LDS)
-  int* rpos = reinterpret_cast<int*>(sv);
   const int nth = k - 1;
   int first = 0, last = n;
   int depth = 2 * (31 - __clz(n));
@@ -225,9 +239,10 @@ __device__ void nth_element_then_sort(float& qv, int& qi, int lane, int n, int k
     const float pv = lane_f(qv, first);
     // __unguarded_partition(first+1, last, pivot=first): the i-th left stop (slot holding a value
     // not cmp-greater than the pivot) swaps with the i-th right stop (value the pivot is not
-    // cmp-greater than; the pivot slot itself guards the scan) while left < right. Stop
-    // positions are compacted into LDS by rank: lpos[i] = i-th left stop, rpos[i] = i-th right
-    // stop counted from the right.
+    // cmp-greater than; the pivot slot itself guards the scan) while left < right. Lane i learns
+    // li = the i-th left stop and ri = the i-th right stop counted from the right by a forward
+    // permute (each stop sends its position to the lane of its rank; lane 63 is never a rank a
+    // left stop or a partial right-stop set reaches, so the other lanes send there).
     const bool isl = lane > first && lane < last && !cmp_gt(qv, pv);
     const bool isg = lane >= first && lane < last && !cmp_gt(pv, qv);
     const uint64_t le = ballot64(isl);
@@ -235,13 +250,10 @@ __device__ void nth_element_then_sort(float& qv, int& qi, int lane, int n, int k
     const int nl = __popcll(le), nr = __popcll(ge);
     const int lrank = bits_below(le);
     const int grank = nr - 1 - bits_below(ge);
-    if (isl) lpos[lrank] = lane;
-    if (isg) rpos[grank] = lane;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int li = lane < nl ? lpos[lane] : 64;
-    const int ri = lane < nr ? rpos[lane] : -1;
+    const int lp = __builtin_amdgcn_ds_permute((isl ? lrank : 63) << 2, lane);
+    const int rp = __builtin_amdgcn_ds_permute((isg ? grank : 63) << 2, lane);
+    const int li = lane < nl ? lp : 64;
+    const int ri = lane < nr ? rp : -1;
     const int sw = __popcll(ballot64(lane < nl && lane < nr && li < ri));
     int cut;
     if (sw == 0) {
@@ -251,14 +263,14 @@ __device__ void nth_element_then_sort(float& qv, int& qi, int lane, int n, int k
       const int r_last = lane_i(ri, sw - 1);
       cut = min(l_next, r_last);
     }
+    // The i-th left stop takes the i-th right stop's slot and vice versa, for i < sw.
+    const int from_r = __builtin_amdgcn_ds_bpermute((isl ? lrank : lane) << 2, ri);
+    const int from_l = __builtin_amdgcn_ds_bpermute((isg ? grank : lane) << 2, li);
     int src = lane;
-    if (isl && lrank < sw) src = rpos[lrank];
-    else if (isg && grank < sw) src = lpos[grank];
-    qv = __shfl(qv, src & 63);
-    qi = __shfl(qi, src & 63);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (isl && lrank < sw) src = from_r;
+    else if (isg && grank < sw) src = from_l;
+    qv = __int_as_float(__builtin_amdgcn_ds_bpermute((src & 63) << 2, __float_as_int(qv)));
+    qi = __builtin_amdgcn_ds_bpermute((src & 63) << 2, qi);
     if (cut <= nth) first = cut;
     else last = cut;
   }

@@ -119,6 +119,14 @@ def test_route_full(gpu, wl_name, T):
     ref_logits = orc.bf16(x.float() @ wr.float().T)
     assert_gemm_bf16_rounding(logits, x, wr, "router logits")
     assert_gemm_bf16_rounding(gate, x, ws, "shared gate logit")
+    # Without the logits output the kernel gives the same indices, weights and histogram; the
+    # histogram holds each 64-token block's expert counts.
+    _, idx2, w2, _, hist2 = ops.route(x.to(gpu), wr.to(gpu), wl.topk, w_shared_gate=ws.to(gpu),
+                                      want_logits=False, want_hist=True)
+    assert torch.equal(idx2, idx) and torch.equal(w2, w) and torch.equal(hist2, hist)
+    blk = torch.arange(T).repeat_interleave(wl.topk) // 64
+    ref_hist = torch.zeros_like(hist.cpu()).index_put_((blk, idx.cpu().long().flatten()), torch.tensor(1, dtype=torch.int32), accumulate=True)
+    assert torch.equal(hist.cpu(), ref_hist)
     # Selection is a function of the logits: exact against the oracle on the GPU logits.
     _, _, ridx, rw = orc.router(None, None, wl.topk, logits=logits.cpu())
     assert torch.equal(idx.cpu().long(), ridx)
