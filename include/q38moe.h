@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define Q38MOE_ABI_VERSION 2
+#define Q38MOE_ABI_VERSION 3
 
 #define Q38MOE_OK 0
 #define Q38MOE_EINVAL (-1)   /* bad shape, null pointer, misalignment, unsupported dtype */
@@ -194,6 +194,65 @@ int q38moe_block_forward(const void* x, const void* w_router, const void* w_gate
                          void* topk_w, int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
                          int32_t Is, void* workspace, size_t workspace_bytes, int32_t dtype,
                          void* stream);
+
+/*
+ * FP8 expert path, R14. There is no reference function: the benchmark set's fp8 configuration
+ * (e4m3 expert weights with per-output-channel fp32 scales, per-token e4m3 activations, bf16
+ * outputs) defines it, and these entry points fix its arithmetic. e4m3 is the OCP format
+ * (torch.float8_e4m3fn, largest finite 448), stored one byte per value.
+ *
+ * Per-row quantisation of x [R,C] bf16 (C % 64 == 0, C <= 4096):
+ *   amax[r] = max_c |x[r,c]| (NaN if the row holds a NaN); inv = amax > 0 ? 448/amax : 0 (fp32)
+ *   q[r,c] = e4m3(round-to-nearest-even(clamp(x[r,c]*inv, -448, 448))); scale[r] = amax/448
+ * so x ~ q * scale. Quantises expert weights at load time (rows = output channels:
+ * gate_up [E*2I, h], down [E*h, I], shared [I,h]/[h,I]) and, inside the fp8 block, the tokens
+ * and the SwiGLU rows. q must be 8-byte aligned.
+ */
+int q38moe_quantize_rows(const void* x, void* q, float* scale, int64_t R, int32_t C, void* stream);
+
+/*
+ * Grouped gate/up GEMM on e4m3 operands (R6 in fp8): as q38moe_gate_up, with
+ *   acc = sum_c xq[tok,c] * wq[n,c] (exact e4m3 products, fp32 accumulation)
+ *   g = bf16(acc_g * row_scale[r] * s_gate_up[e, n]), u likewise with row I + n; H as q38moe_gate_up.
+ * xq [T,h] e4m3 tokens; row_scale [T*k + shared_rows] fp32 in sorted row order (the token scale of
+ * each row; q38moe_block_forward_fp8 derives it in its permutation pass); wq_gate_up [E,2I,h]
+ * e4m3 + s_gate_up [E,2I]; shared rows use wq_sh_gate/wq_sh_up [I,h] + s_sh_gate/s_sh_up [I].
+ */
+int q38moe_gate_up_fp8(const void* xq, const float* row_scale, const void* wq_gate_up,
+                       const float* s_gate_up, const void* wq_sh_gate, const float* s_sh_gate,
+                       const void* wq_sh_up, const float* s_sh_up, const int32_t* perm,
+                       const int32_t* tiles, const int32_t* tile_count, int64_t shared_rows,
+                       void* H, int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
+                       void* stream);
+
+/*
+ * Grouped down GEMM on e4m3 operands (R7 in fp8): Y[r,c] = bf16((sum_i Hq[r,i] wq[c,i]) *
+ * row_scale[r] * s_down[e,c]). Hq [T*k + shared_rows, I] e4m3 with row_scale per row
+ * (q38moe_quantize_rows of H); wq_down [E,h,I] e4m3 + s_down [E,h]; shared rows use wq_sh_down
+ * [h,I] + s_sh_down [h].
+ */
+int q38moe_down_fp8(const void* Hq, const float* row_scale, const void* wq_down, const float* s_down,
+                    const void* wq_sh_down, const float* s_sh_down, const int32_t* tiles,
+                    const int32_t* tile_count, int64_t shared_rows, void* Y, int64_t T, int32_t h,
+                    int32_t E, int32_t k, int32_t I, void* stream);
+
+/*
+ * MoE block with fp8 experts (R0 over R14): q38moe_block_forward's pipeline with the routed and
+ * shared expert GEMMs on e4m3 (Is == I: the shared expert runs inside the grouped GEMMs). The
+ * router and the shared-expert gate logit stay bf16 on x; x is quantised per token, the SwiGLU
+ * rows per row; combine and the gated shared sum as in bf16. Weights as for q38moe_gate_up_fp8 /
+ * q38moe_down_fp8. Workspace from q38moe_block_fp8_workspace_bytes. h, I <= 4096.
+ */
+int q38moe_block_fp8_workspace_bytes(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
+                                     size_t* bytes);
+int q38moe_block_forward_fp8(const void* x, const void* w_router, const void* wq_gate_up,
+                             const float* s_gate_up, const void* wq_down, const float* s_down,
+                             const void* wq_sh_gate, const float* s_sh_gate, const void* wq_sh_up,
+                             const float* s_sh_up, const void* wq_sh_down, const float* s_sh_down,
+                             const void* w_sh_gate_proj, const float* logit_bias, void* out,
+                             void* logits, int32_t* topk_idx, void* topk_w, int64_t T, int32_t h,
+                             int32_t E, int32_t k, int32_t I, void* workspace,
+                             size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -231,3 +231,96 @@ def reference_block_forward(x, params, k, logit_bias=None):
     routed = experts_eager(x, idx, w, params["experts.gate_up_proj"], params["experts.down_proj"])
     sh = torch.sigmoid(F.linear(x, params["shared_expert_gate.weight"])) * sh
     return routed + sh
+
+
+# ---- fp8 expert path (R14). The reference has no fp8: these restate this repository's definition
+# (include/q38moe.h, q38moe_quantize_rows / q38moe_block_forward_fp8) on the CPU. ----
+
+E4M3_MAX = 448.0
+
+
+def quant_e4m3_rows(t):
+    """Per-row e4m3 quantisation: amax = max|x| per row (fp32), inv = 448/amax (0 for a zero row),
+    q = e4m3(RNE(clamp(x*inv, +-448))) via torch.float8_e4m3fn, scale = amax/448. Returns
+    (q uint8 bit patterns, same shape; scale fp32, shape[:-1])."""
+    x = _f(t)
+    shape = x.shape
+    x2 = x.reshape(-1, shape[-1])
+    amax = x2.abs().amax(dim=1)
+    inv = torch.where(amax > 0, torch.tensor(E4M3_MAX, dtype=torch.float32) / amax, torch.zeros_like(amax))
+    inv = torch.where(torch.isnan(amax), amax, inv)
+    q = (x2 * inv[:, None]).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+    scale = amax / E4M3_MAX
+    return q.view(torch.uint8).reshape(shape), scale.reshape(shape[:-1])
+
+
+def e4m3_value(q):
+    """uint8 e4m3 bit patterns -> fp32 values."""
+    return q.view(torch.float8_e4m3fn).to(torch.float32)
+
+
+def quant_weights_fp8(params):
+    """The block's expert weights in e4m3 with per-output-channel scales (q38moe_quantize_rows on
+    each weight row)."""
+    names = ("experts.gate_up_proj", "experts.down_proj", "shared_expert.gate_proj.weight",
+             "shared_expert.up_proj.weight", "shared_expert.down_proj.weight")
+    return {n: quant_e4m3_rows(params[n]) for n in names}
+
+
+def _fp8_matmul(qa, sa, qw, sw):
+    """(sum_c qa[r,c] qw[n,c]) * sa[r] * sw[n]: exact e4m3 products, fp32 sums, then the scales."""
+    return (e4m3_value(qa) @ e4m3_value(qw).T) * sa[:, None] * sw[None, :]
+
+
+def experts_fp8(x, idx, w, wq, k, gate_logit):
+    """The e4m3 experts of q38moe_block_forward_fp8 for given routing (idx [T,k], w bf16 [T,k]) and
+    shared-gate logits: tokens quantised per row; routed and shared gate/up on e4m3 with the bf16
+    roundings of inference:90-96; SwiGLU rows (sorted routed rows, then the shared rows) quantised
+    per row; down on e4m3 rounded to bf16; weight, k-sum and gated shared sum as in ``block``."""
+    T, h = x.shape
+    qg, sg = wq["experts.gate_up_proj"]
+    qd, sd = wq["experts.down_proj"]
+    E, twoI, _ = qg.shape
+    I = twoI // 2
+    xq, sx = quant_e4m3_rows(x)
+    counts, starts, perm = permute_cpu(idx.numpy(), E)
+    perm_t = torch.from_numpy(perm.astype(np.int64))
+    P = T * k
+    H = torch.zeros(P + T, I, dtype=torch.bfloat16)  # sorted routed rows [0, P), shared [P, P + T)
+
+    def swiglu(qa, sa, qgate, sgate, qup, sup):
+        g = _f(bf16(_fp8_matmul(qa, sa, qgate, sgate)))
+        u = _f(bf16(_fp8_matmul(qa, sa, qup, sup)))
+        return bf16(_f(bf16(F.silu(g))) * u)
+
+    for e in range(E):
+        c, s = int(counts[e]), int(starts[e])
+        if c == 0:
+            continue
+        tok = perm_t[s:s + c] // k
+        H[s:s + c] = swiglu(xq[tok], sx[tok], qg[e, :I], sg[e, :I], qg[e, I:], sg[e, I:])
+    H[P:] = swiglu(xq, sx, *wq["shared_expert.gate_proj.weight"], *wq["shared_expert.up_proj.weight"])
+    Hq, sH = quant_e4m3_rows(H)
+    Y = torch.zeros(P + T, h, dtype=torch.bfloat16)
+    for e in range(E):
+        c, s = int(counts[e]), int(starts[e])
+        if c:
+            Y[s:s + c] = bf16(_fp8_matmul(Hq[s:s + c], sH[s:s + c], qd[e], sd[e]))
+    Y[P:] = bf16(_fp8_matmul(Hq[P:], sH[P:], *wq["shared_expert.down_proj.weight"]))
+    wflat = _f(w.reshape(-1))
+    y = torch.zeros(P, h, dtype=torch.bfloat16)
+    y[perm_t] = bf16(_f(Y[:P]) * wflat[perm_t][:, None])
+    routed = bf16(_f(y).view(T, k, h).sum(dim=1))
+    sh = Y[P:]
+    gated = bf16(_f(bf16(torch.sigmoid(_f(gate_logit))))[:, None] * _f(sh))
+    out = bf16(_f(routed) + _f(gated))
+    return out, dict(xq=xq, sx=sx, perm=perm_t, H=H, Hq=Hq, sH=sH, Y=Y, routed=routed, shared=sh)
+
+
+def block_fp8(x, params, wq, k, logit_bias=None):
+    """q38moe_block_forward_fp8 on the CPU: the bf16 router and shared-gate logit of ``block``, then
+    ``experts_fp8``. Returns out and intermediates."""
+    logits, probs, idx, w = router(x, params["gate.weight"], k, logit_bias)
+    gate_logit = bf16(_f(x) @ _f(params["shared_expert_gate.weight"]).reshape(-1))
+    out, inter = experts_fp8(x, idx, w, wq, k, gate_logit)
+    return out, dict(inter, logits=logits, idx=idx, w=w, gate_logit=gate_logit)

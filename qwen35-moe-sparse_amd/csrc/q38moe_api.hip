@@ -123,6 +123,26 @@ BlockWs block_layout(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int3
   return b;
 }
 
+// fp8 block workspace: the bf16 block's, plus the e4m3 tokens and SwiGLU rows with their scales.
+struct Fp8Ws {
+  BlockWs b;
+  size_t xq, sx, sa, Hq, sH, end;
+};
+
+Fp8Ws fp8_layout(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I) {
+  Fp8Ws f;
+  f.b = block_layout(T, h, E, k, I, I);
+  const int64_t rows = T * k + T;
+  size_t off = f.b.end;
+  f.xq = off; off = align_up(off + (size_t)T * h);
+  f.sx = off; off = align_up(off + sizeof(float) * T);
+  f.sa = off; off = align_up(off + sizeof(float) * rows);
+  f.Hq = off; off = align_up(off + (size_t)rows * I);
+  f.sH = off; off = align_up(off + sizeof(float) * rows);
+  f.end = off;
+  return f;
+}
+
 template <typename P>
 P* at(void* base, size_t off) {
   return reinterpret_cast<P*>(static_cast<char*>(base) + off);
@@ -484,6 +504,173 @@ int q38moe_block_forward(const void* x, const void* w_router, const void* w_gate
                      L.fused ? static_cast<const uint16_t*>(w_sh_up) : nullptr,
                      L.fused ? static_cast<const uint16_t*>(w_sh_down) : nullptr, sh_out, gate, out, T, h, E, k, I,
                      L.fused ? T : 0, hist, workspace, L.ex, st);
+}
+
+// ---- fp8 expert path (R14) --------------------------------------------------------------------
+
+int q38moe_quantize_rows(const void* x, void* q, float* scale, int64_t R, int32_t C, void* stream) {
+  g_err[0] = 0;
+  if (R < 0) return fail(Q38MOE_EINVAL, "R must be >= 0");
+  if (C < 64 || C % 64 != 0 || C > 4096) return fail(Q38MOE_EINVAL, "C must be a multiple of 64 in [64, 4096] (got %d)", C);
+  if (R == 0) return Q38MOE_OK;
+  Q38_CHECK(check_ptr(x, "x"));
+  if (q == nullptr || scale == nullptr) return fail(Q38MOE_EINVAL, "q and scale must not be NULL");
+  if (reinterpret_cast<uintptr_t>(q) % 8 != 0) return fail(Q38MOE_EINVAL, "q must be 8-byte aligned");
+  (void)hipGetLastError();
+  Q38_HIP(q38::launch_quant_rows(static_cast<const uint16_t*>(x), static_cast<uint8_t*>(q), scale, R, C,
+                                 static_cast<hipStream_t>(stream)),
+          "quantize_rows launch");
+  return Q38MOE_OK;
+}
+
+int q38moe_block_fp8_workspace_bytes(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, size_t* bytes) {
+  g_err[0] = 0;
+  Q38_CHECK(check_routing(T, E, k));
+  Q38_CHECK(check_dim(h, "h"));
+  Q38_CHECK(check_dim(I, "I"));
+  if (bytes == nullptr) return fail(Q38MOE_EINVAL, "bytes must not be NULL");
+  *bytes = fp8_layout(T, h, E, k, I).end;
+  return Q38MOE_OK;
+}
+
+int q38moe_gate_up_fp8(const void* xq, const float* row_scale, const void* wq_gate_up, const float* s_gate_up,
+                       const void* wq_sh_gate, const float* s_sh_gate, const void* wq_sh_up,
+                       const float* s_sh_up, const int32_t* perm, const int32_t* tiles,
+                       const int32_t* tile_count, int64_t shared_rows, void* H, int64_t T, int32_t h,
+                       int32_t E, int32_t k, int32_t I, void* stream) {
+  g_err[0] = 0;
+  Q38_CHECK(check_routing(T, E, k));
+  Q38_CHECK(check_dim(h, "h"));
+  Q38_CHECK(check_dim(I, "I"));
+  if (T == 0) return Q38MOE_OK;
+  Q38_CHECK(check_rows(T, h, k));
+  Q38_CHECK(check_ptr(xq, "xq"));
+  Q38_CHECK(check_ptr(wq_gate_up, "wq_gate_up"));
+  Q38_CHECK(check_ptr(H, "H"));
+  Q38_CHECK(check_ptr(tiles, "tiles"));
+  if (perm == nullptr || tile_count == nullptr || row_scale == nullptr || s_gate_up == nullptr)
+    return fail(Q38MOE_EINVAL, "perm, tile_count, row_scale and s_gate_up must not be NULL");
+  if (shared_rows < 0 || shared_rows > T) return fail(Q38MOE_EINVAL, "shared_rows must be in [0, T]");
+  if (shared_rows > 0) {
+    Q38_CHECK(check_ptr(wq_sh_gate, "wq_sh_gate"));
+    Q38_CHECK(check_ptr(wq_sh_up, "wq_sh_up"));
+    if (s_sh_gate == nullptr || s_sh_up == nullptr) return fail(Q38MOE_EINVAL, "shared-expert scales must not be NULL");
+  }
+  (void)hipGetLastError();
+  Q38_HIP(q38::launch_gate_up_fp8(static_cast<const uint8_t*>(xq), perm, reinterpret_cast<const int4*>(tiles),
+                                  tile_count, (int)max_tiles_impl(T, E, k, shared_rows), 0, (int)(T * k), row_scale,
+                                  static_cast<const uint8_t*>(wq_gate_up), s_gate_up,
+                                  static_cast<const uint8_t*>(wq_sh_gate), s_sh_gate,
+                                  static_cast<const uint8_t*>(wq_sh_up), s_sh_up, static_cast<uint16_t*>(H), I, h,
+                                  E, k, static_cast<hipStream_t>(stream)),
+          "gate_up_fp8 launch");
+  return Q38MOE_OK;
+}
+
+int q38moe_down_fp8(const void* Hq, const float* row_scale, const void* wq_down, const float* s_down,
+                    const void* wq_sh_down, const float* s_sh_down, const int32_t* tiles,
+                    const int32_t* tile_count, int64_t shared_rows, void* Y, int64_t T, int32_t h,
+                    int32_t E, int32_t k, int32_t I, void* stream) {
+  g_err[0] = 0;
+  Q38_CHECK(check_routing(T, E, k));
+  Q38_CHECK(check_dim(h, "h"));
+  Q38_CHECK(check_dim(I, "I"));
+  if (T == 0) return Q38MOE_OK;
+  Q38_CHECK(check_rows(T, h, k));
+  Q38_CHECK(check_ptr(Hq, "Hq"));
+  Q38_CHECK(check_ptr(wq_down, "wq_down"));
+  Q38_CHECK(check_ptr(Y, "Y"));
+  Q38_CHECK(check_ptr(tiles, "tiles"));
+  if (tile_count == nullptr || row_scale == nullptr || s_down == nullptr)
+    return fail(Q38MOE_EINVAL, "tile_count, row_scale and s_down must not be NULL");
+  if (shared_rows < 0 || shared_rows > T) return fail(Q38MOE_EINVAL, "shared_rows must be in [0, T]");
+  if (shared_rows > 0) {
+    Q38_CHECK(check_ptr(wq_sh_down, "wq_sh_down"));
+    if (s_sh_down == nullptr) return fail(Q38MOE_EINVAL, "s_sh_down must not be NULL");
+  }
+  (void)hipGetLastError();
+  Q38_HIP(q38::launch_down_fp8(static_cast<const uint8_t*>(Hq), reinterpret_cast<const int4*>(tiles), tile_count,
+                               (int)max_tiles_impl(T, E, k, shared_rows), 0, row_scale,
+                               static_cast<const uint8_t*>(wq_down), s_down, static_cast<const uint8_t*>(wq_sh_down),
+                               s_sh_down, static_cast<uint16_t*>(Y), h, I, E, static_cast<hipStream_t>(stream)),
+          "down_fp8 launch");
+  return Q38MOE_OK;
+}
+
+int q38moe_block_forward_fp8(const void* x, const void* w_router, const void* wq_gate_up, const float* s_gate_up,
+                             const void* wq_down, const float* s_down, const void* wq_sh_gate,
+                             const float* s_sh_gate, const void* wq_sh_up, const float* s_sh_up,
+                             const void* wq_sh_down, const float* s_sh_down, const void* w_sh_gate_proj,
+                             const float* logit_bias, void* out, void* logits, int32_t* topk_idx, void* topk_w,
+                             int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  g_err[0] = 0;
+  Q38_CHECK(check_routing(T, E, k));
+  Q38_CHECK(check_dim(h, "h"));
+  Q38_CHECK(check_dim(I, "I"));
+  if (h > 4096 || I > 4096) return fail(Q38MOE_EINVAL, "fp8 path: h and I must be <= 4096");
+  if (T == 0) return Q38MOE_OK;
+  Q38_CHECK(check_rows(T, h, k));
+  Q38_CHECK(check_ptr(x, "x"));
+  Q38_CHECK(check_ptr(w_router, "w_router"));
+  Q38_CHECK(check_ptr(wq_gate_up, "wq_gate_up"));
+  Q38_CHECK(check_ptr(wq_down, "wq_down"));
+  Q38_CHECK(check_ptr(wq_sh_gate, "wq_sh_gate"));
+  Q38_CHECK(check_ptr(wq_sh_up, "wq_sh_up"));
+  Q38_CHECK(check_ptr(wq_sh_down, "wq_sh_down"));
+  Q38_CHECK(check_ptr(w_sh_gate_proj, "w_sh_gate_proj"));
+  Q38_CHECK(check_ptr(out, "out"));
+  if (s_gate_up == nullptr || s_down == nullptr || s_sh_gate == nullptr || s_sh_up == nullptr || s_sh_down == nullptr)
+    return fail(Q38MOE_EINVAL, "weight scales must not be NULL");
+  const Fp8Ws F = fp8_layout(T, h, E, k, I);
+  const BlockWs& L = F.b;
+  if (workspace == nullptr || workspace_bytes < F.end)
+    return fail(Q38MOE_EWORKSPACE, "workspace needs %zu bytes (got %zu)", F.end, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) % kAlign != 0)
+    return fail(Q38MOE_EINVAL, "workspace must be 256-byte aligned");
+  (void)hipGetLastError();
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t P = T * k;
+  int32_t* idx = topk_idx != nullptr ? topk_idx : at<int32_t>(workspace, L.idx);
+  uint16_t* w = topk_w != nullptr ? static_cast<uint16_t*>(topk_w) : at<uint16_t>(workspace, L.w);
+  uint16_t* gate = at<uint16_t>(workspace, L.gate);
+  const ExpertsWs& X = L.ex;
+  int32_t* hist = at<int32_t>(workspace, X.hist);
+  int32_t* inv = at<int32_t>(workspace, X.inv);
+  int32_t* perm = at<int32_t>(workspace, X.perm);
+  int4* tiles = at<int4>(workspace, X.tiles);
+  int32_t* tile_count = at<int32_t>(workspace, X.tile_count);
+  uint16_t* H = at<uint16_t>(workspace, X.H);
+  uint16_t* Y = at<uint16_t>(workspace, X.Y);
+  uint8_t* xq = at<uint8_t>(workspace, F.xq);
+  float* sx = at<float>(workspace, F.sx);
+  float* sa = at<float>(workspace, F.sa);
+  uint8_t* Hq = at<uint8_t>(workspace, F.Hq);
+  float* sH = at<float>(workspace, F.sH);
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  // Router, shared gate logit and histogram in bf16 (modeling:828, 831), then the tokens in e4m3.
+  Q38_HIP(q38::launch_route(xb, static_cast<const uint16_t*>(w_router), static_cast<const uint16_t*>(w_sh_gate_proj),
+                            nullptr, logit_bias, static_cast<uint16_t*>(logits), idx, w, gate, hist, T, h, E, k, st),
+          "route launch");
+  Q38_HIP(q38::launch_quant_rows(xb, xq, sx, T, h, st), "quantize x launch");
+  // Permutation; each sorted row takes its token's scale (shared rows P + t: token t).
+  Q38_HIP(q38::launch_permute(idx, false, hist, at<int32_t>(workspace, X.counts), at<int32_t>(workspace, X.starts),
+                              perm, inv, tiles, tile_count, q38::gemm_block_m(), (int)X.max_tiles, (int)T, T, E, k, st,
+                              sx, sa),
+          "permute launch");
+  Q38_HIP(q38::launch_gate_up_fp8(xq, perm, tiles, tile_count, (int)X.max_tiles, 0, (int)P, sa,
+                                  static_cast<const uint8_t*>(wq_gate_up), s_gate_up,
+                                  static_cast<const uint8_t*>(wq_sh_gate), s_sh_gate,
+                                  static_cast<const uint8_t*>(wq_sh_up), s_sh_up, H, I, h, E, k, st),
+          "gate_up_fp8 launch");
+  // SwiGLU rows to e4m3, one scale per row (routed pairs in sorted order, then the shared rows).
+  Q38_HIP(q38::launch_quant_rows(H, Hq, sH, P + T, I, st), "quantize H launch");
+  Q38_HIP(q38::launch_down_fp8(Hq, tiles, tile_count, (int)X.max_tiles, 0, sH, static_cast<const uint8_t*>(wq_down),
+                               s_down, static_cast<const uint8_t*>(wq_sh_down), s_sh_down, Y, h, I, E, st),
+          "down_fp8 launch");
+  Q38_HIP(q38::launch_combine(Y, inv, idx, false, w, Y + P * h, gate, static_cast<uint16_t*>(out), T, h, E, k, st),
+          "combine launch");
+  return Q38MOE_OK;
 }
 
 }  // extern "C"

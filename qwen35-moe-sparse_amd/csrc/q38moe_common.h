@@ -63,6 +63,16 @@ __device__ __forceinline__ f32x16_t mfma32x32x16(u32x4_t a, u32x4_t b, f32x16_t 
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
 
+// 32x32x64 e4m3 x e4m3 MFMA (gfx950 f8f6f4 form, both operands e4m3, no block scales): 32 bytes
+// per lane; lane = row (lane % 32) as in the bf16 forms.
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ i32x8_t cat8(u32x4_t lo, u32x4_t hi) {
+  return __builtin_bit_cast(i32x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+__device__ __forceinline__ f32x16_t mfma32x32x64_fp8(i32x8_t a, i32x8_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
 // 16x16x32 bf16 MFMA: A fragment = row (lane % 16), k-chunk (lane / 16); D[i] of lane l = row
 // 4*(l/16) + i, column l % 16.
 __device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {

@@ -65,6 +65,12 @@ struct GemmParams {
   int P;                      // first shared-expert row of the row space
   int N, K, E, topk;
   int ntiles_n;               // output-column tiles per row tile
+  // e4m3 operands only (FP8 instantiations): K counts 16-bit units (two e4m3 values each), so
+  // the copy machinery moves the same 64 bytes per row and slice. Dequantisation scales:
+  const float* a_scale;       // per GEMM row (the sorted row space)
+  const float* w_scale;       // routed weights: gate/up [E, 2N], down [E, N]
+  const float* ws_scale_a;    // shared expert: gate [N] (gate/up) or down [N]
+  const float* ws_scale_b;    // shared expert: up [N] (gate/up)
 };
 
 __device__ __forceinline__ int swz(int r, int c) { return r * BK + ((c ^ ((r >> 2) & 3)) << 3); }
@@ -146,6 +152,25 @@ __device__ __forceinline__ void copy_sources(const GemmParams& p, int4 ti, int n
   }
 }
 
+// Dequantisation scale of weight row rb (0..BW-1) of tile `ti`, output-column tile `nt`: the same
+// row mapping as copy_sources (fp8 only).
+template <int MODE>
+__device__ __forceinline__ const float* weight_scale_src(const GemmParams& p, int4 ti, int nt, int rb) {
+  const int N = p.N;
+  const bool shared_grp = ti.x >= p.E;
+  if (MODE == MODE_GATE_UP) {
+    const int half = rb >> 7, within = rb & 127;
+    const bool up = within >= 64;
+    int col = nt * 128 + 64 * half + (within & 63);
+    col = col < N ? col : 0;
+    if (shared_grp) return (up ? p.ws_scale_b : p.ws_scale_a) + col;
+    return p.w_scale + (int64_t)ti.x * 2 * N + (up ? N : 0) + col;
+  }
+  int col = nt * BW + rb;
+  col = col < N ? col : 0;
+  return shared_grp ? p.ws_scale_a + col : p.w_scale + (int64_t)ti.x * N + col;
+}
+
 // Async global -> LDS copies issued from inline asm: lane l copies 16 (or 4) bytes from gsrc to
 // LDS [lds_wave_base + 16*l] (or + 4*l); M0 holds the wave's LDS base. The compiler's wait
 // analysis mistakes the copy's address register for a destination (its builtin form is followed
@@ -190,7 +215,7 @@ __device__ __forceinline__ void wait_vmcnt_barrier(int n) {
 #undef Q38_W
 }
 
-template <int MODE, bool ASYNC_ROWS>
+template <int MODE, bool ASYNC_ROWS, bool FP8>
 __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p) {
   // 16-byte stores per wave and tile: 2 per 32x32 output block, 2 x 2 (gate/up) or 2 x 4 blocks.
   constexpr int EPI_STORES = MODE == MODE_GATE_UP ? 8 : 16;
@@ -202,6 +227,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
   __shared__ __attribute__((aligned(16))) int32_t next_rows[BM];
   // Epilogue staging, private to each wave: 32 output rows x 64 columns (bf16, 128 bytes per row).
   __shared__ __attribute__((aligned(16))) uint16_t epi_stage[8 * 32 * 64];
+  // fp8: dequantisation scales of the tile's 256 activation rows and 256 weight rows, double
+  // buffered by tile parity (copied one tile ahead, like the gather indices).
+  __shared__ __attribute__((aligned(16))) float sc_a[FP8 ? 2 : 1][FP8 ? BM : 1];
+  __shared__ __attribute__((aligned(16))) float sc_w[FP8 ? 2 : 1][FP8 ? BW : 1];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches, SGPR M0
   const int wm = wave >> 1, wn = wave & 1;
@@ -236,6 +265,18 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
   const uint16_t* src[NCOPY];
   const uint16_t* src_n[NCOPY];
   gather_rows<MODE>(p, ti, wave, lane, rows);
+  // fp8: the first tile's dequantisation scales (the wait below completes them).
+#define Q38_SCALES(BUF, TI, NT)                                                               \
+  do {                                                                                     \
+    if (is_a) {                                                                            \
+      const int r_ = 64 * wave + lane;                                                     \
+      dma4(p.a_scale + (TI).y + (r_ < (TI).z ? r_ : 0), lds_addr(&sc_a[BUF][64 * wave]));  \
+    } else {                                                                               \
+      dma4(weight_scale_src<MODE>(p, TI, NT, 64 * (wave - 4) + lane),                      \
+           lds_addr(&sc_w[BUF][64 * (wave - 4)]));                                         \
+    }                                                                                      \
+  } while (0)
+  if (FP8) Q38_SCALES(0, ti, L % p.ntiles_n);
   // Retire these loads on every path (waves >= 4 never read them); a load left pending in the
   // compiler's bookkeeping makes it wait for all copies wherever its register is reused.
   wait_vmcnt0();
@@ -263,6 +304,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
 
   f32x16_t acc[4][2];
   int stores_prev = 0;  // epilogue stores this wave issued at the previous tile's end
+  int tpar = 0;         // fp8: scale buffer of the current tile
   for (;;) {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -320,7 +362,23 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
   } while (0)
 #define Q38_COMPUTE()                                                                      \
   do {                                                                                     \
-    if (active) {                                                                          \
+    if (active && FP8) {                                                                   \
+      /* e4m3: one 32x32x64 MFMA per block and slice; lane half lh takes the slice's */    \
+      /* 16-byte chunks 2lh, 2lh+1 of its row in both operands (any k order shared by */   \
+      /* both operands gives the same dot product). */                                     \
+      const uint16_t* as_ = ring_a + ra * SLOT_ELEMS;                                      \
+      const uint16_t* bs_ = ring_w + rw * SLOT_ELEMS;                                      \
+      i32x8_t wf8[4], af8[2];                                                              \
+      _Pragma("unroll") for (int t = 0; t < 4; ++t)                                        \
+        wf8[t] = cat8(ld16(bs_ + swz(128 * wn + 32 * t + lr, 2 * lh)),                     \
+                      ld16(bs_ + swz(128 * wn + 32 * t + lr, 2 * lh + 1)));                \
+      _Pragma("unroll") for (int mi = 0; mi < 2; ++mi)                                     \
+        af8[mi] = cat8(ld16(as_ + swz(64 * wm + 32 * mi + lr, 2 * lh)),                    \
+                       ld16(as_ + swz(64 * wm + 32 * mi + lr, 2 * lh + 1)));               \
+      _Pragma("unroll") for (int t = 0; t < 4; ++t)                                        \
+        _Pragma("unroll") for (int mi = 0; mi < 2; ++mi)                                   \
+          acc[t][mi] = mfma32x32x64_fp8(wf8[t], af8[mi], acc[t][mi]);                      \
+    } else if (active) {                                                                   \
       const uint16_t* as_ = ring_a + ra * SLOT_ELEMS;                                      \
       const uint16_t* bs_ = ring_w + rw * SLOT_ELEMS;                                      \
       u32x4_t wf[2][4], af[2][2];                                                          \
@@ -341,6 +399,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
     fill = fill + 1 == ring_n ? 0 : fill + 1;                                              \
   } while (0)
 
+    // fp8: the next tile's scales go to the other buffer once the step-0 barrier has retired the
+    // previous tile's epilogue reads of it.
+#define Q38_NEXT_SCALES()                                                                  \
+  do {                                                                                     \
+    if (FP8 && kt == 0 && has_next) Q38_SCALES(tpar ^ 1, tin, Ln % p.ntiles_n);            \
+  } while (0)
     // Phase 1: this wave's copy at step kt is this tile's slice kt + dist.
     const int p1 = nk - dist;
     const int head = min(dist, p1);
@@ -348,6 +412,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
     for (; kt < head; ++kt) {  // kt < dist: the previous epilogue's stores follow the slice
       if (steady) Q38_WAIT_STEADY(stores_prev != 0);
       else Q38_WAIT_BARRIER(4 * (dist - 1) + stores_prev);
+      Q38_NEXT_SCALES();
       Q38_ISSUE(fill, src, kt + dist);
       Q38_COMPUTE();
     }
@@ -363,10 +428,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
     for (; kt < nk; ++kt) {
       if (steady && has_next) Q38_WAIT_STEADY(kt < dist && stores_prev != 0);
       else Q38_WAIT_BARRIER(4 * (has_next ? dist - 1 : nk - 1 - kt) + Q38_STORES_AFTER(kt));
+      Q38_NEXT_SCALES();
       if (has_next) Q38_ISSUE(fill, src_n, kt + dist - nk);
       Q38_COMPUTE();
     }
 #undef Q38_WAIT_BARRIER
+#undef Q38_NEXT_SCALES
 #undef Q38_WAIT_STEADY
 #undef Q38_STORES_AFTER
 #undef Q38_NEXT_SOURCES
@@ -384,6 +451,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
     if (active) {
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
+        // fp8: dequantisation by the activation row's and the weight rows' scales.
+        const float sa = FP8 ? sc_a[tpar][64 * wm + 32 * mi + lr] : 1.0f;
 #pragma unroll
         for (int tp = 0; tp < NT_OUT / 2; ++tp) {
 #pragma unroll
@@ -391,21 +460,31 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
             const int to = 2 * tp + tt;
 #pragma unroll
             for (int gq = 0; gq < 4; ++gq) {
+              f32x4_t sw0 = {1.0f, 1.0f, 1.0f, 1.0f}, sw1 = sw0;
+              if (FP8) {
+                const float* swp = &sc_w[tpar][128 * wn + 32 * to + 8 * gq + 4 * lh];
+                sw0 = *reinterpret_cast<const f32x4_t*>(swp) * sa;
+                if (MODE == MODE_GATE_UP) sw1 = *reinterpret_cast<const f32x4_t*>(swp + 64) * sa;
+              }
               uint32_t v[2];
 #pragma unroll
               for (int h2 = 0; h2 < 2; ++h2) {
                 const int i = 4 * gq + 2 * h2;
+                const float a0 = FP8 ? acc[to][mi][i] * sw0[2 * h2] : acc[to][mi][i];
+                const float a1 = FP8 ? acc[to][mi][i + 1] * sw0[2 * h2 + 1] : acc[to][mi][i + 1];
                 if (MODE == MODE_GATE_UP) {
                   // Reference rounding (inference.py:90-96): bf16 gate and up, bf16 silu(gate),
                   // bf16 product; each bf16 rounding is one packed RNE conversion of two values.
+                  const float b0 = FP8 ? acc[to + 2][mi][i] * sw1[2 * h2] : acc[to + 2][mi][i];
+                  const float b1 = FP8 ? acc[to + 2][mi][i + 1] * sw1[2 * h2 + 1] : acc[to + 2][mi][i + 1];
                   float g0, g1, u0, u1, s0, s1;
-                  unpack_bf16x2(pack_bf16x2(acc[to][mi][i], acc[to][mi][i + 1]), g0, g1);
-                  unpack_bf16x2(pack_bf16x2(acc[to + 2][mi][i], acc[to + 2][mi][i + 1]), u0, u1);
+                  unpack_bf16x2(pack_bf16x2(a0, a1), g0, g1);
+                  unpack_bf16x2(pack_bf16x2(b0, b1), u0, u1);
                   unpack_bf16x2(pack_bf16x2(g0 * __builtin_amdgcn_rcpf(1.0f + __expf(-g0)),
                                             g1 * __builtin_amdgcn_rcpf(1.0f + __expf(-g1))), s0, s1);
                   v[h2] = pack_bf16x2(s0 * u0, s1 * u1);
                 } else {
-                  v[h2] = pack_bf16x2(acc[to][mi][i], acc[to][mi][i + 1]);
+                  v[h2] = pack_bf16x2(a0, a1);
                 }
               }
               const int ch = 4 * tt + gq;
@@ -429,6 +508,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
     }
     stores_prev = active ? EPI_STORES : 0;
     if (!has_next) break;
+    tpar ^= 1;
     L = Ln;
     ti = tin;
     Ln = Lnn;
@@ -437,6 +517,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
     for (int q = 0; q < NCOPY; ++q) src[q] = src_n[q];
   }
 #undef Q38_ISSUE
+#undef Q38_SCALES
   // No LDS copy may still be landing when the workgroup's LDS is released.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
@@ -457,64 +538,118 @@ static unsigned grid_for(int max_mtiles, int ntiles_n) {
   return (unsigned)(tiles < cus[dev] ? tiles : cus[dev]);
 }
 
-hipError_t launch_gate_up(const uint16_t* x, const int32_t* perm, const int4* tiles,
-                          const int32_t* ntiles_dev, int max_mtiles, int64_t M_dense, int P,
-                          const uint16_t* w_gate_up, const uint16_t* ws_gate,
-                          const uint16_t* ws_up, uint16_t* H, int N, int K, int E, int topk,
-                          hipStream_t stream) {
+// K is in elements; e4m3 operands pass it to the kernel in 16-bit units (two elements each).
+static hipError_t gate_up_impl(const void* x, const int32_t* perm, const int4* tiles,
+                               const int32_t* ntiles_dev, int max_mtiles, int64_t M_dense, int P,
+                               const void* w_gate_up, const void* ws_gate, const void* ws_up,
+                               uint16_t* H, int N, int K, int E, int topk, bool fp8,
+                               const float* a_scale, const float* w_scale, const float* ws_scale_gate,
+                               const float* ws_scale_up, hipStream_t stream) {
   GemmParams p;
-  p.A = x;
+  p.A = static_cast<const uint16_t*>(x);
   p.perm = perm;
   p.tiles = tiles;
   p.ntiles_dev = ntiles_dev;
   p.ntiles_host = tiles != nullptr ? 0 : (int)((M_dense + BM - 1) / BM);
   p.M = M_dense;
-  p.W = w_gate_up;
-  p.Ws_a = ws_gate;
-  p.Ws_b = ws_up;
+  p.W = static_cast<const uint16_t*>(w_gate_up);
+  p.Ws_a = static_cast<const uint16_t*>(ws_gate);
+  p.Ws_b = static_cast<const uint16_t*>(ws_up);
   p.C = H;
   p.P = P;
   p.N = N;
-  p.K = K;
+  p.K = fp8 ? K / 2 : K;
   p.E = E;
   p.topk = topk;
   p.ntiles_n = (N + 127) / 128;
+  p.a_scale = a_scale;
+  p.w_scale = w_scale;
+  p.ws_scale_a = ws_scale_gate;
+  p.ws_scale_b = ws_scale_up;
   const int mt = tiles != nullptr ? max_mtiles : p.ntiles_host;
   if (mt == 0) return hipSuccess;
   const dim3 grid(grid_for(mt, p.ntiles_n));
-  if (K / BK >= 2 * (NA - 1) + 1)
-    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, true>), grid, dim3(NTHREADS), 0, stream, p);
+  const bool async_rows = p.K / BK >= 2 * (NA - 1) + 1;
+  if (fp8 && async_rows)
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, true, true>), grid, dim3(NTHREADS), 0, stream, p);
+  else if (fp8)
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, false, true>), grid, dim3(NTHREADS), 0, stream, p);
+  else if (async_rows)
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, true, false>), grid, dim3(NTHREADS), 0, stream, p);
   else
-    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, false>), grid, dim3(NTHREADS), 0, stream, p);
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, false, false>), grid, dim3(NTHREADS), 0, stream, p);
   return hipGetLastError();
+}
+
+static hipError_t down_impl(const void* H, const int4* tiles, const int32_t* ntiles_dev,
+                            int max_mtiles, int64_t M_dense, const void* w_down, const void* ws_down,
+                            uint16_t* Y, int N, int K, int E, bool fp8, const float* a_scale,
+                            const float* w_scale, const float* ws_scale, hipStream_t stream) {
+  GemmParams p;
+  p.A = static_cast<const uint16_t*>(H);
+  p.perm = nullptr;
+  p.tiles = tiles;
+  p.ntiles_dev = ntiles_dev;
+  p.ntiles_host = tiles != nullptr ? 0 : (int)((M_dense + BM - 1) / BM);
+  p.M = M_dense;
+  p.W = static_cast<const uint16_t*>(w_down);
+  p.Ws_a = static_cast<const uint16_t*>(ws_down);
+  p.Ws_b = nullptr;
+  p.C = Y;
+  p.P = 0;
+  p.N = N;
+  p.K = fp8 ? K / 2 : K;
+  p.E = E;
+  p.topk = 1;
+  p.ntiles_n = (N + BW - 1) / BW;
+  p.a_scale = a_scale;
+  p.w_scale = w_scale;
+  p.ws_scale_a = ws_scale;
+  p.ws_scale_b = nullptr;
+  const int mt = tiles != nullptr ? max_mtiles : p.ntiles_host;
+  if (mt == 0) return hipSuccess;
+  const dim3 grid(grid_for(mt, p.ntiles_n));
+  if (fp8)
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_DOWN, false, true>), grid, dim3(NTHREADS), 0, stream, p);
+  else
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_DOWN, false, false>), grid, dim3(NTHREADS), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_gate_up(const uint16_t* x, const int32_t* perm, const int4* tiles,
+                          const int32_t* ntiles_dev, int max_mtiles, int64_t M_dense, int P,
+                          const uint16_t* w_gate_up, const uint16_t* ws_gate,
+                          const uint16_t* ws_up, uint16_t* H, int N, int K, int E, int topk,
+                          hipStream_t stream) {
+  return gate_up_impl(x, perm, tiles, ntiles_dev, max_mtiles, M_dense, P, w_gate_up, ws_gate, ws_up, H, N, K,
+                      E, topk, false, nullptr, nullptr, nullptr, nullptr, stream);
 }
 
 hipError_t launch_down(const uint16_t* H, const int4* tiles, const int32_t* ntiles_dev,
                        int max_mtiles, int64_t M_dense, const uint16_t* w_down,
                        const uint16_t* ws_down, uint16_t* Y, int N, int K, int E,
                        hipStream_t stream) {
-  GemmParams p;
-  p.A = H;
-  p.perm = nullptr;
-  p.tiles = tiles;
-  p.ntiles_dev = ntiles_dev;
-  p.ntiles_host = tiles != nullptr ? 0 : (int)((M_dense + BM - 1) / BM);
-  p.M = M_dense;
-  p.W = w_down;
-  p.Ws_a = ws_down;
-  p.Ws_b = nullptr;
-  p.C = Y;
-  p.P = 0;
-  p.N = N;
-  p.K = K;
-  p.E = E;
-  p.topk = 1;
-  p.ntiles_n = (N + BW - 1) / BW;
-  const int mt = tiles != nullptr ? max_mtiles : p.ntiles_host;
-  if (mt == 0) return hipSuccess;
-  const dim3 grid(grid_for(mt, p.ntiles_n));
-  hipLaunchKernelGGL((grouped_gemm_kernel<MODE_DOWN, false>), grid, dim3(NTHREADS), 0, stream, p);
-  return hipGetLastError();
+  return down_impl(H, tiles, ntiles_dev, max_mtiles, M_dense, w_down, ws_down, Y, N, K, E, false, nullptr,
+                   nullptr, nullptr, stream);
+}
+
+hipError_t launch_gate_up_fp8(const uint8_t* xq, const int32_t* perm, const int4* tiles,
+                              const int32_t* ntiles_dev, int max_mtiles, int64_t M_dense, int P,
+                              const float* a_scale, const uint8_t* wq_gate_up, const float* s_gate_up,
+                              const uint8_t* wq_sh_gate, const float* s_sh_gate,
+                              const uint8_t* wq_sh_up, const float* s_sh_up, uint16_t* H, int N,
+                              int K, int E, int topk, hipStream_t stream) {
+  return gate_up_impl(xq, perm, tiles, ntiles_dev, max_mtiles, M_dense, P, wq_gate_up, wq_sh_gate, wq_sh_up, H,
+                      N, K, E, topk, true, a_scale, s_gate_up, s_sh_gate, s_sh_up, stream);
+}
+
+hipError_t launch_down_fp8(const uint8_t* Hq, const int4* tiles, const int32_t* ntiles_dev,
+                           int max_mtiles, int64_t M_dense, const float* a_scale,
+                           const uint8_t* wq_down, const float* s_down, const uint8_t* wq_sh_down,
+                           const float* s_sh_down, uint16_t* Y, int N, int K, int E,
+                           hipStream_t stream) {
+  return down_impl(Hq, tiles, ntiles_dev, max_mtiles, M_dense, wq_down, wq_sh_down, Y, N, K, E, true, a_scale,
+                   s_down, s_sh_down, stream);
 }
 
 }  // namespace q38

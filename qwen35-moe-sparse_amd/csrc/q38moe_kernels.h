@@ -16,7 +16,8 @@ hipError_t launch_histogram(const void* idx, bool idx64, int32_t* hist, int64_t 
 hipError_t launch_permute(const void* idx, bool idx64, const int32_t* hist, int32_t* counts,
                           int32_t* starts, int32_t* perm, int32_t* inv, int4* tiles,
                           int32_t* tile_count, int block_m, int max_tiles, int shared_rows,
-                          int64_t T, int E, int k, hipStream_t stream);
+                          int64_t T, int E, int k, hipStream_t stream,
+                          const float* row_scale_in = nullptr, float* row_scale_out = nullptr);
 
 // Rows per grouped-GEMM tile.
 int gemm_block_m();
@@ -36,8 +37,27 @@ hipError_t launch_down(const uint16_t* H, const int4* tiles, const int32_t* ntil
                        const uint16_t* ws_down, uint16_t* Y, int N, int K, int E,
                        hipStream_t stream);
 
+// e4m3 forms (fp8 expert path): A rows and weights e4m3 (K elements per row), fp32 scales per
+// GEMM row (a_scale, the sorted row space) and per weight row; outputs bf16 as above.
+hipError_t launch_gate_up_fp8(const uint8_t* xq, const int32_t* perm, const int4* tiles,
+                              const int32_t* ntiles_dev, int max_mtiles, int64_t M_dense, int P,
+                              const float* a_scale, const uint8_t* wq_gate_up, const float* s_gate_up,
+                              const uint8_t* wq_sh_gate, const float* s_sh_gate,
+                              const uint8_t* wq_sh_up, const float* s_sh_up, uint16_t* H, int N,
+                              int K, int E, int topk, hipStream_t stream);
+hipError_t launch_down_fp8(const uint8_t* Hq, const int4* tiles, const int32_t* ntiles_dev,
+                           int max_mtiles, int64_t M_dense, const float* a_scale,
+                           const uint8_t* wq_down, const float* s_down, const uint8_t* wq_sh_down,
+                           const float* s_sh_down, uint16_t* Y, int N, int K, int E,
+                           hipStream_t stream);
+
 hipError_t launch_combine(const uint16_t* Y, const int32_t* inv, const void* idx, bool idx64,
                           const uint16_t* w, const uint16_t* shared, const uint16_t* gate,
                           uint16_t* out, int64_t T, int h, int E, int k, hipStream_t stream);
+
+// Per-row e4m3 quantisation (fp8 expert path): q [R,C] e4m3 bytes, scale [R] fp32 (C % 64 == 0,
+// C <= 4096).
+hipError_t launch_quant_rows(const uint16_t* x, uint8_t* q, float* scale, int64_t R, int C,
+                             hipStream_t stream);
 
 }  // namespace q38

@@ -38,7 +38,8 @@ __global__ __launch_bounds__(256) void permute_kernel(
     const IdxT* __restrict__ idx, const int32_t* __restrict__ hist, int64_t T, int E, int k,
     int nblk, int32_t* __restrict__ counts, int32_t* __restrict__ starts,
     int32_t* __restrict__ perm, int32_t* __restrict__ inv, int4* __restrict__ tiles,
-    int32_t* __restrict__ tile_count, int block_m, int max_tiles, int shared_rows) {
+    int32_t* __restrict__ tile_count, int block_m, int max_tiles, int shared_rows,
+    const float* __restrict__ row_scale_in, float* __restrict__ row_scale_out) {
   constexpr int NCHUNK = PERM_TOKENS * PERM_KMAX / 64;  // 64-pair chunks per block (<= 8)
   __shared__ int s_tot[4][64];
   __shared__ int s_bef[4][64];
@@ -162,9 +163,15 @@ __global__ __launch_bounds__(256) void permute_kernel(
       if (off < cap) {
         perm[off] = (int32_t)pair;
         if (inv != nullptr) inv[pair] = off;
+        // fp8 path: the token's quantisation scale follows its row into sorted order.
+        if (row_scale_out != nullptr) row_scale_out[off] = row_scale_in[pair / k];
       }
     }
   }
+
+  // fp8 path: shared-expert rows P + t take token t's scale.
+  if (row_scale_out != nullptr && tid < t1 - t0 && t0 + tid < shared_rows)
+    row_scale_out[cap + t0 + tid] = row_scale_in[t0 + tid];
 
   if (b == 0 && tiles != nullptr) {
     // Tile table, in the order the persistent grouped GEMM walks it: every full tile (block_m
@@ -223,18 +230,19 @@ hipError_t launch_histogram(const void* idx, bool idx64, int32_t* hist, int64_t 
 hipError_t launch_permute(const void* idx, bool idx64, const int32_t* hist, int32_t* counts,
                           int32_t* starts, int32_t* perm, int32_t* inv, int4* tiles,
                           int32_t* tile_count, int block_m, int max_tiles, int shared_rows,
-                          int64_t T, int E, int k, hipStream_t stream) {
+                          int64_t T, int E, int k, hipStream_t stream, const float* row_scale_in,
+                          float* row_scale_out) {
   // At least one block, so T == 0 still writes zero counts and an empty tile table.
   const int64_t nblk = (T + PERM_TOKENS - 1) / PERM_TOKENS;
   const unsigned grid = (unsigned)(nblk > 0 ? nblk : 1);
   if (idx64)
     hipLaunchKernelGGL(permute_kernel<int64_t>, dim3(grid), dim3(256), 0, stream,
                        (const int64_t*)idx, hist, T, E, k, (int)nblk, counts, starts, perm, inv,
-                       tiles, tile_count, block_m, max_tiles, shared_rows);
+                       tiles, tile_count, block_m, max_tiles, shared_rows, row_scale_in, row_scale_out);
   else
     hipLaunchKernelGGL(permute_kernel<int32_t>, dim3(grid), dim3(256), 0, stream,
                        (const int32_t*)idx, hist, T, E, k, (int)nblk, counts, starts, perm, inv,
-                       tiles, tile_count, block_m, max_tiles, shared_rows);
+                       tiles, tile_count, block_m, max_tiles, shared_rows, row_scale_in, row_scale_out);
   return hipGetLastError();
 }
 

@@ -287,3 +287,106 @@ def block_forward(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_sh_down,
     if return_router:
         return out, logits, idx, w
     return out
+
+
+# ---- fp8 expert path (R14: e4m3 experts with per-output-channel scales; no reference function) ----
+
+FP8_WEIGHT_NAMES = ("experts.gate_up_proj", "experts.down_proj", "shared_expert.gate_proj.weight",
+                    "shared_expert.up_proj.weight", "shared_expert.down_proj.weight")
+
+
+def quantize_rows(x):
+    """Per-row e4m3 quantisation of x [..., C] bf16 (C % 64 == 0, C <= 4096): returns
+    (q uint8 [..., C] = torch.float8_e4m3fn bit patterns, scale fp32 [...]) with x ~ q * scale
+    (amax/448 per row, round-to-nearest-even, saturating at +-448)."""
+    _need(x, "x", dtype=torch.bfloat16)
+    C = x.shape[-1]
+    R = x.numel() // C if C else 0
+    q = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    scale = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    check(lib.q38moe_quantize_rows(_ptr(x), _ptr(q), _ptr(scale), R, C, _stream(x.device)), "q38moe_quantize_rows")
+    return q, scale
+
+
+def quantize_weights_fp8(params):
+    """e4m3 copies of the expert weights of a MoE block's state dict (per-output-channel scales):
+    {name: (q uint8, scale fp32)} for the routed gate_up [E,2I,h] / down [E,h,I] projections and the
+    shared expert's gate/up [I,h] and down [h,I] projections. Done once, at load time."""
+    return {n: quantize_rows(params[n].contiguous()) for n in FP8_WEIGHT_NAMES}
+
+
+def gate_up_fp8(xq, row_scale, wq, perm, tiles, tile_count, k, shared_rows=0):
+    """Grouped gate/up GEMM on e4m3 (q38moe_gate_up_fp8): xq [T,h] uint8 e4m3 tokens, row_scale
+    [T*k + shared_rows] fp32 in sorted row order, wq = quantize_weights_fp8(...). H bf16."""
+    _need(xq, "xq", dtype=torch.uint8, ndim=2)
+    _need(row_scale, "row_scale", dtype=torch.float32, ndim=1)
+    qg, sg = wq["experts.gate_up_proj"]
+    T, h = xq.shape
+    E, twoI, _ = qg.shape
+    I = twoI // 2
+    if row_scale.numel() != T * k + shared_rows:
+        raise ValueError("row_scale must hold T*k + shared_rows entries")
+    (qsg, ssg), (qsu, ssu) = wq["shared_expert.gate_proj.weight"], wq["shared_expert.up_proj.weight"]
+    H = torch.empty(T * k + shared_rows, I, dtype=torch.bfloat16, device=xq.device)
+    check(lib.q38moe_gate_up_fp8(_ptr(xq), _ptr(row_scale), _ptr(qg), _ptr(sg), _ptr(qsg), _ptr(ssg), _ptr(qsu),
+                                 _ptr(ssu), _ptr(perm), _ptr(tiles), _ptr(tile_count), shared_rows, _ptr(H), T, h, E,
+                                 k, I, _stream(xq.device)), "q38moe_gate_up_fp8")
+    return H
+
+
+def down_fp8(Hq, row_scale, wq, tiles, tile_count, T, k, shared_rows=0):
+    """Grouped down GEMM on e4m3 (q38moe_down_fp8): Hq [T*k + shared_rows, I] uint8, row_scale per
+    row; Y bf16 [rows, h]."""
+    _need(Hq, "Hq", dtype=torch.uint8, ndim=2)
+    _need(row_scale, "row_scale", dtype=torch.float32, ndim=1)
+    qd, sd = wq["experts.down_proj"]
+    E, h, I = qd.shape
+    qsd, ssd = wq["shared_expert.down_proj.weight"]
+    Y = torch.empty(T * k + shared_rows, h, dtype=torch.bfloat16, device=Hq.device)
+    check(lib.q38moe_down_fp8(_ptr(Hq), _ptr(row_scale), _ptr(qd), _ptr(sd), _ptr(qsd), _ptr(ssd), _ptr(tiles),
+                              _ptr(tile_count), shared_rows, _ptr(Y), T, h, E, k, I, _stream(Hq.device)),
+          "q38moe_down_fp8")
+    return Y
+
+
+def block_fp8_workspace_bytes(T, h, E, k, I):
+    n = ctypes.c_size_t()
+    check(lib.q38moe_block_fp8_workspace_bytes(T, h, E, k, I, ctypes.byref(n)), "q38moe_block_fp8_workspace_bytes")
+    return n.value
+
+
+def block_forward_fp8(x, w_router, wq, w_sh_gate_proj, k, logit_bias=None, return_router=False, workspace=None,
+                      out=None):
+    """The MoE block with e4m3 experts (q38moe_block_forward_fp8): bf16 router and shared gate,
+    per-token e4m3 tokens, e4m3 gate/up and down GEMMs with the weights of quantize_weights_fp8."""
+    _need(x, "x", ndim=2)
+    _need(w_router, "w_router", ndim=2)
+    _need(w_sh_gate_proj, "w_sh_gate_proj")
+    T, h = x.shape
+    E = w_router.shape[0]
+    (qg, sg), (qd, sd) = wq["experts.gate_up_proj"], wq["experts.down_proj"]
+    (qsg, ssg), (qsu, ssu), (qsd, ssd) = (wq["shared_expert.gate_proj.weight"], wq["shared_expert.up_proj.weight"],
+                                          wq["shared_expert.down_proj.weight"])
+    I = qg.shape[1] // 2
+    if qg.shape != (E, 2 * I, h) or qd.shape != (E, h, I) or qsg.shape != (I, h) or qsd.shape != (h, I):
+        raise ValueError("fp8 weights must be gate_up [E,2I,h], down [E,h,I], shared [I,h]/[h,I] (Is == I)")
+    if logit_bias is not None:
+        _need(logit_bias, "logit_bias", dtype=torch.float32, ndim=1)
+    dev = x.device
+    nbytes = block_fp8_workspace_bytes(T, h, E, k, I)
+    if workspace is None or workspace.numel() < nbytes:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    if out is None:
+        out = torch.empty(T, h, dtype=torch.bfloat16, device=dev)
+    logits = idx = w = None
+    if return_router:
+        logits = torch.empty(T, E, dtype=torch.bfloat16, device=dev)
+        idx = torch.empty(T, k, dtype=torch.int32, device=dev)
+        w = torch.empty(T, k, dtype=torch.bfloat16, device=dev)
+    check(lib.q38moe_block_forward_fp8(_ptr(x), _ptr(w_router), _ptr(qg), _ptr(sg), _ptr(qd), _ptr(sd), _ptr(qsg),
+                                       _ptr(ssg), _ptr(qsu), _ptr(ssu), _ptr(qsd), _ptr(ssd), _ptr(w_sh_gate_proj),
+                                       _ptr(logit_bias), _ptr(out), _ptr(logits), _ptr(idx), _ptr(w), T, h, E, k, I,
+                                       _ptr(workspace), workspace.numel(), _stream(dev)), "q38moe_block_forward_fp8")
+    if return_router:
+        return out, logits, idx, w
+    return out

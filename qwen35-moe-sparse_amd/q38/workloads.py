@@ -83,7 +83,8 @@ WORKLOADS = {
     # seeded inputs for a ~20x span of expert loads: max 7620 / min 369 pairs (20.7x).
     "c3": Workload("c3", hidden=1024, experts=64, topk=5, inter=256, shared_inter=256, batch=4, seq=4096,
                    zipf_s=1.2, zipf_alpha=0.24),
-    # FP8 expert path shape (bf16 here until the fp8 kernels exist).
+    # FP8 expert path: bf16 router and activations, e4m3 expert weights (per-output-channel
+    # scales) and per-token e4m3 expert inputs (q38moe_block_forward_fp8).
     "c4": Workload("c4", hidden=2048, experts=64, topk=5, inter=512, shared_inter=512, batch=8, seq=4096,
                    dtype="fp8"),
 }
