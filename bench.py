@@ -21,6 +21,7 @@ sys.path.insert(0, str(REPO))
 
 METRIC = "MoE-layer tokens/sec at 16K tokens bf16 (1 GPU) + % MFMA peak"
 PEAK_BF16 = 2.5e15   # dense bf16 MFMA, MI355X datasheet
+PEAK_FP8 = 5.0e15    # dense fp8 MFMA, MI355X datasheet
 PEAK_HBM = 8.0e12    # HBM3E bytes/s
 
 
@@ -84,6 +85,50 @@ def kernel_breakdown(wl, x, d, bias, iters, stream):
         dt = time_stream(fn, iters, stream)
         if bound == "mfma":
             achieved, peak, unit = work / dt / 1e12, PEAK_BF16 / 1e12, "TFLOP/s"
+        else:
+            achieved, peak, unit = work / dt / 1e9, PEAK_HBM / 1e9, "GB/s"
+        out[name] = dict(us=round(dt * 1e6, 2), bound=bound, work=work, achieved=round(achieved, 2),
+                         peak=peak, unit=unit, frac=round(achieved / peak, 4))
+    return out
+
+
+def kernel_breakdown_fp8(wl, x, d, wq, bias, iters, stream):
+    """Per-stage durations of the fp8 block (e4m3 experts), each stage relaunched alone."""
+    import torch
+    from q38.hip import ops
+    T, h, E, k, I = wl.tokens, wl.hidden, wl.experts, wl.topk, wl.inter
+    P = T * k
+    logits, idx, w, gate, hist = ops.route(x, d["gate.weight"], k, w_shared_gate=d["shared_expert_gate.weight"],
+                                           logit_bias=bias, want_hist=True)
+    xq, sx = ops.quantize_rows(x)
+    counts, starts, perm, inv, tiles, tcount = ops.permute(idx, hist, E, shared_rows=T)
+    row_scale = torch.cat([sx[perm.long() // k], sx])
+    H = ops.gate_up_fp8(xq, row_scale, wq, perm, tiles, tcount, k, shared_rows=T)
+    Hq, sH = ops.quantize_rows(H)
+    Y = ops.down_fp8(Hq, sH, wq, tiles, tcount, T, k, shared_rows=T)
+    torch.cuda.synchronize()
+    fl = wl.flops()
+    stages = {
+        "route": (lambda: ops.route(x, d["gate.weight"], k, w_shared_gate=d["shared_expert_gate.weight"],
+                                    logit_bias=bias, want_hist=True), "hbm",
+                  T * h * 2 + (E + 1) * h * 2 + P * 6 + T * 2),
+        # x read (bf16) + e4m3 codes and scales written
+        "quant_x": (lambda: ops.quantize_rows(x), "hbm", T * h * 3 + T * 4),
+        "permute": (lambda: ops.permute(idx, hist, E, shared_rows=T), "hbm", P * 4 * 3),
+        "gate_up": (lambda: ops.gate_up_fp8(xq, row_scale, wq, perm, tiles, tcount, k, shared_rows=T), "mfma",
+                    fl["gate_up"] + fl["shared"] * 2 // 3),
+        "quant_h": (lambda: ops.quantize_rows(H), "hbm", (P + T) * I * 3 + (P + T) * 4),
+        "down": (lambda: ops.down_fp8(Hq, sH, wq, tiles, tcount, T, k, shared_rows=T), "mfma",
+                 fl["down"] + fl["shared"] // 3),
+        "combine": (lambda: ops.combine(Y, inv, w, E, shared_out=Y[P:], shared_gate_logit=gate), "hbm",
+                    T * h * 2 * (k + 2)),
+    }
+    out = {}
+    for name, (fn, bound, work) in stages.items():
+        fn()
+        dt = time_stream(fn, iters, stream)
+        if bound == "mfma":
+            achieved, peak, unit = work / dt / 1e12, PEAK_FP8 / 1e12, "TFLOP/s"
         else:
             achieved, peak, unit = work / dt / 1e9, PEAK_HBM / 1e9, "GB/s"
         out[name] = dict(us=round(dt * 1e6, 2), bound=bound, work=work, achieved=round(achieved, 2),
@@ -209,9 +254,19 @@ def main():
     out = torch.empty(T, h, dtype=torch.bfloat16, device=dev)
     weights = [d[n] for n in workloads.PARAM_ORDER]
     stream = torch.cuda.current_stream(dev)
+    fp8 = wl.dtype == "fp8"
+    if fp8:
+        # e4m3 expert weights with per-output-channel scales, quantised once before timing (load time).
+        wq = ops.quantize_weights_fp8(d)
+        ws = torch.empty(ops.block_fp8_workspace_bytes(T, h, wl.experts, k, wl.inter), dtype=torch.uint8,
+                         device=dev)
 
     def step():
-        ops.block_forward(x, *weights, k, logit_bias=bias, workspace=ws, out=out)
+        if fp8:
+            ops.block_forward_fp8(x, d["gate.weight"], wq, d["shared_expert_gate.weight"], k, logit_bias=bias,
+                                  workspace=ws, out=out)
+        else:
+            ops.block_forward(x, *weights, k, logit_bias=bias, workspace=ws, out=out)
 
     with torch.inference_mode():
         for _ in range(args.warmup):
@@ -228,7 +283,8 @@ def main():
         torch.cuda.synchronize()
         ms = start.elapsed_time(end) / args.steps
         log(f"[bench] timed {args.steps} steps: {ms:.4f} ms/step")
-        kernels = kernel_breakdown(wl, x, d, bias, args.kernel_iters, stream)
+        kernels = (kernel_breakdown_fp8(wl, x, d, wq, bias, args.kernel_iters, stream) if fp8 else
+                   kernel_breakdown(wl, x, d, bias, args.kernel_iters, stream))
         log(f"[bench] kernels: " + ", ".join(f"{n} {v['us']}us" for n, v in kernels.items()))
 
     fl = wl.flops()
@@ -247,7 +303,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp8 e4m3 experts (fp32 accumulate), bf16 router/activations" if fp8 else "bf16",
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights; no checkpoint)",
         "config": {"workload": f"{wl.name}: one Q38 MoE block forward, {wl.batch}x{wl.seq} packed tokens",
                    "tokens": T, "hidden": h, "experts": wl.experts, "top_k": k, "expert_inter": wl.inter,
@@ -256,8 +312,8 @@ def main():
                      "unit": dk["unit"], "frac": dk["frac"], "traffic": hbm_traffic(wl.name, dom),
                      "work_per_launch": dk["work"]},
         # Routed + shared expert GEMM FLOPs over the two grouped launches that compute them.
-        "mfma_frac_expert_gemms": round(expert_fl / (expert_us * 1e-6) / PEAK_BF16, 4),
-        "mfma_frac_block": round(fl["block"] / (ms * 1e-3) / PEAK_BF16, 4),
+        "mfma_frac_expert_gemms": round(expert_fl / (expert_us * 1e-6) / (PEAK_FP8 if fp8 else PEAK_BF16), 4),
+        "mfma_frac_block": round(fl["block"] / (ms * 1e-3) / (PEAK_FP8 if fp8 else PEAK_BF16), 4),
         "kernels": kernels,
     }
     if not args.no_cpu_baseline:
