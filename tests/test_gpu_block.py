@@ -158,3 +158,40 @@ def test_dropin_module_and_registry(gpu):
     with pytest.raises(RuntimeError, match="no backward"):
         block.float().requires_grad_(True)
         block(x.view(1, -1, wl.hidden).to(gpu).float())
+
+
+# Shapes off the benchmark configs: few or single experts, k = 1 (torch's partial_sort path when
+# k*64 <= E), k = 8, the smallest hidden/intermediate sizes (one or two K slices), ragged and single
+# tokens, and a shared expert narrower than the routed ones (separate dense shared GEMMs).
+EDGE_SHAPES = [
+    dict(experts=8, topk=2, hidden=128, inter=64, shared_inter=64, T=100),
+    dict(experts=1, topk=1, hidden=64, inter=64, shared_inter=64, T=37),
+    dict(experts=64, topk=1, hidden=256, inter=64, shared_inter=64, T=1),
+    dict(experts=64, topk=8, hidden=256, inter=128, shared_inter=64, T=300),
+    dict(experts=16, topk=4, hidden=512, inter=192, shared_inter=192, T=2000),
+]
+
+
+@pytest.mark.parametrize("shape", EDGE_SHAPES, ids=lambda s: "E{experts}k{topk}h{hidden}I{inter}Is{shared_inter}T{T}".format(**s))
+def test_block_forward_edge_shapes(gpu, shape):
+    ops = _ops()
+    shape = dict(shape)
+    T = shape.pop("T")
+    wl, x, params, _ = _setup("c2", T, **shape)
+    d = {n: p.to(gpu) for n, p in params.items()}
+    out, logits, idx, w = ops.block_forward(
+        x.to(gpu), d["gate.weight"], d["experts.gate_up_proj"], d["experts.down_proj"],
+        d["shared_expert.gate_proj.weight"], d["shared_expert.up_proj.weight"], d["shared_expert.down_proj.weight"],
+        d["shared_expert_gate.weight"], wl.topk, return_router=True)
+    torch.cuda.synchronize()
+    _, _, sidx, _ = orc.router(None, None, wl.topk, logits=logits.cpu())
+    assert torch.equal(idx.cpu().long(), sidx)
+    ref_out, _ = orc.block(x, params, wl.topk)
+    # The oracle block routes on CPU-computed logits; re-run its experts on the GPU's routing.
+    _, _, _, rw = orc.router(None, None, wl.topk, logits=logits.cpu())
+    routed, _, _ = orc.experts_grouped(x, sidx, rw, params["experts.gate_up_proj"], params["experts.down_proj"])
+    sh = orc.shared_expert(x, params["shared_expert.gate_proj.weight"], params["shared_expert.up_proj.weight"],
+                           params["shared_expert.down_proj.weight"])
+    gl = orc.bf16(orc._f(x) @ orc._f(params["shared_expert_gate.weight"]).reshape(-1))
+    ref = orc.bf16(orc._f(routed) + orc._f(orc.bf16(orc._f(orc.bf16(torch.sigmoid(orc._f(gl))))[:, None] * orc._f(sh))))
+    assert_bf16_close(out.cpu(), ref, what=f"edge block {shape}")

@@ -131,3 +131,30 @@ def test_block_forward_fp8(gpu, name, T):
     rel_bf16 = float((out.cpu().float() - bf_out.float()).norm() / bf_out.float().norm())
     print(f"{name} T={T}: vs fake-quant max-abs {mx:.3e} rel {r:.3e}; vs bf16 block rel {rel_bf16:.3e}")
     assert rel_bf16 < 8e-2
+
+
+@pytest.mark.parametrize("shape", [
+    dict(experts=8, topk=2, hidden=128, inter=64, T=100),
+    dict(experts=1, topk=1, hidden=64, inter=64, T=37),
+    dict(experts=64, topk=8, hidden=256, inter=128, T=300),
+    dict(experts=16, topk=4, hidden=512, inter=192, T=1),
+], ids=lambda s: "E{experts}k{topk}h{hidden}I{inter}T{T}".format(**s))
+def test_block_forward_fp8_edge_shapes(gpu, shape):
+    """fp8 block off the benchmark shapes: one or two K slices (down on I = 64 is a single e4m3
+    slice), few experts, k = 1 and 8, a single token."""
+    from q38 import workloads
+    ops = _ops()
+    shape = dict(shape)
+    T = shape.pop("T")
+    wl = workloads.get("c4", shared_inter=shape["inter"], **shape)
+    x, params, _ = workloads.make(wl, tokens=T)
+    d = {n: p.to(gpu) for n, p in params.items()}
+    wq = ops.quantize_weights_fp8(d)
+    out, logits, idx, w = ops.block_forward_fp8(x.to(gpu), d["gate.weight"], wq, d["shared_expert_gate.weight"],
+                                                wl.topk, return_router=True)
+    torch.cuda.synchronize()
+    _, _, sidx, _ = orc.router(None, None, wl.topk, logits=logits.cpu())
+    assert torch.equal(idx.cpu().long(), sidx)
+    gate_logit = orc.bf16(orc._f(x) @ orc._f(params["shared_expert_gate.weight"]).reshape(-1))
+    ref_out, _ = orc.experts_fp8(x, idx.cpu().long(), w.cpu(), orc.quant_weights_fp8(params), wl.topk, gate_logit)
+    assert_bf16_close(out.cpu(), ref_out, max_abs=5e-2, what=f"fp8 edge block {shape}")
