@@ -218,6 +218,86 @@ def copy_probe(mib):
     log(f"[bench] copy probe: {mib} MiB read, {mib} MiB written")
 
 
+def prefill_bench(args):
+    """Workload c5: the packed no-cache prefill of a 12-layer random-init Q38 model (q38.prefill)
+    on 4 x 4096 tokens, the fused HIP MoE block in every layer; the token mixers are torch code.
+    Reports whole-model tokens/s, the share of the 12 MoE blocks, and a bounded CPU sample of the
+    same restatement (CPU oracle in place of the HIP blocks)."""
+    import torch
+    from q38 import prefill as P
+
+    cfg = P.c5_config()
+    dev = torch.device("cuda:0")
+    batch, seq = 4, 4096
+    t0 = time.time()
+    params = P.init_params(cfg, 0)
+    model = P.Q38Prefill(cfg).load_params(params).to(device=dev, dtype=torch.bfloat16)
+    ids = P.make_ids(batch, seq, cfg).to(dev)
+    log(f"[bench] c5 prefill model built in {time.time() - t0:.1f} s")
+    stream = torch.cuda.current_stream(dev)
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            model(ids)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(args.steps):
+            model(ids)
+        end.record(stream)
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / args.steps
+        log(f"[bench] timed {args.steps} prefill steps: {ms:.2f} ms/step")
+        # One MoE block on a layer-shaped input, as inside the prefill (T = batch * seq tokens).
+        blk = model.model.layers[0].mlp
+        xb = torch.randn(batch, seq, cfg.hidden, device=dev).to(torch.bfloat16)
+        for _ in range(3):
+            blk(xb)
+        start.record(stream)
+        for _ in range(20):
+            blk(xb)
+        end.record(stream)
+        torch.cuda.synchronize()
+        moe_ms = start.elapsed_time(end) / 20
+    T = batch * seq
+    res = {
+        "metric": "Q38 packed no-cache prefill tokens/sec (config 5, 1 GPU)",
+        "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded random-init parameters, uniform token ids with EOS about every 1000)",
+        "config": {"workload": f"c5: 12-layer Q38 packed prefill, {batch}x{seq} tokens", "layers": cfg.layers,
+                   "hidden": cfg.hidden, "experts": cfg.experts, "top_k": cfg.topk, "vocab": cfg.vocab,
+                   "parallelism": "single GPU"},
+        "roofline": None,
+        "moe": {"ms_per_block": round(moe_ms, 4), "blocks": cfg.layers,
+                "share_of_step": round(cfg.layers * moe_ms / ms, 4),
+                "mfma_frac_block": round(moe_block_flops(cfg, T) / (moe_ms * 1e-3) / PEAK_BF16, 4)},
+    }
+    if not args.no_cpu_baseline:
+        import oracle.moe_oracle as O
+
+        def cpu_moe(block, x):
+            w = {n: q for n, q in block.named_parameters()}
+            B, S, h = x.shape
+            return O.reference_block_forward(x.reshape(-1, h), w, block.gate.top_k).view(B, S, h)
+
+        cpu = P.Q38Prefill(cfg, moe_forward=cpu_moe).load_params(params).to(dtype=torch.bfloat16)
+        sample = P.make_ids(1, 1024, cfg)
+        t = time.time()
+        cpu(sample)
+        sec = time.time() - t
+        res["cpu_baseline"] = {"value": round(1024 / sec, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+                               "kind": "port", "sample": "one 1024-token sequence through the same 12-layer "
+                               "restatement in bf16 torch on the host cores, CPU oracle MoE blocks"}
+    print(json.dumps(res), flush=True)
+
+
+def moe_block_flops(cfg, T):
+    """MoE block FLOPs for T tokens: routed experts, shared expert, router (flops.py:25, 38-40)."""
+    h, I, Is, E, k = cfg.hidden, cfg.moe_ffn, cfg.shared_ffn, cfg.experts, cfg.topk
+    return 2 * T * k * h * 3 * I + 6 * T * h * Is + 2 * T * h * E
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -234,6 +314,9 @@ def main():
                                    "across GPUs with no exchange, run one process per GPU", "n_gpus": args.gpus}))
         sys.exit(2)
 
+    if args.workload == "c5":
+        prefill_bench(args)
+        return
     import torch
     from q38 import workloads
     from q38.hip import ops
