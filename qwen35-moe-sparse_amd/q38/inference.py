@@ -55,18 +55,30 @@ def hip_moe_block_forward(self, hidden_states):
     An optional ``routing_bias`` attribute (fp32 [E]) is added to the router logits before the
     softmax (routing-skew workload; None = reference behaviour).
     """
+    return _fused_block(self, hidden_states, False)
+
+
+def hip_moe_block_forward_with_router(self, hidden_states):
+    """``hip_moe_block_forward`` that also returns the router logits [B*S, E] (the gate's output[0],
+    modeling:805-807, what the reference's router-logits recorder keeps), from the same fused call."""
+    return _fused_block(self, hidden_states, True)
+
+
+def _fused_block(self, hidden_states, want_logits):
     weights = _block_weights(self)
     _forward_only(hidden_states, *weights)
     _check_act(getattr(getattr(self.experts, "config", None), "hidden_act", None))
     shape = hidden_states.shape
     x = hidden_states.reshape(-1, shape[-1]).contiguous()
     k = self.gate.top_k
-    out = ops.block_forward(x, *(w.contiguous() for w in weights), k,
-                            logit_bias=getattr(self, "routing_bias", None),
+    res = ops.block_forward(x, *(w.contiguous() for w in weights), k,
+                            logit_bias=getattr(self, "routing_bias", None), return_router=want_logits,
                             workspace=_workspace(self, x.device, ops.block_workspace_bytes(
                                 x.shape[0], x.shape[1], weights[0].shape[0], k, weights[1].shape[1] // 2,
                                 weights[3].shape[0])))
-    return out.view(shape)
+    if want_logits:
+        return res[0].view(shape), res[1]
+    return res.view(shape)
 
 
 def _workspace(module, device, nbytes):

@@ -24,6 +24,7 @@ import os
 import zlib
 from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass
+from typing import Optional, Tuple
 
 import numpy as np
 import torch
@@ -561,11 +562,41 @@ def _moe_default(block, x):
     return block(x)
 
 
+def load_balancing_loss(router_logits, num_experts, top_k):
+    """load_balancing_loss_func without an attention mask (modeling:1289-1355), the Switch
+    Transformer auxiliary loss: per layer, softmax of the logits (in their dtype), the top-k set,
+    per-expert assignment counts and probability sums; then E * sum_e (counts_e / rows) *
+    (prob_sum_e / rows) over all layers' rows. On the GPU the top-k set comes from torch's GPU
+    top-k: a tie at the k-th rank may resolve to the other expert than on the CPU."""
+    dev = router_logits[0].device
+    counts = torch.zeros(num_experts, dtype=torch.float32, device=dev)
+    probs = torch.zeros(num_experts, dtype=torch.float32, device=dev)
+    rows = 0
+    for lg in router_logits:
+        p = torch.softmax(lg, dim=-1)
+        chosen = torch.topk(p, top_k, dim=-1).indices
+        counts = counts + torch.bincount(chosen.reshape(-1), minlength=num_experts).float()
+        probs = probs + p.float().sum(dim=0)
+        rows += p.shape[0]
+    return torch.sum((counts / rows) * (probs / rows)) * num_experts
+
+
+@dataclass
+class PrefillOutput:
+    """The fields of MoeCausalLMOutputWithPast the packed prefill fills (modeling:1425-1433)."""
+
+    logits: torch.Tensor
+    aux_loss: Optional[torch.Tensor] = None
+    router_logits: Optional[Tuple[torch.Tensor, ...]] = None
+
+
 class Q38Prefill(nn.Module):
     """Qwen3_8MoeForCausalLM's packed no-cache prefill (modeling:1233-1275, 1398-1431): ids [B,S]
     -> logits [B,S,vocab] in the parameter dtype. Forward-only; the MoE blocks run the fused HIP
     block. ``moe_forward(block, x[B,S,h]) -> [B,S,h]`` replaces the MoE call (tests use it to put
-    the CPU oracle in place of the kernels)."""
+    the CPU oracle in place of the kernels). With ``output_router_logits`` the forward returns a
+    PrefillOutput with every layer's router logits [B*S, E] (the fused block's own) and the
+    load-balancing loss over them (modeling:1410-1427)."""
 
     def __init__(self, cfg, moe_forward=None):
         super().__init__()
@@ -585,9 +616,17 @@ class Q38Prefill(nn.Module):
         self.requires_grad_(False)
         return self
 
+    def _moe_with_router(self, block, x):
+        if self.moe_forward is _moe_default:
+            from .inference import hip_moe_block_forward_with_router
+
+            return hip_moe_block_forward_with_router(block, x)
+        return self.moe_forward(block, x), F.linear(x.reshape(-1, x.shape[-1]), block.gate.weight)
+
     @torch.no_grad()
-    def forward(self, ids):
+    def forward(self, ids, output_router_logits=False):
         cfg, M = self.cfg, self.model
+        router = [] if output_router_logits else None
         B, length = ids.shape
         if length == 0:
             raise ValueError("Q38 prefill needs at least one token")
@@ -608,12 +647,20 @@ class Q38Prefill(nn.Module):
                 y = _qsa(layer.self_attn, M.indexers[str(i)], x, cos, sin, cfg)
             X = _mhc_post(X, y, st)
             xin, st = _mhc_pre(M.mhc[2 * i + 1], X, cfg)
-            y = self.moe_forward(layer.mlp, _zc_norm(xin, layer.post_attention_layernorm.weight, cfg.rms_eps).to(dt))
+            x = _zc_norm(xin, layer.post_attention_layernorm.weight, cfg.rms_eps).to(dt)
+            if router is None:
+                y = self.moe_forward(layer.mlp, x)
+            else:
+                y, lg = self._moe_with_router(layer.mlp, x)
+                router.append(lg)
             X = _mhc_post(X, y, st)
             if i == 0 and M.ngram is not None:
                 X = X + _ngram_delta(M.ngram, X.mean(2).to(dt), ids, cfg).unsqueeze(2)
         hs = _zc_norm(X.sum(2)[:, :length].to(dt), M.norm.weight, cfg.rms_eps)
-        return F.linear(hs, M.embed_tokens.weight)
+        logits = F.linear(hs, M.embed_tokens.weight)
+        if router is None:
+            return logits
+        return PrefillOutput(logits, load_balancing_loss(router, cfg.experts, cfg.topk), tuple(router))
 
 
 def build(cfg=None, seed=0, device="cuda", dtype=torch.bfloat16, moe_forward=None):

@@ -6,9 +6,10 @@ loaded by name, on ``q38.prefill.make_ids`` input, in fp32 and in bf16. Only thi
 the reference, and only in the build container where the checkout lives at /root/reference; the
 tests read the vectors it writes (prefill_c5.npz), never the reference.
 
-The bf16 run casts the reference model with ``.to(torch.bfloat16)`` and then puts the rotary
-inverse-frequency buffers back in fp32, as a model loaded with ``from_pretrained(dtype=bf16)``
-(q38/evaluate.py:185) keeps them.
+Each run asks for ``output_router_logits`` and also stores the load-balancing loss the reference
+computes over the layers' router logits (modeling:1410-1427). The bf16 run casts the reference
+model with ``.to(torch.bfloat16)`` and then puts the rotary inverse-frequency buffers back in fp32,
+as a model loaded with ``from_pretrained(dtype=bf16)`` (q38/evaluate.py:185) keeps them.
 
 Usage: python tests/golden/make_prefill_golden.py [--batch 2 --seq 1024] [--debug /tmp/dump.pt]
 """
@@ -81,11 +82,11 @@ def run(model, ids, debug):
         model.model._layer = recording
     t = time.time()
     with torch.no_grad():
-        logits = model(input_ids=ids, use_cache=False).logits
-    print(f"  forward {time.time() - t:.1f} s", flush=True)
+        out = model(input_ids=ids, use_cache=False, output_router_logits=True)
+    print(f"  forward {time.time() - t:.1f} s, aux_loss {float(out.aux_loss):.8f}", flush=True)
     if debug:
         model.model._layer = inner
-    return logits, layers_out
+    return out.logits, float(out.aux_loss), layers_out
 
 
 def main():
@@ -108,8 +109,9 @@ def main():
                ids_seed=args.ids_seed, ids=ids.numpy().astype(np.int32), rows=np.array(ROWS, dtype=np.int32))
     dumps = {}
     print("reference fp32", flush=True)
-    logits, layers = run(model, ids, args.debug)
+    logits, aux, layers = run(model, ids, args.debug)
     lf = logits.float()
+    out["aux_loss_fp32"] = np.float64(aux)
     out["lse_fp32"] = torch.logsumexp(lf, -1).numpy()
     out["argmax_fp32"] = lf.argmax(-1).numpy().astype(np.int32)
     out["logits_fp32"] = np.stack([lf[b, s].numpy() for b, s in ROWS])
@@ -119,8 +121,9 @@ def main():
     for m in model.modules():  # fp32 rotary tables, as from_pretrained(dtype=bf16) leaves them
         if hasattr(m, "inv_freq") and hasattr(m, "compute_default_rope_parameters"):
             m.inv_freq = m.compute_default_rope_parameters(m.config)[0]
-    logits, layers = run(model, ids, args.debug)
+    logits, aux, layers = run(model, ids, args.debug)
     lf = logits.float()
+    out["aux_loss_bf16"] = np.float64(aux)
     out["lse_bf16"] = torch.logsumexp(lf, -1).numpy()
     out["argmax_bf16"] = lf.argmax(-1).numpy().astype(np.int32)
     out["logits_bf16"] = np.stack([bf16_bits(logits[b, s]) for b, s in ROWS])

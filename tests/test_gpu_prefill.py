@@ -63,9 +63,18 @@ def test_prefill_bf16_hip_within_reference_bf16_spread(gpu, golden, params):
     model = P.Q38Prefill(P.c5_config()).load_params(params).to(device=gpu, dtype=torch.bfloat16)
     ids = torch.from_numpy(golden["ids"].astype(np.int64)).to(gpu)
     with torch.inference_mode():
-        logits = model(ids)
+        out = model(ids, output_router_logits=True)
         again = model(ids)
+    logits = out.logits
     assert logits.dtype == torch.bfloat16 and torch.isfinite(logits).all()
+    # The load-balancing loss over the fused blocks' router logits: within the spread the bf16 trunk
+    # gives the router inputs, measured on the loss's distance from its uniform-load value k.
+    k = P.c5_config().topk
+    spread_aux = abs(float(golden["aux_loss_bf16"]) - float(golden["aux_loss_fp32"]))
+    assert len(out.router_logits) == 12 and out.router_logits[0].dtype == torch.bfloat16
+    aux_ref = float(golden["aux_loss_fp32"])
+    print(f"aux loss {float(out.aux_loss):.7f} vs reference fp32 {aux_ref:.7f} (bf16 {float(golden['aux_loss_bf16']):.7f})")
+    assert abs(float(out.aux_loss) - aux_ref) <= max(2 * spread_aux, 0.1 * abs(aux_ref - k))
     assert torch.equal(logits, again), "the HIP prefill must be deterministic"
     ref32, ref16 = golden["logits_fp32"], _bf16_rows(golden["logits_bf16"])
     spread = _rel(ref16, ref32)

@@ -115,8 +115,13 @@ def test_prefill_matches_reference_fp32():
     cfg = P.c5_config()
     model = P.Q38Prefill(cfg, moe_forward=_oracle_moe).load_params(P.init_params(cfg, int(g["seed"])))
     ids = torch.from_numpy(g["ids"].astype(np.int64))
-    logits = model(ids)
+    out = model(ids, output_router_logits=True)
+    logits = out.logits
     assert logits.shape == (int(g["batch"]), int(g["seq"]), cfg.vocab) and logits.dtype == torch.float32
+    # Router logits of every layer and the load-balancing loss over them (modeling:1289-1355, 1410-1427).
+    assert len(out.router_logits) == cfg.layers
+    assert all(r.shape == (ids.numel(), cfg.experts) for r in out.router_logits)
+    assert abs(float(out.aux_loss) - float(g["aux_loss_fp32"])) < 1e-5
     lse = torch.logsumexp(logits, -1).numpy()
     assert np.abs(lse - g["lse_fp32"]).max() < 1e-5
     assert (logits.argmax(-1).numpy() == g["argmax_fp32"]).mean() > 0.999
@@ -124,6 +129,19 @@ def test_prefill_matches_reference_fp32():
     ref = g["logits_fp32"]
     assert np.linalg.norm(rows - ref) / np.linalg.norm(ref) < 1e-4
     assert np.abs(rows - ref).max() < 1e-3
+
+
+def test_load_balancing_loss_closed_forms():
+    """k = E selects every expert in every row, so the loss is E whatever the logits; with one
+    layer of identical rows the loss is E * p[top] summed over the top-k experts."""
+    torch.manual_seed(3)
+    E = 8
+    lg = (torch.randn(50, E) * 3, torch.randn(20, E))
+    assert abs(float(P.load_balancing_loss(lg, E, E)) - E) < 1e-5
+    row = torch.tensor([[2.0, 1.0, 0.5, 0.0, -1.0, -2.0, -3.0, -4.0]])
+    p = torch.softmax(row, -1)[0]
+    got = float(P.load_balancing_loss((row.repeat(7, 1),), E, 2))
+    assert abs(got - E * float(p[0] + p[1])) < 1e-5
 
 
 def test_prefill_pads_to_whole_blocks():
