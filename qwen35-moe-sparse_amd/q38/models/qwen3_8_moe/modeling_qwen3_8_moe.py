@@ -1,17 +1,34 @@
-"""Drop-in MoE modules of the Q38 model, running on the gfx950 HIP kernels.
+"""Drop-in MoE modules of the Q38 model, running on the gfx950 HIP kernels, and the causal-LM
+model class for packed prefill and HF export.
 
 Same class names, constructor signatures, submodule names, parameter names/shapes and forward
 signatures as the reference (q38/models/qwen3_8_moe/modeling_qwen3_8_moe.py:740-835), so a
 reference state dict loads unchanged and callers (the packed prefill's ``layer.mlp(...)`` at
-modeling:1271, the decoder layer at :909) use them as they are. Forward-only: every forward raises
-under autograd. Inputs and weights must be bf16 CUDA tensors; there is no CPU path.
+modeling:1271, the decoder layer at :909) use them as they are. ``Qwen3_8MoeForCausalLM`` is the
+reference's causal-LM class for uncached packed prefill (modeling:1358-1433) over the restated trunk
+of ``q38.prefill``; it is registered for the Auto classes like the reference (__init__.py:8-12), so
+``save_pretrained`` exports this file and ``from_pretrained(..., trust_remote_code=True)`` runs the
+kernels again. The imports of the library are absolute because an export runs this file outside
+the package: the ``q38`` package must be importable where an export is loaded.
+Forward-only: every forward raises under autograd. Inputs and weights must be bf16 CUDA tensors;
+there is no CPU path.
 """
 import torch
 from torch import nn
+from transformers.modeling_outputs import MoeCausalLMOutputWithPast
+from transformers.modeling_utils import PreTrainedModel
 
-from ...hip import ops
-from ...inference import (EXPERTS_IMPLEMENTATION, _check_act, _forward_only, hip_experts_forward,
-                          hip_moe_block_forward)
+from q38 import prefill as _prefill
+from q38.hip import ops
+from q38.inference import (EXPERTS_IMPLEMENTATION, _check_act, _forward_only, hip_experts_forward,
+                           hip_moe_block_forward, hip_moe_block_forward_with_router,
+                           register_experts_implementation)
+
+from .configuration_qwen3_8_moe import Qwen3_8MoeTextConfig
+
+# "q38_hip" must be a registered experts implementation before a model whose config selects it is
+# built (transformers checks the name in PreTrainedModel.__init__).
+register_experts_implementation()
 
 try:  # the reference decorates its experts class with transformers' dispatcher (modeling:756)
     from transformers.integrations.moe import use_experts_implementation
@@ -122,10 +139,107 @@ class Qwen3_8MoeSparseMoeBlock(nn.Module):
 
 
 def new_config(**kwargs):
-    from .configuration_qwen3_8_moe import Qwen3_8MoeTextConfig
-
     kwargs.setdefault("experts_implementation", EXPERTS_IMPLEMENTATION)
     return Qwen3_8MoeTextConfig(**kwargs)
 
 
-__all__ = ["Qwen3_8MoeMLP", "Qwen3_8MoeExperts", "Qwen3_8MoeTopKRouter", "Qwen3_8MoeSparseMoeBlock"]
+def prefill_config(config):
+    """The ``q38.prefill.PrefillConfig`` of a Qwen3_8MoeTextConfig (reference field names)."""
+    if config.linear_key_head_dim != config.linear_value_head_dim:
+        raise ValueError("the prefill needs equal DeltaNet key and value head widths")
+    rope = config.rope_parameters or {}
+    eos = config.eos_token_id[0] if isinstance(config.eos_token_id, (list, tuple)) else config.eos_token_id
+    return _prefill.PrefillConfig(
+        vocab=config.vocab_size, hidden=config.hidden_size, layers=config.num_hidden_layers,
+        heads=config.num_attention_heads, kv_heads=config.num_key_value_heads, head_dim=config.head_dim,
+        lin_k_heads=config.linear_num_key_heads, lin_v_heads=config.linear_num_value_heads,
+        lin_head_dim=config.linear_key_head_dim, conv_kernel=config.linear_conv_kernel_dim,
+        experts=config.num_experts, topk=config.num_experts_per_tok, moe_ffn=config.moe_intermediate_size,
+        shared_ffn=config.shared_expert_intermediate_size, rope_theta=rope.get("rope_theta", 1e7),
+        partial_rotary=rope.get("partial_rotary_factor", 0.25), n_branch=config.n_branch,
+        mhc_iters=config.mhc_iters, qsa_blocks=config.qsa_blocks, indexer_heads=config.indexer_heads,
+        indexer_head_dim=config.indexer_head_dim, ngram_rows=config.ngram_rows, eos_id=eos,
+        pad_id=config.pad_token_id if config.pad_token_id is not None else eos, rms_eps=config.rms_norm_eps,
+        layer_types=tuple(config.layer_types))
+
+
+class Qwen3_8MoePreTrainedModel(PreTrainedModel):
+    """Weight initialisation of a fresh model after the reference's (modeling:935-960, 1036-1043,
+    1169-1177); loading a checkpoint replaces all of it."""
+
+    config_class = Qwen3_8MoeTextConfig
+    base_model_prefix = "model"
+    _keys_to_ignore_on_load_unexpected = [r"^mtp\."]
+
+    @torch.no_grad()
+    def _init_weights(self, module):
+        std = self.config.initializer_range
+        if isinstance(module, (nn.Linear, nn.Conv1d, nn.Embedding)):
+            module.weight.normal_(0.0, std)
+            if getattr(module, "bias", None) is not None:
+                module.bias.zero_()
+        elif isinstance(module, _prefill._Norm):
+            module.weight.fill_(module.init_value)
+        elif isinstance(module, nn.RMSNorm):  # the N-gram embedding's norm
+            module.weight.fill_(0.02)
+        elif isinstance(module, Qwen3_8MoeExperts):
+            module.gate_up_proj.normal_(0.0, std)
+            module.down_proj.normal_(0.0, std)
+        elif isinstance(module, Qwen3_8MoeTopKRouter):
+            module.weight.normal_(0.0, std)
+        elif isinstance(module, _prefill._DeltaNet):
+            module.dt_bias.fill_(1.0)
+            module.A_log.copy_(torch.empty_like(module.A_log).uniform_(0.01, 16).log_())
+        elif isinstance(module, _prefill._MHC):
+            n = module.b_pre.numel()
+            pre = torch.full((n,), 0.1)
+            pre[module.slot % n] = 0.7
+            module.b_pre.copy_(torch.log(pre / (1 - pre)))
+            module.b_post.zero_()
+            module.b_res.copy_(torch.full((n, n), -8.0) + 8.0 * torch.eye(n))
+            module.alphas.fill_(0.1)
+            module.B.weight.zero_()
+        elif isinstance(module, _prefill._NGram):
+            module.gate.bias.fill_(-1.0)
+
+
+class Qwen3_8MoeForCausalLM(Qwen3_8MoePreTrainedModel):
+    """Causal LM head over the Q38 trunk for uncached packed prefill (modeling:1358-1433): the same
+    module tree and parameter names as the reference (``model.*``, tied ``lm_head``), the MoE blocks
+    on the fused HIP block. ``forward(input_ids, output_router_logits=None, logits_to_keep=0)``
+    returns logits (and with router logits, the load-balancing loss) in a MoeCausalLMOutputWithPast."""
+
+    _tied_weights_keys = {"lm_head.weight": "model.embed_tokens.weight"}
+
+    def __init__(self, config):
+        super().__init__(config)
+        self.prefill_config = prefill_config(config)
+        self.model = _prefill._Trunk(self.prefill_config)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        self.post_init()
+
+    def get_input_embeddings(self):
+        return self.model.embed_tokens
+
+    def get_output_embeddings(self):
+        return self.lm_head
+
+    def _moe(self, block, x, with_router):
+        return hip_moe_block_forward_with_router(block, x) if with_router else block(x)
+
+    def forward(self, input_ids=None, output_router_logits=None, logits_to_keep=0, **kwargs):
+        if input_ids is None or kwargs.get("past_key_values") is not None or kwargs.get("attention_mask") is not None:
+            raise ValueError("Q38 supports uncached packed prefill from input_ids without attention_mask")
+        want = self.config.output_router_logits if output_router_logits is None else output_router_logits
+        router = [] if want else None
+        cfg = self.prefill_config
+        with torch.no_grad():
+            hs = _prefill.trunk_forward(self.model, cfg, input_ids, self._moe, router)
+            keep = slice(-logits_to_keep, None) if isinstance(logits_to_keep, int) else logits_to_keep
+            logits = self.lm_head(hs[:, keep, :])
+            aux = _prefill.load_balancing_loss(router, cfg.experts, cfg.topk) if want else None
+        return MoeCausalLMOutputWithPast(logits=logits, aux_loss=aux, router_logits=tuple(router) if want else None)
+
+
+__all__ = ["Qwen3_8MoeMLP", "Qwen3_8MoeExperts", "Qwen3_8MoeTopKRouter", "Qwen3_8MoeSparseMoeBlock",
+           "Qwen3_8MoePreTrainedModel", "Qwen3_8MoeForCausalLM"]

@@ -63,9 +63,11 @@ class PrefillConfig:
     eos_id: int = 53
     pad_id: int = 53
     rms_eps: float = 1e-6
+    layer_types: tuple = ()  # empty: [lin, lin, lin, full] repeating (presets.py:55-56)
 
     def layer_kind(self, i):
-        """[lin, lin, lin, full] repeating (presets.py:55-56)."""
+        if self.layer_types:
+            return self.layer_types[i]
         return "full_attention" if i % 4 == 3 else "linear_attention"
 
     @property
@@ -203,8 +205,9 @@ def make_ids(batch, seq, cfg, seed=1234, eos_every=1000):
 # ---- modules (parameter holders under the reference names) -------------------------------------
 
 class _Norm(nn.Module):
-    def __init__(self, dim):
+    def __init__(self, dim, init=0.0):
         super().__init__()
+        self.init_value = init  # 0 for the zero-centred norms, 1 for the gated norm
         self.weight = nn.Parameter(torch.zeros(dim))
 
 
@@ -224,7 +227,7 @@ class _DeltaNet(nn.Module):
         self.conv1d = nn.Conv1d(conv, conv, c.conv_kernel, groups=conv, bias=False)
         self.dt_bias = nn.Parameter(torch.ones(c.lin_v_heads))
         self.A_log = nn.Parameter(torch.zeros(c.lin_v_heads))
-        self.norm = _Norm(c.lin_head_dim)
+        self.norm = _Norm(c.lin_head_dim, init=1.0)
         self.out_proj = _linear(vd, c.hidden)
 
 
@@ -248,9 +251,10 @@ class _Indexer(nn.Module):
 
 
 class _MHC(nn.Module):
-    def __init__(self, c):
+    def __init__(self, c, slot=0):
         super().__init__()
         n = c.n_branch
+        self.slot = slot  # the branch this sublayer mainly reads (H_pre initialisation)
         self.A = _linear(n * c.hidden, c.mhc_rank)
         self.B = _linear(c.mhc_rank, 2 * n + n * n)
         self.b_pre = nn.Parameter(torch.zeros(n))
@@ -301,7 +305,7 @@ class _Trunk(nn.Module):
         self.embed_tokens = nn.Embedding(c.vocab, c.hidden)
         self.layers = nn.ModuleList([_Layer(c, i) for i in range(c.layers)])
         self.norm = _Norm(c.hidden)
-        self.mhc = nn.ModuleList([_MHC(c) for _ in range(2 * c.layers)])
+        self.mhc = nn.ModuleList([_MHC(c, j) for j in range(2 * c.layers)])
         self.indexers = nn.ModuleDict({str(i): _Indexer(c) for i in range(c.layers)
                                        if c.layer_kind(i) == "full_attention"})
         self.ngram = _NGram(c) if c.ngram_rows else None
@@ -625,42 +629,54 @@ class Q38Prefill(nn.Module):
 
     @torch.no_grad()
     def forward(self, ids, output_router_logits=False):
-        cfg, M = self.cfg, self.model
         router = [] if output_router_logits else None
-        B, length = ids.shape
-        if length == 0:
-            raise ValueError("Q38 prefill needs at least one token")
-        pad = (-length) % BLK  # right padding to whole blocks (modeling:1236-1239)
-        if pad:
-            ids = F.pad(ids, (0, pad), value=cfg.pad_id)
-        S = ids.shape[1]
-        dt = M.embed_tokens.weight.dtype
-        e = F.embedding(ids, M.embed_tokens.weight)
-        cos, sin = rope_tables(cfg, S, dt, ids.device)
-        X = e.float().unsqueeze(2).expand(-1, -1, cfg.n_branch, -1).contiguous()
-        for i, layer in enumerate(M.layers):
-            xin, st = _mhc_pre(M.mhc[2 * i], X, cfg)
-            x = _zc_norm(xin, layer.input_layernorm.weight, cfg.rms_eps).to(dt)
-            if layer.kind == "linear_attention":
-                y = _delta_net(layer.linear_attn, x, cfg)
-            else:
-                y = _qsa(layer.self_attn, M.indexers[str(i)], x, cos, sin, cfg)
-            X = _mhc_post(X, y, st)
-            xin, st = _mhc_pre(M.mhc[2 * i + 1], X, cfg)
-            x = _zc_norm(xin, layer.post_attention_layernorm.weight, cfg.rms_eps).to(dt)
-            if router is None:
-                y = self.moe_forward(layer.mlp, x)
-            else:
-                y, lg = self._moe_with_router(layer.mlp, x)
-                router.append(lg)
-            X = _mhc_post(X, y, st)
-            if i == 0 and M.ngram is not None:
-                X = X + _ngram_delta(M.ngram, X.mean(2).to(dt), ids, cfg).unsqueeze(2)
-        hs = _zc_norm(X.sum(2)[:, :length].to(dt), M.norm.weight, cfg.rms_eps)
-        logits = F.linear(hs, M.embed_tokens.weight)
+        hs = trunk_forward(self.model, self.cfg, ids, self._moe, router)
+        logits = F.linear(hs, self.model.embed_tokens.weight)
         if router is None:
             return logits
-        return PrefillOutput(logits, load_balancing_loss(router, cfg.experts, cfg.topk), tuple(router))
+        return PrefillOutput(logits, load_balancing_loss(router, self.cfg.experts, self.cfg.topk), tuple(router))
+
+    def _moe(self, block, x, with_router):
+        if not with_router:
+            return self.moe_forward(block, x)
+        return self._moe_with_router(block, x)
+
+
+def trunk_forward(M, cfg, ids, moe, router=None):
+    """Qwen3_8MoeTextModel.trunk + final norm (modeling:1233-1287) over the modules of _Trunk M:
+    ids [B, S] -> normed hidden states [B, S, h] in the parameter dtype. ``moe(block, x, r)`` runs
+    one MoE block, returning (y, router logits) when r is true; with a ``router`` list the logits
+    of every layer are appended to it."""
+    B, length = ids.shape
+    if length == 0:
+        raise ValueError("Q38 prefill needs at least one token")
+    pad = (-length) % BLK  # right padding to whole blocks (modeling:1236-1239)
+    if pad:
+        ids = F.pad(ids, (0, pad), value=cfg.pad_id)
+    S = ids.shape[1]
+    dt = M.embed_tokens.weight.dtype
+    e = F.embedding(ids, M.embed_tokens.weight)
+    cos, sin = rope_tables(cfg, S, dt, ids.device)
+    X = e.float().unsqueeze(2).expand(-1, -1, cfg.n_branch, -1).contiguous()
+    for i, layer in enumerate(M.layers):
+        xin, st = _mhc_pre(M.mhc[2 * i], X, cfg)
+        x = _zc_norm(xin, layer.input_layernorm.weight, cfg.rms_eps).to(dt)
+        if layer.kind == "linear_attention":
+            y = _delta_net(layer.linear_attn, x, cfg)
+        else:
+            y = _qsa(layer.self_attn, M.indexers[str(i)], x, cos, sin, cfg)
+        X = _mhc_post(X, y, st)
+        xin, st = _mhc_pre(M.mhc[2 * i + 1], X, cfg)
+        x = _zc_norm(xin, layer.post_attention_layernorm.weight, cfg.rms_eps).to(dt)
+        if router is None:
+            y = moe(layer.mlp, x, False)
+        else:
+            y, lg = moe(layer.mlp, x, True)
+            router.append(lg)
+        X = _mhc_post(X, y, st)
+        if i == 0 and M.ngram is not None:
+            X = X + _ngram_delta(M.ngram, X.mean(2).to(dt), ids, cfg).unsqueeze(2)
+    return _zc_norm(X.sum(2)[:, :length].to(dt), M.norm.weight, cfg.rms_eps)
 
 
 def build(cfg=None, seed=0, device="cuda", dtype=torch.bfloat16, moe_forward=None):
