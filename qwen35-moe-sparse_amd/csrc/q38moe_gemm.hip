@@ -193,8 +193,16 @@ __device__ __forceinline__ void dma4(const void* gsrc, uint32_t lds) {
 }
 
 // s_waitcnt vmcnt(N) + s_barrier for a compile-time N.
+// Every wait also drains this wave's LDS reads: the bf16 main loop reads the second half of
+// slice j while it multiplies the first, so those reads may still be in flight here, and the
+// copies issued after the barrier refill the slot they read. The drain is a separate builtin wait,
+// so that the compiler's own wait insertion knows no LDS read or scalar load is pending after it
+// (lgkmcnt counts both, and while a scalar load may be pending it can only wait for zero).
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt_barrier_imm() {
+  wait_lgkm0();
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
@@ -202,6 +210,7 @@ __device__ __forceinline__ void wait_vmcnt_barrier_imm() {
 // multi-level branch tree, used only off the steady state (drain after the last tile, K shorter
 // than a ring).
 __device__ __forceinline__ void wait_vmcnt_barrier(int n) {
+  wait_lgkm0();
 #define Q38_W(N) case N: asm volatile("s_waitcnt vmcnt(" #N ")\n\ts_barrier" ::: "memory"); break;
   switch (n) {
     Q38_W(1) Q38_W(2) Q38_W(3) Q38_W(4) Q38_W(5) Q38_W(6) Q38_W(7) Q38_W(8) Q38_W(9) Q38_W(10)
@@ -258,6 +267,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
   // flight): a separate instantiation, so the main one carries no such load.
   constexpr bool async_rows = ASYNC_ROWS;
 
+  // K-slice order rotated per work unit: slice j of unit L is K slice (j + rot(L)) mod nk (the
+  // sum over K is order-free up to fp32 rounding). Rows are 2 KiB (or 512 B) apart, so without it
+  // the 512 row segments of a slice sit at one offset modulo the row pitch in every unit, and the
+  // units running together on an XCD would all hit the same few L2 channels at each step.
+  auto rot_of = [&](int u) { return (2 * u) % nk; };
+  int rot = rot_of(L);
   int4 ti = tile_entry(p, L / p.ntiles_n);
   int Ln = L + G;
   int4 tin = Ln < used ? tile_entry(p, Ln / p.ntiles_n) : make_int4(0, 0, 0, 0);
@@ -289,20 +304,21 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
 
   // This wave's 64 rows of a slot: activation rows 64w.. of ring_a, weight rows 64(w-4).. of ring_w.
   const uint32_t my_ring = is_a ? lds_addr(ring_a) + 2 * 64 * wave * BK : lds_addr(ring_w) + 2 * 64 * (wave - 4) * BK;
-#define Q38_ISSUE(SLOT, SRC, KS)                                                         \
+#define Q38_ISSUE(SLOT, SRC, KS, ROT)                                                    \
   do {                                                                                   \
     const uint32_t st_ = my_ring + (uint32_t)(SLOT) * (2 * SLOT_ELEMS);                  \
-    const int ko_ = (KS) * BK;                                                           \
+    const int ko_ = ((KS) + (ROT) < nk ? (KS) + (ROT) : (KS) + (ROT) - nk) * BK;         \
     _Pragma("unroll") for (int q_ = 0; q_ < NCOPY; ++q_)                                 \
       dma16((SRC)[q_] + ko_, st_ + q_ * (2 * 16 * BK));                                  \
   } while (0)
 
   uint16_t* const sink = reinterpret_cast<uint16_t*>(q38moe_gemm_store_sink + 64 * wave + lane);
-  for (int d = 0; d < dist; ++d) Q38_ISSUE(d, src, d);
+  for (int d = 0; d < dist; ++d) Q38_ISSUE(d, src, d, rot);
   int fill = dist;  // ring slot of the next copy: (slice + dist) % ring_n
   int ra = 0, rw = 0;  // ring_a / ring_w slots of the slice being multiplied
 
   f32x16_t acc[4][2];
+  u32x4_t wy[4], ay[2];  // bf16: the current slice's second-half fragments (see Q38_COMPUTE)
   int stores_prev = 0;  // epilogue stores this wave issued at the previous tile's end
   int tpar = 0;         // fp8: scale buffer of the current tile
   for (;;) {
@@ -379,20 +395,32 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
         _Pragma("unroll") for (int mi = 0; mi < 2; ++mi)                                   \
           acc[t][mi] = mfma32x32x64_fp8(wf8[t], af8[mi], acc[t][mi]);                      \
     } else if (active) {                                                                   \
+      /* bf16, software-pipelined by half slices (16 k each): the reads of this slice's */ \
+      /* first half run under the MFMAs of the previous slice's second half (held in    */ \
+      /* wy/ay since the previous step), and the reads of the second half under the     */ \
+      /* MFMAs of the first, so the matrix pipe is not left waiting on LDS after the     */ \
+      /* barrier. The tile's last second half is multiplied after the slice loop.       */ \
       const uint16_t* as_ = ring_a + ra * SLOT_ELEMS;                                      \
       const uint16_t* bs_ = ring_w + rw * SLOT_ELEMS;                                      \
-      u32x4_t wf[2][4], af[2][2];                                                          \
-      _Pragma("unroll") for (int kk = 0; kk < 2; ++kk) {                                   \
-        const int c = 2 * kk + lh;                                                         \
-        _Pragma("unroll") for (int t = 0; t < 4; ++t)                                      \
-          wf[kk][t] = ld16(bs_ + swz(128 * wn + 32 * t + lr, c));                           \
-        _Pragma("unroll") for (int mi = 0; mi < 2; ++mi)                                   \
-          af[kk][mi] = ld16(as_ + swz(64 * wm + 32 * mi + lr, c));                          \
-      }                                                                                    \
-      _Pragma("unroll") for (int kk = 0; kk < 2; ++kk)                                     \
+      u32x4_t wx[4], ax[2];                                                                \
+      _Pragma("unroll") for (int t = 0; t < 4; ++t)                                        \
+        wx[t] = ld16(bs_ + swz(128 * wn + 32 * t + lr, lh));                               \
+      _Pragma("unroll") for (int mi = 0; mi < 2; ++mi)                                     \
+        ax[mi] = ld16(as_ + swz(64 * wm + 32 * mi + lr, lh));                              \
+      /* keeps these reads ahead of the MFMAs below (not sunk past the branch) */          \
+      asm volatile("" ::: "memory");                                                       \
+      if (kt > 0) {                                                                        \
         _Pragma("unroll") for (int t = 0; t < 4; ++t)                                      \
           _Pragma("unroll") for (int mi = 0; mi < 2; ++mi)                                 \
-            acc[t][mi] = mfma32x32x16(wf[kk][t], af[kk][mi], acc[t][mi]);                  \
+            acc[t][mi] = mfma32x32x16(wy[t], ay[mi], acc[t][mi]);                          \
+      }                                                                                    \
+      _Pragma("unroll") for (int t = 0; t < 4; ++t)                                        \
+        wy[t] = ld16(bs_ + swz(128 * wn + 32 * t + lr, 2 + lh));                           \
+      _Pragma("unroll") for (int mi = 0; mi < 2; ++mi)                                     \
+        ay[mi] = ld16(as_ + swz(64 * wm + 32 * mi + lr, 2 + lh));                          \
+      _Pragma("unroll") for (int t = 0; t < 4; ++t)                                        \
+        _Pragma("unroll") for (int mi = 0; mi < 2; ++mi)                                   \
+          acc[t][mi] = mfma32x32x16(wx[t], ax[mi], acc[t][mi]);                            \
     }                                                                                      \
     ra = ra + 1 == NA ? 0 : ra + 1;                                                        \
     rw = rw + 1 == NW ? 0 : rw + 1;                                                        \
@@ -413,13 +441,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
       if (steady) Q38_WAIT_STEADY(stores_prev != 0);
       else Q38_WAIT_BARRIER(4 * (dist - 1) + stores_prev);
       Q38_NEXT_SCALES();
-      Q38_ISSUE(fill, src, kt + dist);
+      Q38_ISSUE(fill, src, kt + dist, rot);
       Q38_COMPUTE();
     }
     // Only reached with p1 > dist, i.e. steady: the count is the role's constant.
     for (; kt < p1; ++kt) {
       Q38_WAIT_STEADY(false);
-      Q38_ISSUE(fill, src, kt + dist);
+      Q38_ISSUE(fill, src, kt + dist, rot);
       Q38_COMPUTE();
     }
     // Phase 2 (this wave's last `dist` steps): the copies run on into the next tile, or the
@@ -429,8 +457,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
       if (steady && has_next) Q38_WAIT_STEADY(kt < dist && stores_prev != 0);
       else Q38_WAIT_BARRIER(4 * (has_next ? dist - 1 : nk - 1 - kt) + Q38_STORES_AFTER(kt));
       Q38_NEXT_SCALES();
-      if (has_next) Q38_ISSUE(fill, src_n, kt + dist - nk);
+      if (has_next) Q38_ISSUE(fill, src_n, kt + dist - nk, rot_of(Ln));
       Q38_COMPUTE();
+    }
+    // The last slice's second half.
+    if (active && !FP8) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) acc[t][mi] = mfma32x32x16(wy[t], ay[mi], acc[t][mi]);
     }
 #undef Q38_WAIT_BARRIER
 #undef Q38_NEXT_SCALES
@@ -510,6 +545,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
     if (!has_next) break;
     tpar ^= 1;
     L = Ln;
+    rot = rot_of(L);
     ti = tin;
     Ln = Lnn;
     tin = tinn;
