@@ -55,11 +55,22 @@ __global__ __launch_bounds__(256) void permute_kernel(
   for (int i = tid; i < NCHUNK * 64; i += 256) (&s_ccnt[0][0])[i] = 0;
 
   // Expert totals over all blocks and the counts of the blocks before this one. Thread `tid`
-  // sums column e over rows part, part + 4, ...; 16 independent loads are in flight per step
-  // (a wave's load is one contiguous 256-byte row).
+  // sums column e over rows part, part + 4, ...; up to 64 independent loads are in flight per
+  // step (a wave's load is one contiguous 256-byte row), so the 256 rows of the benchmark's
+  // 16384 tokens take one round trip to L2.
   int tot = 0, bef = 0;
   if (e < E) {
     int bb = part;
+    for (; bb + 252 < nblk; bb += 256) {
+      int c[64];
+#pragma unroll
+      for (int u = 0; u < 64; ++u) c[u] = hist[(int64_t)(bb + 4 * u) * E + e];
+#pragma unroll
+      for (int u = 0; u < 64; ++u) {
+        tot += c[u];
+        if (bb + 4 * u < b) bef += c[u];
+      }
+    }
     for (; bb + 60 < nblk; bb += 64) {
       int c[16];
 #pragma unroll

@@ -355,6 +355,20 @@ __device__ __forceinline__ int wr_slot(int n, int c) { return n * (ROUTE_KCHUNK 
 
 constexpr int SEL_LANES = 8;  // lanes per token in the selection fast path
 
+// Value of lane (lane ^ O) for O in {1, 2, 4}, by DPP (no LDS round trip): quad permutes for 1 and
+// 2; for 4, the half-row mirror (lane i of each 8 takes 7 - i) followed by the quad reverse (i takes
+// 3 - i within its quad), whose composition is i -> i ^ 4.
+template <int O>
+__device__ __forceinline__ int xor_lanes(int v) {
+  static_assert(O == 1 || O == 2 || O == 4, "xor_lanes: O in {1, 2, 4}");
+  if constexpr (O == 1) return __builtin_amdgcn_update_dpp(0, v, 0xb1, 0xf, 0xf, false);
+  else if constexpr (O == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4e, 0xf, 0xf, false);
+  else return __builtin_amdgcn_update_dpp(0, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false), 0x1b, 0xf, 0xf, false);
+}
+template <int O>
+__device__ __forceinline__ float xor_lanes_f(float v) { return __int_as_float(xor_lanes<O>(__float_as_int(v))); }
+
+
 // Compare-exchange for a descending list: afterwards v[i] >= v[j] (unless one is NaN; rows with a
 // NaN take the replay path, so their order here does not matter).
 __device__ __forceinline__ void cas_desc(float& vi, int& ii, float& vj, int& ij) {
@@ -384,6 +398,27 @@ __device__ __forceinline__ void sort8_desc(float (&v)[8], int (&id)[8]) {
   Q38_CE(2, 4); Q38_CE(3, 5);
   Q38_CE(1, 2); Q38_CE(3, 4); Q38_CE(5, 6);
 #undef Q38_CE
+}
+
+// One merge round of group_select (partner = lane ^ O): keeps the NP largest of the two sorted
+// lists (elementwise max of one list and the other reversed is bitonic) and re-sorts them.
+template <int O, int NP>
+__device__ __forceinline__ void merge_round(float (&v)[NP], int (&id)[NP], int& nan) {
+  float ov[NP];
+  int oid[NP];
+#pragma unroll
+  for (int r = 0; r < NP; ++r) {
+    ov[r] = xor_lanes_f<O>(v[NP - 1 - r]);
+    oid[r] = xor_lanes<O>(id[NP - 1 - r]);
+  }
+  nan |= xor_lanes<O>(nan);
+#pragma unroll
+  for (int r = 0; r < NP; ++r) {
+    const bool take = ov[r] > v[r];
+    v[r] = take ? ov[r] : v[r];
+    id[r] = take ? oid[r] : id[r];
+  }
+  bitonic_merge_desc<NP>(v, id);
 }
 
 // Per-token selection by a group of SEL_LANES lanes (lane s of the group holds experts s,
@@ -427,24 +462,10 @@ __device__ __forceinline__ bool group_select(const float* row, const float* bias
       id[r] = r < 8 ? li[r & 7] : -1;
     }
   }
-#pragma unroll
-  for (int o = 1; o < SEL_LANES; o <<= 1) {
-    float ov[NP];
-    int oid[NP];
-#pragma unroll
-    for (int r = 0; r < NP; ++r) {
-      ov[r] = __shfl_xor(v[NP - 1 - r], o);
-      oid[r] = __shfl_xor(id[NP - 1 - r], o);
-    }
-    nan |= __shfl_xor(nan, o);
-#pragma unroll
-    for (int r = 0; r < NP; ++r) {
-      const bool take = ov[r] > v[r];
-      v[r] = take ? ov[r] : v[r];
-      id[r] = take ? oid[r] : id[r];
-    }
-    bitonic_merge_desc<NP>(v, id);
-  }
+  static_assert(SEL_LANES == 8, "merge rounds below are for 8 lanes per token");
+  merge_round<1>(v, id, nan);
+  merge_round<2>(v, id, nan);
+  merge_round<4>(v, id, nan);
   const float m = v[0];
   if (nan || !__builtin_isfinite(m)) return false;
   const int lim = min(k, E - 1);
@@ -457,8 +478,9 @@ __device__ __forceinline__ bool group_select(const float* row, const float* bias
 #pragma unroll
   for (int j = 0; j < PER; ++j)
     if (s + SEL_LANES * j < E) sum += expf(z[j] - m);
-#pragma unroll
-  for (int o = 1; o < SEL_LANES; o <<= 1) sum += __shfl_xor(sum, o);
+  sum += xor_lanes_f<1>(sum);
+  sum += xor_lanes_f<2>(sum);
+  sum += xor_lanes_f<4>(sum);
   const float inv = 1.0f / sum;
   float pr[KP1];
   float tot = 0.0f;
