@@ -267,13 +267,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
   // flight): a separate instantiation, so the main one carries no such load.
   constexpr bool async_rows = ASYNC_ROWS;
 
-  // K-slice order rotated per work unit: slice j of unit L is K slice (j + rot(L)) mod nk (the
-  // sum over K is order-free up to fp32 rounding). Rows are 2 KiB (or 512 B) apart, so without it
-  // the 512 row segments of a slice sit at one offset modulo the row pitch in every unit, and the
-  // units running together on an XCD would all hit the same few L2 channels at each step.
-  auto rot_of = [&](int u) { return (2 * u) % nk; };
-  int rot = rot_of(L);
+  // K-slice order rotated per expert: slice j of a unit of expert e is K slice (j + 2e) mod nk (the
+  // sum over K is order-free up to fp32 rounding); shared-expert units rotate by row tile. Rows are
+  // 2 KiB (or 512 B) apart, so without it the 512 row segments of a slice sit at one offset modulo
+  // the row pitch in every unit, and the units running together on an XCD would all hit the same
+  // few L2 channels at each step. The units of one expert (adjacent in the tile list, run together
+  // on one XCD) keep one order, so their copies of the same weight rows and, for the output-column
+  // tiles of a row tile, of the same gathered activation rows meet in that XCD's L2.
+  auto rot_of = [&](int4 t_, int u) { return (t_.x < p.E ? 2 * t_.x : 2 * (u / p.ntiles_n)) % nk; };
   int4 ti = tile_entry(p, L / p.ntiles_n);
+  int rot = rot_of(ti, L);
   int Ln = L + G;
   int4 tin = Ln < used ? tile_entry(p, Ln / p.ntiles_n) : make_int4(0, 0, 0, 0);
   int rows[NCOPY], rows_n[NCOPY];
@@ -457,7 +460,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
       if (steady && has_next) Q38_WAIT_STEADY(kt < dist && stores_prev != 0);
       else Q38_WAIT_BARRIER(4 * (has_next ? dist - 1 : nk - 1 - kt) + Q38_STORES_AFTER(kt));
       Q38_NEXT_SCALES();
-      if (has_next) Q38_ISSUE(fill, src_n, kt + dist - nk, rot_of(Ln));
+      if (has_next) Q38_ISSUE(fill, src_n, kt + dist - nk, rot_of(tin, Ln));
       Q38_COMPUTE();
     }
     // The last slice's second half.
@@ -545,8 +548,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
     if (!has_next) break;
     tpar ^= 1;
     L = Ln;
-    rot = rot_of(L);
     ti = tin;
+    rot = rot_of(ti, L);
     Ln = Lnn;
     tin = tinn;
 #pragma unroll
