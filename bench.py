@@ -30,9 +30,14 @@ def log(msg):
 
 
 def time_stream(fn, iters, stream):
+    """Seconds per launch of `fn` (stage kernels relaunched back to back on `stream`). A GPU spin
+    queued first keeps the device busy while the host enqueues every launch, so the events time the
+    kernels back to back, not the host's per-call work (output allocation, argument checks)."""
     import torch
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        torch.cuda._sleep(4_000_000)  # about 2 ms of spinning at the MI355X clock
     start.record(stream)
     for _ in range(iters):
         fn()
