@@ -537,6 +537,7 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
   __shared__ float s_sv[ROUTE_THREADS / 64][64];
   __shared__ int s_si[ROUTE_THREADS / 64][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // the same, as a scalar
   const int64_t tb = (int64_t)blockIdx.x * ROUTE_TOKENS;
   if (tid < 64) {
     s_hist[tid] = 0;
@@ -560,23 +561,30 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
       const int kc = min(ROUTE_KCHUNK, h - k0);  // multiple of 64
       __syncthreads();                            // previous chunk fully consumed
       const bool full = kc == ROUTE_KCHUNK;
-      // This wave's x rows for a full chunk: all loads in flight before the MFMAs.
-      u32x4_t a[32];
-      if (full && mma) {
-#pragma unroll
-        for (int s = 0; s < 32; ++s) a[s] = ld16(xa + k0 + s * 32);
-      }
-      // Router weights -> LDS by asynchronous copies: one wave instruction fills 64 slots
-      // (1 KiB) of a row; lane l takes the 16-byte chunk that the swizzle puts in slot l.
-      // A chunk narrower than 512 columns leaves slots past kc/8 unused; their lanes copy chunk 0.
-      const int halves = (kc + 511) / 512;        // 1 KiB row segments in this chunk
-      for (int q = wave; q < nrows_w * halves; q += ROUTE_THREADS / 64) {
-        const int n = q / halves, part = q - n * halves;
+      // Router weights -> LDS by asynchronous copies, issued before the x loads so that they are
+      // not queued behind them: one wave instruction fills 64 slots (1 KiB) of a row; lane l takes
+      // the 16-byte chunk that the swizzle puts in slot l. A chunk narrower than 512 columns leaves
+      // slots past kc/8 unused; their lanes copy chunk 0. The loop is wave-uniform (scalar
+      // control), and each block starts at a different row so that the blocks, which all copy the
+      // same weights at once, spread over the L2 channels.
+      const int halves = (kc + 511) / 512;        // 1 KiB row segments in this chunk: 1 or 2
+      const int nseg = nrows_w * halves;
+      const int seg0 = (int)((blockIdx.x * 37u) % (unsigned)nseg);
+      for (int q = wave_u; q < nseg; q += ROUTE_THREADS / 64) {
+        int qq = q + seg0;
+        qq = qq >= nseg ? qq - nseg : qq;
+        const int n = halves == 2 ? qq >> 1 : qq, part = halves == 2 ? qq & 1 : 0;
         const uint16_t* src = n < 64 ? (n < E ? wr + (int64_t)n * h : nullptr) : wsg;
         if (src != nullptr) {
           const int c = (part * 64 + lane) ^ (n & 15);
           load_lds16(src + k0 + (c < kc / 8 ? c : 0) * 8, &s_w[n * (ROUTE_KCHUNK / 8) + part * 64]);
         }
+      }
+      // This wave's x rows for a full chunk: all loads in flight before the MFMAs.
+      u32x4_t a[32];
+      if (full && mma) {
+#pragma unroll
+        for (int s = 0; s < 32; ++s) a[s] = ld16(xa + k0 + s * 32);
       }
       wait_vmcnt0();
       __syncthreads();
