@@ -92,48 +92,27 @@ __device__ __forceinline__ void swap_slots(float& qv, int& qi, int lane, int a, 
   }
 }
 
-// libstdc++ __insertion_sort (a stable insertion sort) of slots [lo, hi), hi - lo <= KMAX.
+// libstdc++ __insertion_sort (a stable insertion sort) of slots [lo, hi), hi - lo <= KMAX. Under
+// the strict weak order cmp_gt its result is the stable descending sort, so the element in slot p
+// moves to lo + (the number of slots in [lo, hi) holding a cmp-greater value, plus those before p
+// holding an equivalent one). Every lane computes that rank against the n values (read as
+// scalars) and one forward permute places the elements; lanes outside [lo, hi) keep theirs.
 __device__ void insertion_sort_slots(float& qv, int& qi, int lane, int lo, int hi) {
   const int n = hi - lo;
   if (n <= 1) return;
-  float v[KMAX];
-  int id[KMAX];
+  int rank = 0;
 #pragma unroll
   for (int j = 0; j < KMAX; ++j) {
-    const int src = min(lo + j, 63);
-    v[j] = lane_f(qv, src);
-    id[j] = lane_i(qi, src);
-  }
-#pragma unroll
-  for (int i = 1; i < KMAX; ++i) {
-    if (i < n) {
-      const float cv = v[i];
-      const int ci = id[i];
-      int j = i;
-#pragma unroll
-      for (int jj = i; jj > 0; --jj) {
-        if (j == jj && cmp_gt(cv, v[jj - 1])) {
-          v[jj] = v[jj - 1];
-          id[jj] = id[jj - 1];
-          j = jj - 1;
-        }
-      }
-#pragma unroll
-      for (int jj = 0; jj <= i; ++jj) {
-        if (jj == j) {
-          v[jj] = cv;
-          id[jj] = ci;
-        }
-      }
+    if (j < n) {  // wave-uniform
+      const float vj = lane_f(qv, lo + j);
+      const bool gt = cmp_gt(vj, qv);
+      const bool equiv = !gt && !cmp_gt(qv, vj);
+      rank += (gt || (equiv && lo + j < lane)) ? 1 : 0;
     }
   }
-#pragma unroll
-  for (int j = 0; j < KMAX; ++j) {
-    if (j < n && lane == lo + j) {
-      qv = v[j];
-      qi = id[j];
-    }
-  }
+  const int dst = (lane >= lo && lane < hi) ? lo + rank : lane;
+  qv = __int_as_float(__builtin_amdgcn_ds_permute(dst << 2, __float_as_int(qv)));
+  qi = __builtin_amdgcn_ds_permute(dst << 2, qi);
 }
 
 // libstdc++ __adjust_heap + __push_heap on LDS arrays based at `first` (single lane).
