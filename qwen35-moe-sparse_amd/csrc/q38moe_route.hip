@@ -478,18 +478,6 @@ __device__ __forceinline__ bool group_select(const float* row, const float* bias
   return true;
 }
 
-__device__ bool group_select_k(const float* row, const float* bias, int E, int k, int s, int* oi, float* ow) {
-  switch (k) {
-    case 1: return group_select<2>(row, bias, E, k, s, oi, ow);
-    case 2: return group_select<3>(row, bias, E, k, s, oi, ow);
-    case 3: return group_select<4>(row, bias, E, k, s, oi, ow);
-    case 4: return group_select<5>(row, bias, E, k, s, oi, ow);
-    case 5: return group_select<6>(row, bias, E, k, s, oi, ow);
-    case 6: return group_select<7>(row, bias, E, k, s, oi, ow);
-    case 7: return group_select<8>(row, bias, E, k, s, oi, ow);
-    default: return group_select<9>(row, bias, E, k, s, oi, ow);
-  }
-}
 
 // One block = 64 tokens, 8 waves. Phase 1: logits on 16x16x32 MFMA (waves 0-3, 16 tokens each),
 // router weights (+ the shared-expert gate row as column 64) staged in LDS per 1024-wide K chunk
@@ -499,6 +487,9 @@ __device__ bool group_select_k(const float* row, const float* bias, int E, int k
 // distinct). Phase 4: tokens with ties are replayed wave-parallel through libstdc++'s algorithm.
 constexpr int ROUTE_THREADS = 512;  // 8 waves: 0-3 multiply, all select and replay ties
 
+// KT = k (1..KMAX) as a template parameter: each instantiation carries only its own selection
+// network, which keeps the kernel's code within the instruction cache.
+template <int KT>
 __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
     const uint16_t* __restrict__ wsg, const uint16_t* __restrict__ logits_in,
@@ -628,7 +619,7 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     if (t < T) {  // uniform over the token's lanes
       int oi[KMAX];
       float ow[KMAX];
-      const bool ok = group_select_k(s_logit[tl], bias != nullptr ? s_bias : nullptr, E, k,
+      const bool ok = group_select<KT + 1>(s_logit[tl], bias != nullptr ? s_bias : nullptr, E, k,
                                      lane % SEL_LANES, oi, ow);
       if (lane % SEL_LANES == 0) {
         if (ok) {
@@ -670,8 +661,16 @@ hipError_t launch_route(const uint16_t* x, const uint16_t* wr, const uint16_t* w
                         int64_t T, int h, int E, int k, hipStream_t stream) {
   const int64_t nblk = (T + ROUTE_TOKENS - 1) / ROUTE_TOKENS;
   if (nblk == 0) return hipSuccess;
-  hipLaunchKernelGGL(route_kernel, dim3((unsigned)nblk), dim3(ROUTE_THREADS), 0, stream, x, wr, wsg,
-                     logits_in, bias, logits_out, idx_out, w_out, gate_out, hist, T, h, E, k);
+#define Q38_ROUTE(KT)                                                                                  \
+  case KT:                                                                                             \
+    hipLaunchKernelGGL(route_kernel<KT>, dim3((unsigned)nblk), dim3(ROUTE_THREADS), 0, stream, x, wr, wsg, \
+                       logits_in, bias, logits_out, idx_out, w_out, gate_out, hist, T, h, E, k);         \
+    break;
+  switch (k) {
+    Q38_ROUTE(1) Q38_ROUTE(2) Q38_ROUTE(3) Q38_ROUTE(4) Q38_ROUTE(5) Q38_ROUTE(6) Q38_ROUTE(7) Q38_ROUTE(8)
+    default: return hipErrorInvalidValue;
+  }
+#undef Q38_ROUTE
   return hipGetLastError();
 }
 

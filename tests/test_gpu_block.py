@@ -227,3 +227,22 @@ def test_block_forward_edge_shapes(gpu, shape):
     gl = orc.bf16(orc._f(x) @ orc._f(params["shared_expert_gate.weight"]).reshape(-1))
     ref = orc.bf16(orc._f(routed) + orc._f(orc.bf16(orc._f(orc.bf16(torch.sigmoid(orc._f(gl))))[:, None] * orc._f(sh))))
     assert_bf16_close(out.cpu(), ref, what=f"edge block {shape}")
+
+
+@pytest.mark.parametrize("name", ["c2", "c3"])
+def test_block_forward_deterministic(gpu, name):
+    """Two forwards of the same inputs are bit-identical: no floating-point atomics anywhere in the
+    path (histograms are integer, the k-sum runs in a fixed order), so outputs, logits, indices and
+    weights repeat exactly."""
+    ops = _ops()
+    wl, x, params, bias = _setup(name, 4096)
+    d = {n: p.to(gpu) for n, p in params.items()}
+    args = (x.to(gpu), d["gate.weight"], d["experts.gate_up_proj"], d["experts.down_proj"],
+            d["shared_expert.gate_proj.weight"], d["shared_expert.up_proj.weight"],
+            d["shared_expert.down_proj.weight"], d["shared_expert_gate.weight"], wl.topk)
+    kw = dict(logit_bias=None if bias is None else bias.to(gpu), return_router=True)
+    first = ops.block_forward(*args, **kw)
+    second = ops.block_forward(*args, **kw)
+    torch.cuda.synchronize()
+    for a, b in zip(first, second):
+        assert torch.equal(a, b)
