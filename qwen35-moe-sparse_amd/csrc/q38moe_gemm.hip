@@ -539,7 +539,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
             const int r = 64 * wm + 32 * mi + row;
             const int col = col_wave + 64 * tp + 8 * ch;
             uint16_t* dst = p.C + (int64_t)(ti.y + r) * p.N + col;
-            st16(r < ti.z && col < p.N ? dst : sink, d);
+            // Down's Y rows (201 MB at config 2, read once by the combine) are written
+            // non-temporally so that they do not displace the weights and activations from the
+            // 256 MB MALL; gate/up's H rows, which down reads right away, are cached.
+            if (MODE == MODE_DOWN) st16_stream(r < ti.z && col < p.N ? dst : sink, d);
+            else st16(r < ti.z && col < p.N ? dst : sink, d);
           }
         }
       }
