@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define Q38MOE_ABI_VERSION 3
+#define Q38MOE_ABI_VERSION 4
 
 #define Q38MOE_OK 0
 #define Q38MOE_EINVAL (-1)   /* bad shape, null pointer, misalignment, unsupported dtype */
@@ -253,6 +253,46 @@ int q38moe_block_forward_fp8(const void* x, const void* w_router, const void* wq
                              void* logits, int32_t* topk_idx, void* topk_w, int64_t T, int32_t h,
                              int32_t E, int32_t k, int32_t I, void* workspace,
                              size_t workspace_bytes, void* stream);
+
+/*
+ * Experts backward (the differentiable experts path, inference.py:358-384, whose gradients of x,
+ * top_k_weights, gate_up_proj and down_proj scripts/check_q38_kernels.py:19-27 checks). The Python
+ * layer chains these with q38moe_down (transposed weights) and q38moe_combine (unit weights) on the
+ * permutation and tile table of the forward, built without shared-expert rows.
+ *
+ * Gathered grouped GEMM: C[r] = bf16(x[perm[r] / k] . w[e]^T) for the T*k sorted rows of the tile
+ * table (e = the row's expert); w [E,N,K], x [T,K], C [T*k,N] bf16; K, N multiples of 64. Used to
+ * recompute the gate/up pre-activations [g | u] (w = gate_up_proj, N = 2I, K = h).
+ */
+int q38moe_gather_gemm(const void* x, const int32_t* perm, const void* w, const int32_t* tiles,
+                       const int32_t* tile_count, void* C, int64_t T, int32_t K, int32_t N, int32_t E,
+                       int32_t k, void* stream);
+
+/*
+ * Routing-weight gradient (routed = raw * top_k_weights, inference.py:381):
+ *   dw[p] = bf16(sum_c fp32(bf16(dout[t,c] * Y[inv[p],c])))   for pairs p = t*k + j,
+ * Y the unweighted down rows in sorted order [T*k,h]; pairs whose expert lies outside [0,E) get 0.
+ */
+int q38moe_pair_dots(const void* dout, const void* Y, const int32_t* inv, const void* topk_idx,
+                     int32_t idx_is_int64, void* dw, int64_t T, int32_t h, int32_t E, int32_t k,
+                     void* stream);
+
+/*
+ * Rows in sorted order: dst[r] = bf16(src[perm[r] / k] * w[perm[r]]), or the plain gathered row
+ * when w is NULL (the routed raw rows' gradient dout * top_k_weights, or the gathered activation
+ * rows of the weight gradients), for r < rows: the sorted rows the permutation filled (sum of the
+ * per-expert counts; T*k when no index was dropped). src [T,h], w [T*k], dst [rows,h] bf16.
+ */
+int q38moe_gather_rows(const void* src, const int32_t* perm, const void* w, void* dst, int64_t rows,
+                       int32_t h, int32_t k, void* stream);
+
+/*
+ * SwiGLU backward (act = bf16(silu(g)), h = bf16(act * u), inference.py:378):
+ *   d_u = bf16(dh * act), d_g = bf16(bf16(dh * u) * sigmoid(g) * (1 + g * (1 - sigmoid(g))))
+ * dH [rows,I], GU = [g | u] [rows,2I], dGU = [d_g | d_u] [rows,2I] bf16; I a multiple of 64.
+ */
+int q38moe_swiglu_backward(const void* dH, const void* GU, void* dGU, int64_t rows, int32_t I,
+                           void* stream);
 
 #ifdef __cplusplus
 }

@@ -341,6 +341,83 @@ int q38moe_down(const void* H, const void* w_down, const void* w_sh_down, const 
   return Q38MOE_OK;
 }
 
+int q38moe_gather_gemm(const void* x, const int32_t* perm, const void* w, const int32_t* tiles,
+                       const int32_t* tile_count, void* C, int64_t T, int32_t K, int32_t N, int32_t E,
+                       int32_t k, void* stream) {
+  g_err[0] = 0;
+  Q38_CHECK(check_routing(T, E, k));
+  Q38_CHECK(check_dim(K, "K"));
+  Q38_CHECK(check_dim(N, "N"));
+  if (T == 0) return Q38MOE_OK;
+  Q38_CHECK(check_rows(T, K, k));
+  Q38_CHECK(check_rows(T, N, k));
+  Q38_CHECK(check_ptr(x, "x"));
+  Q38_CHECK(check_ptr(w, "w"));
+  Q38_CHECK(check_ptr(C, "C"));
+  Q38_CHECK(check_ptr(tiles, "tiles"));
+  if (perm == nullptr || tile_count == nullptr) return fail(Q38MOE_EINVAL, "perm and tile_count must not be NULL");
+  (void)hipGetLastError();
+  Q38_HIP(q38::launch_gather_gemm(static_cast<const uint16_t*>(x), perm, reinterpret_cast<const int4*>(tiles),
+                                  tile_count, (int)max_tiles_impl(T, E, k, 0), static_cast<const uint16_t*>(w),
+                                  static_cast<uint16_t*>(C), N, K, E, k, static_cast<hipStream_t>(stream)),
+          "gather gemm launch");
+  return Q38MOE_OK;
+}
+
+int q38moe_pair_dots(const void* dout, const void* Y, const int32_t* inv, const void* topk_idx,
+                     int32_t idx_is_int64, void* dw, int64_t T, int32_t h, int32_t E, int32_t k,
+                     void* stream) {
+  g_err[0] = 0;
+  Q38_CHECK(check_routing(T, E, k));
+  Q38_CHECK(check_dim(h, "h"));
+  if (T == 0) return Q38MOE_OK;
+  Q38_CHECK(check_rows(T, h, k));
+  Q38_CHECK(check_ptr(dout, "dout"));
+  Q38_CHECK(check_ptr(Y, "Y"));
+  if (inv == nullptr || dw == nullptr) return fail(Q38MOE_EINVAL, "inv and dw must not be NULL");
+  (void)hipGetLastError();
+  Q38_HIP(q38::launch_pair_dots(static_cast<const uint16_t*>(dout), static_cast<const uint16_t*>(Y), inv, topk_idx,
+                                idx_is_int64 != 0, static_cast<uint16_t*>(dw), T, h, E, k,
+                                static_cast<hipStream_t>(stream)),
+          "pair dots launch");
+  return Q38MOE_OK;
+}
+
+int q38moe_gather_rows(const void* src, const int32_t* perm, const void* w, void* dst, int64_t rows,
+                       int32_t h, int32_t k, void* stream) {
+  g_err[0] = 0;
+  if (k < 1 || k > 8) return fail(Q38MOE_EINVAL, "k must be in [1, 8] (got %d)", k);
+  Q38_CHECK(check_dim(h, "h"));
+  if (rows < 0) return fail(Q38MOE_EINVAL, "rows must be >= 0");
+  if (rows == 0) return Q38MOE_OK;
+  if (rows * (int64_t)h >= (int64_t)1 << 31) return fail(Q38MOE_EINVAL, "rows * h must be < 2^31");
+  Q38_CHECK(check_ptr(src, "src"));
+  Q38_CHECK(check_ptr(dst, "dst"));
+  if (perm == nullptr) return fail(Q38MOE_EINVAL, "perm must not be NULL");
+  (void)hipGetLastError();
+  Q38_HIP(q38::launch_gather_rows(static_cast<const uint16_t*>(src), perm, static_cast<const uint16_t*>(w),
+                                  static_cast<uint16_t*>(dst), rows, h, k, static_cast<hipStream_t>(stream)),
+          "gather rows launch");
+  return Q38MOE_OK;
+}
+
+int q38moe_swiglu_backward(const void* dH, const void* GU, void* dGU, int64_t rows, int32_t I,
+                           void* stream) {
+  g_err[0] = 0;
+  Q38_CHECK(check_dim(I, "I"));
+  if (rows < 0) return fail(Q38MOE_EINVAL, "rows must be >= 0");
+  if (rows == 0) return Q38MOE_OK;
+  if (rows * (int64_t)I * 2 >= (int64_t)1 << 31) return fail(Q38MOE_EINVAL, "rows * 2I must be < 2^31");
+  Q38_CHECK(check_ptr(dH, "dH"));
+  Q38_CHECK(check_ptr(GU, "GU"));
+  Q38_CHECK(check_ptr(dGU, "dGU"));
+  (void)hipGetLastError();
+  Q38_HIP(q38::launch_swiglu_backward(static_cast<const uint16_t*>(dH), static_cast<const uint16_t*>(GU),
+                                      static_cast<uint16_t*>(dGU), rows, I, static_cast<hipStream_t>(stream)),
+          "swiglu backward launch");
+  return Q38MOE_OK;
+}
+
 int q38moe_shared_expert(const void* x, const void* w_gate, const void* w_up,
                          const void* w_down, void* Hs, void* out, int64_t T, int32_t h,
                          int32_t Is, int32_t dtype, void* stream) {

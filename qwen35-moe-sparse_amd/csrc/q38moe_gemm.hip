@@ -5,6 +5,9 @@
 //     a_r = x[r - P] for shared-expert rows. Reference rounding: inference.py:90-96.
 //   down (MODE_DOWN):      Y[r, c] = bf16(H[r].Wd[c])  (inference.py:122-127; the routing weight
 //     is applied by the combine with the reference's rounding, inference.py:128-130).
+//   gathered (MODE_GATHER): C[r, c] = bf16(a_r.W[c]) with a_r gathered as for gate/up and the weight
+//     rows plain, as for down: the experts backward's recomputation of the gate/up pre-activations
+//     (W = gate_up_proj[e], 2I output columns).
 // Rows live in one space: [0, P) routed pairs in expert-sorted order, [P, P+T) shared-expert
 // tokens; outputs are stored row-contiguous in that order (no scatter).
 //
@@ -49,7 +52,7 @@ constexpr int NCOPY = 4;       // async copies per lane per slice (16 rows each,
 // array nobody reads are dead code to the optimizer, and the slice waits count every one.
 __device__ __attribute__((aligned(16))) u32x4_t q38moe_gemm_store_sink[8 * 64];
 
-enum { MODE_GATE_UP = 0, MODE_DOWN = 1 };
+enum { MODE_GATE_UP = 0, MODE_DOWN = 1, MODE_GATHER = 2 };
 
 struct GemmParams {
   const uint16_t* A;          // activations: x [T,h] (gate/up) or H rows (down)
@@ -90,7 +93,7 @@ __device__ __forceinline__ int4 tile_entry(const GemmParams& p, int mt) {
 // True when the activation rows of tile `ti` are gathered through perm (routed gate/up rows).
 template <int MODE>
 __device__ __forceinline__ bool gathered(const GemmParams& p, int4 ti) {
-  return MODE == MODE_GATE_UP && ti.x < p.E;
+  return (MODE == MODE_GATE_UP || MODE == MODE_GATHER) && ti.x < p.E;
 }
 
 // Row index behind each of this lane's activation copies (only activation-copying waves use it):
@@ -129,7 +132,7 @@ __device__ __forceinline__ void copy_sources(const GemmParams& p, int4 ti, int n
     const int c = (lane & 3) ^ ((r >> 2) & 3);
     if (wave < 4) {
       int64_t arow = rows[q];
-      if (MODE == MODE_GATE_UP) arow = shared_grp ? (int64_t)(rows[q] - p.P) : (int64_t)(rows[q] / p.topk);
+      if (MODE != MODE_DOWN) arow = shared_grp ? (int64_t)(rows[q] - p.P) : (int64_t)(rows[q] / p.topk);
       src[q] = p.A + arow * K + c * 8;
     } else {
       const int rb = r - BM;
@@ -656,6 +659,30 @@ static hipError_t down_impl(const void* H, const int4* tiles, const int32_t* nti
     hipLaunchKernelGGL((grouped_gemm_kernel<MODE_DOWN, false, true>), grid, dim3(NTHREADS), 0, stream, p);
   else
     hipLaunchKernelGGL((grouped_gemm_kernel<MODE_DOWN, false, false>), grid, dim3(NTHREADS), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_gemm(const uint16_t* A, const int32_t* perm, const int4* tiles,
+                              const int32_t* ntiles_dev, int max_mtiles, const uint16_t* W, uint16_t* C,
+                              int N, int K, int E, int topk, hipStream_t stream) {
+  GemmParams p = {};
+  p.A = A;
+  p.perm = perm;
+  p.tiles = tiles;
+  p.ntiles_dev = ntiles_dev;
+  p.W = W;
+  p.C = C;
+  p.N = N;
+  p.K = K;
+  p.E = E;
+  p.topk = topk;
+  p.ntiles_n = (N + BW - 1) / BW;
+  if (max_mtiles == 0) return hipSuccess;
+  const dim3 grid(grid_for(max_mtiles, p.ntiles_n));
+  if (K / BK >= 2 * (NA - 1) + 1)
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATHER, true, false>), grid, dim3(NTHREADS), 0, stream, p);
+  else
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATHER, false, false>), grid, dim3(NTHREADS), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -37,6 +37,20 @@ hipError_t launch_down(const uint16_t* H, const int4* tiles, const int32_t* ntil
                        const uint16_t* ws_down, uint16_t* Y, int N, int K, int E,
                        hipStream_t stream);
 
+// Grouped GEMM with gathered activation rows and plain weight rows: C[r] = bf16(A[perm[r] / topk] .
+// W[e]^T) for the routed rows of a tile table without shared-expert rows; W [E, N, K].
+hipError_t launch_gather_gemm(const uint16_t* A, const int32_t* perm, const int4* tiles,
+                              const int32_t* ntiles_dev, int max_mtiles, const uint16_t* W, uint16_t* C,
+                              int N, int K, int E, int topk, hipStream_t stream);
+
+// Experts backward element-wise steps (q38moe_backward.hip).
+hipError_t launch_pair_dots(const uint16_t* dout, const uint16_t* Y, const int32_t* inv, const void* idx,
+                            bool idx64, uint16_t* dw, int64_t T, int h, int E, int k, hipStream_t stream);
+hipError_t launch_gather_rows(const uint16_t* src, const int32_t* perm, const uint16_t* w, uint16_t* dst,
+                              int64_t P, int h, int k, hipStream_t stream);
+hipError_t launch_swiglu_backward(const uint16_t* dH, const uint16_t* GU, uint16_t* dGU, int64_t rows, int I,
+                                  hipStream_t stream);
+
 // e4m3 forms (fp8 expert path): A rows and weights e4m3 (K elements per row), fp32 scales per
 // GEMM row (a_scale, the sorted row space) and per weight row; outputs bf16 as above.
 hipError_t launch_gate_up_fp8(const uint8_t* xq, const int32_t* perm, const int4* tiles,

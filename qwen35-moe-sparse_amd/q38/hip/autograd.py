@@ -1,0 +1,86 @@
+"""Differentiable routed experts on HIP: the training counterpart of ``ops.experts_forward``.
+
+The reference's differentiable experts path is ``padded_batched_experts_forward``
+(q38/inference.py:358-384: gather, bmm gate/up, SiLU * up, bmm down, * top_k_weights, scatter-sum);
+its gradients of x, top_k_weights, gate_up_proj and down_proj are what
+scripts/check_q38_kernels.py:19-27 compares. Here the forward is the inference pipeline (histogram,
+permutation, grouped gate/up + SwiGLU, grouped down, combine) keeping the sorted H and Y rows, and
+the backward runs, with Y' = dout[t] * w[p] (the routed raw rows' gradient) in sorted order:
+
+  dw[p]   = <dout[t], Y[p]>                       q38moe_pair_dots
+  [g | u] = x[t] . gate_up_proj[e]^T              q38moe_gather_gemm (recomputed, sorted rows)
+  dH      = Y' . down_proj[e]                     q38moe_down on down_proj^T [E, I, h]
+  dGU     = SwiGLU backward (dH, g, u)            q38moe_swiglu_backward
+  dx_p    = dGU . gate_up_proj[e]                 q38moe_down on gate_up_proj^T [E, h, 2I]
+  dx[t]   = sum_j dx_p[inv[t*k+j]]                q38moe_combine with unit weights
+  d down_proj[e]    = Y'_e^T . H_e                per-expert library GEMMs on the sorted rows
+  d gate_up_proj[e] = dGU_e^T . x_e               (expert row ranges from the counts, one sync)
+
+All tensors bf16 (the grads in the parameters' dtype), indices int32/int64 as in the forward.
+"""
+import torch
+
+from . import ops
+
+
+class HipExperts(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, topk_idx, topk_w, w_gate_up, w_down):
+        T, h = x.shape
+        k = topk_idx.shape[1]
+        E = w_gate_up.shape[0]
+        hist = ops.histogram(topk_idx, E)
+        counts, starts, perm, inv, tiles, tcount = ops.permute(topk_idx, hist, E)
+        H = ops.gate_up(x, w_gate_up, perm, tiles, tcount, k)
+        Y = ops.down(H, w_down, tiles, tcount, T, k)
+        out = ops.combine(Y, inv, topk_w, E, idx=topk_idx)
+        ctx.save_for_backward(x, topk_idx, topk_w, w_gate_up, w_down, counts, starts, perm, inv, tiles, tcount, H, Y)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        x, idx, w, w_gate_up, w_down, counts, starts, perm, inv, tiles, tcount, H, Y = ctx.saved_tensors
+        T, h = x.shape
+        k = idx.shape[1]
+        E, twoI, _ = w_gate_up.shape
+        dout = dout.to(torch.bfloat16).contiguous()
+        need_x, _, need_w, need_gu, need_dn = ctx.needs_input_grad
+        # Host copies of the expert row ranges (the one synchronisation, like the reference's
+        # capacity read, inference.py:372).
+        c_host = counts.cpu().tolist()
+        s_host = starts.cpu().tolist()
+        rows = int(sum(c_host))
+        dw = ops.pair_dots(dout, Y, inv, idx, E) if need_w else None
+        dx = dgu_w = ddn_w = None
+        if need_x or need_gu or need_dn:
+            d_raw = ops.gather_rows(dout, perm, k, rows, w=w)
+            dH = ops.down(d_raw, w_down.transpose(1, 2).contiguous(), tiles, tcount, T, k)
+            GU = ops.gather_gemm(x, perm, w_gate_up, tiles, tcount, k)
+            dGU = ops.swiglu_backward(dH, GU)
+            if need_x:
+                dxp = ops.down(dGU, w_gate_up.transpose(1, 2).contiguous(), tiles, tcount, T, k)
+                dx = ops.combine(dxp, inv, torch.ones_like(w), E, idx=idx)
+            if need_gu or need_dn:
+                xs = ops.gather_rows(x, perm, k, rows) if need_gu else None
+                dgu_w = torch.zeros_like(w_gate_up) if need_gu else None
+                ddn_w = torch.zeros_like(w_down) if need_dn else None
+                for e in range(E):
+                    a, b = s_host[e], s_host[e] + c_host[e]
+                    if b == a:
+                        continue
+                    # Plain row-major operands (the transposed slices are copied first).
+                    if need_gu:
+                        torch.mm(dGU[a:b].t().contiguous(), xs[a:b], out=dgu_w[e])
+                    if need_dn:
+                        torch.mm(d_raw[a:b].t().contiguous(), H[a:b], out=ddn_w[e])
+        return dx, None, dw, dgu_w, ddn_w
+
+
+def experts(x, topk_idx, topk_w, w_gate_up, w_down):
+    """Routed experts with autograd (ExpertsInterface contract): [T,h] bf16; gradients flow to x,
+    topk_w, w_gate_up and w_down."""
+    for t, n in ((x, "hidden_states"), (topk_w, "top_k_weights"), (w_gate_up, "gate_up_proj"), (w_down, "down_proj")):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{n} must be bf16 for the HIP experts, got {t.dtype}")
+    return HipExperts.apply(x.contiguous(), topk_idx.contiguous(), topk_w.contiguous(), w_gate_up.contiguous(),
+                            w_down.contiguous())

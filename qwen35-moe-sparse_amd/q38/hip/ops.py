@@ -211,6 +211,69 @@ def combine(Y, inv, topk_w, E, idx=None, shared_out=None, shared_gate_logit=None
     return out
 
 
+def gather_gemm(x, perm, w, tiles, tile_count, k):
+    """C[r] = bf16(x[perm[r] // k] . w[e]^T) over the T*k sorted rows of a tile table built without
+    shared-expert rows (the gate/up pre-activations [g | u] when w is gate_up_proj): [T*k, N] bf16."""
+    _need(x, "x", ndim=2)
+    _need(perm, "perm", dtype=torch.int32)
+    _need(w, "w", ndim=3)
+    _need(tiles, "tiles", dtype=torch.int32, ndim=2)
+    T, K = x.shape
+    E, N, KK = w.shape
+    if KK != K:
+        raise ValueError(f"w {tuple(w.shape)} does not match x {tuple(x.shape)}")
+    if perm.numel() != T * k or tiles.shape[0] != max_tiles(T, E, k, 0):
+        raise ValueError("perm/tiles were not built for this shape (without shared rows)")
+    C = torch.empty(T * k, N, dtype=torch.bfloat16, device=x.device)
+    check(lib.q38moe_gather_gemm(_ptr(x), _ptr(perm), _ptr(w), _ptr(tiles), _ptr(tile_count), _ptr(C), T, K, N, E,
+                                 k, _stream(x.device)), "q38moe_gather_gemm")
+    return C
+
+
+def pair_dots(dout, Y, inv, idx, E):
+    """Routing-weight gradient dw[t, j] = <dout[t], Y[inv[t*k+j]]> (bf16 products, fp32 sum): [T,k] bf16."""
+    _need(dout, "dout", ndim=2)
+    _need(Y, "Y", ndim=2)
+    _need(inv, "inv", dtype=torch.int32)
+    _need(idx, "topk_idx", dtype=None, ndim=2)
+    T, h = dout.shape
+    k = idx.shape[1]
+    dw = torch.empty(T, k, dtype=torch.bfloat16, device=dout.device)
+    check(lib.q38moe_pair_dots(_ptr(dout), _ptr(Y), _ptr(inv), _ptr(idx), _idx_flag(idx), _ptr(dw), T, h, E, k,
+                               _stream(dout.device)), "q38moe_pair_dots")
+    return dw
+
+
+def gather_rows(src, perm, k, rows, w=None):
+    """Sorted rows r < rows: bf16(src[perm[r] // k] * w[perm[r]]) (w [T,k] or None), in a
+    [perm.numel(), h] bf16 tensor whose rows from `rows` on (the slots of dropped pairs) are left
+    unwritten. rows = the number of sorted rows the permutation filled."""
+    _need(src, "src", ndim=2)
+    _need(perm, "perm", dtype=torch.int32)
+    if w is not None:
+        _need(w, "w")
+    h = src.shape[1]
+    if rows > perm.numel():
+        raise ValueError("rows exceeds the permutation")
+    dst = torch.empty(perm.numel(), h, dtype=torch.bfloat16, device=src.device)
+    check(lib.q38moe_gather_rows(_ptr(src), _ptr(perm), _ptr(w), _ptr(dst), rows, h, k, _stream(src.device)),
+          "q38moe_gather_rows")
+    return dst
+
+
+def swiglu_backward(dH, GU):
+    """[d_g | d_u] from dH [rows, I] and the pre-activations GU = [g | u] [rows, 2I]: [rows, 2I] bf16."""
+    _need(dH, "dH", ndim=2)
+    _need(GU, "GU", ndim=2)
+    rows, I = dH.shape
+    if GU.shape != (rows, 2 * I):
+        raise ValueError(f"GU {tuple(GU.shape)} does not match dH {tuple(dH.shape)}")
+    dGU = torch.empty(rows, 2 * I, dtype=torch.bfloat16, device=dH.device)
+    check(lib.q38moe_swiglu_backward(_ptr(dH), _ptr(GU), _ptr(dGU), rows, I, _stream(dH.device)),
+          "q38moe_swiglu_backward")
+    return dGU
+
+
 def experts_workspace_bytes(T, h, E, k, I):
     n = ctypes.c_size_t()
     check(lib.q38moe_experts_workspace_bytes(T, h, E, k, I, ctypes.byref(n)), "q38moe_experts_workspace_bytes")

@@ -4,9 +4,10 @@ Mirrors the MoE part of the reference's q38/inference.py: ``hip_experts_forward`
 ExpertsInterface signature of ``triton_experts_forward`` (inference.py:158-199) and is registered
 under ``EXPERTS_IMPLEMENTATION`` like inference.py:337-338; ``hip_moe_block_forward`` replaces a
 whole ``Qwen3_8MoeSparseMoeBlock.forward`` (modeling_qwen3_8_moe.py:824-835) with one fused call.
-Both are forward-only and raise under autograd, as the reference's Triton path does
-(inference.py:160-161). They work on the reference's own modules and on the drop-in modules of
-``q38.models.qwen3_8_moe``.
+Under autograd ``hip_experts_forward`` runs the differentiable HIP experts (``q38.hip.autograd``,
+the counterpart of the reference's padded path, inference.py:358-384); the fused block stays
+forward-only and raises under autograd, as the reference's Triton path does (inference.py:160-161).
+They work on the reference's own modules and on the drop-in modules of ``q38.models.qwen3_8_moe``.
 """
 import types
 
@@ -32,13 +33,18 @@ def hip_experts_forward(self, hidden_states, top_k_index, top_k_weights):
 
     self provides ``gate_up_proj`` [E,2I,h] and ``down_proj`` [E,h,I] (modeling:756-767).
     Same math and rounding order as inference.py:158-199; indices outside [0,E) contribute nothing.
+    When autograd needs gradients of any input or weight, the differentiable HIP experts run
+    (gradients of x, top_k_weights, gate_up_proj, down_proj, as the reference's padded path).
     """
-    _forward_only(hidden_states, self.gate_up_proj, self.down_proj, top_k_weights)
     cfg = getattr(self, "config", None)
     _check_act(getattr(cfg, "hidden_act", None))
     weights = top_k_weights
     if weights.dtype != hidden_states.dtype:
         weights = weights.to(hidden_states.dtype)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (hidden_states, weights, self.gate_up_proj,
+                                                                    self.down_proj)):
+        from .hip import autograd
+        return autograd.experts(hidden_states, top_k_index, weights, self.gate_up_proj, self.down_proj)
     return ops.experts_forward(hidden_states.contiguous(), top_k_index.contiguous(), weights.contiguous(),
                                self.gate_up_proj.contiguous(), self.down_proj.contiguous())
 

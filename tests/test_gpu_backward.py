@@ -1,0 +1,109 @@
+"""GPU parity of the differentiable HIP experts (q38.hip.autograd) against CPU autograd of the
+reference's eager experts (modeling:769-793, oracle.experts_eager).
+
+The reference's own gradient check (scripts/check_q38_kernels.py:19-27) compares its kernel path
+with the eager bf16 autograd. Here both sides are measured against fp32 autograd of the same
+bf16-valued inputs: every gradient of the HIP path must lie within relative L2 2.5e-2 of it (the
+reference's tolerance, rtol 0.025) and within twice the error of the eager bf16 autograd plus 2e-3
+(the HIP path rounds at the same points as bf16 autograd; only fp32 summation order differs).
+The forward output keeps the forward tolerance (tests/_util.py).
+"""
+import pytest
+import torch
+
+from _util import assert_bf16_close
+from oracle import moe_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+REL = 2.5e-2
+
+
+def _inputs(name, T, drop=0):
+    from q38 import workloads
+    wl = workloads.get(name)
+    x, params, _ = workloads.make(wl, tokens=T)
+    _, _, idx, w = orc.router(x, params["gate.weight"], wl.topk)
+    if drop:
+        # Dropped pairs (index E): they contribute nothing and get zero weight gradient.
+        g = torch.Generator().manual_seed(7)
+        sel = torch.randperm(idx.numel(), generator=g)[:drop]
+        idx.view(-1)[sel] = wl.experts
+    gdo = torch.Generator().manual_seed(11)
+    dout = (torch.randn(T, wl.hidden, generator=gdo) * 0.05).to(torch.bfloat16)
+    return wl, x, idx, w, params["experts.gate_up_proj"], params["experts.down_proj"], dout
+
+
+def _cpu_grads(x, idx, w, wgu, wdn, dout, dtype):
+    leaves = [t.detach().to(dtype).requires_grad_(True) for t in (x, w, wgu, wdn)]
+    out = orc.experts_eager(leaves[0], idx, *leaves[1:])
+    out.backward(dout.to(dtype))
+    return out.detach().float(), [t.grad.float() for t in leaves]
+
+
+def _rel(a, b):
+    a, b = a.detach().float().cpu(), b.detach().float().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+@pytest.mark.parametrize("name,T,drop", [("c1", 53, 0), ("c1", 700, 40), ("c2", 2048, 0), ("c2", 3001, 97)])
+def test_experts_backward(gpu, name, T, drop):
+    from q38.hip import autograd
+    wl, x, idx, w, wgu, wdn, dout = _inputs(name, T, drop)
+    ref_out, ref_g = _cpu_grads(x, idx, w, wgu, wdn, dout, torch.float32)
+    _, eager_g = _cpu_grads(x, idx, w, wgu, wdn, dout, torch.bfloat16)
+    leaves = [t.to(gpu).requires_grad_(True) for t in (x, w, wgu, wdn)]
+    out = autograd.experts(leaves[0], idx.to(gpu), *leaves[1:])
+    out.backward(dout.to(gpu))
+    torch.cuda.synchronize()
+    assert_bf16_close(out, ref_out, what=f"{name} T={T} forward")
+    for nm, leaf, r, e in zip(("x", "top_k_weights", "gate_up_proj", "down_proj"), leaves, ref_g, eager_g):
+        g = leaf.grad
+        assert g is not None and g.dtype == torch.bfloat16 and g.shape == leaf.shape, nm
+        assert torch.isfinite(g.float()).all(), f"{nm}: non-finite gradient"
+        err, eager_err = _rel(g, r), _rel(e, r)
+        assert err <= REL, f"{name} T={T} d{nm}: rel {err:.3e} vs fp32 autograd (<= {REL})"
+        assert err <= 2 * eager_err + 2e-3, f"{name} T={T} d{nm}: rel {err:.3e}, eager bf16 {eager_err:.3e}"
+    if drop:
+        dropped = idx.to(gpu) == wl.experts
+        assert bool((leaves[1].grad[dropped] == 0).all()), "dropped pairs must get a zero weight gradient"
+
+
+def test_experts_backward_partial_grads(gpu):
+    """Only some inputs need gradients (frozen experts, or frozen router weights)."""
+    from q38.hip import autograd
+    _, x, idx, w, wgu, wdn, dout = _inputs("c1", 301)
+    _, ref_g = _cpu_grads(x, idx, w, wgu, wdn, dout, torch.float32)
+    xg = x.to(gpu).requires_grad_(True)
+    wg = w.to(gpu).requires_grad_(True)
+    out = autograd.experts(xg, idx.to(gpu), wg, wgu.to(gpu), wdn.to(gpu))
+    out.backward(dout.to(gpu))
+    assert _rel(xg.grad, ref_g[0]) <= REL and _rel(wg.grad, ref_g[1]) <= REL
+    wdg = wdn.to(gpu).requires_grad_(True)
+    out = autograd.experts(x.to(gpu), idx.to(gpu), w.to(gpu), wgu.to(gpu), wdg)
+    out.backward(dout.to(gpu))
+    assert _rel(wdg.grad, ref_g[3]) <= REL
+
+
+def test_registered_experts_train(gpu):
+    """The registered ExpertsInterface implementation runs the differentiable path under autograd
+    (module parameters with requires_grad) and the plain forward under inference_mode."""
+    from q38.inference import hip_experts_forward
+    _, x, idx, w, wgu, wdn, dout = _inputs("c1", 257)
+    _, ref_g = _cpu_grads(x, idx, w, wgu, wdn, dout, torch.float32)
+
+    class Experts(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.gate_up_proj = torch.nn.Parameter(wgu.to(gpu))
+            self.down_proj = torch.nn.Parameter(wdn.to(gpu))
+
+    m = Experts()
+    xg = x.to(gpu).requires_grad_(True)
+    out = hip_experts_forward(m, xg, idx.to(gpu), w.to(gpu))
+    out.backward(dout.to(gpu))
+    assert _rel(xg.grad, ref_g[0]) <= REL
+    assert _rel(m.gate_up_proj.grad, ref_g[2]) <= REL and _rel(m.down_proj.grad, ref_g[3]) <= REL
+    with torch.inference_mode():
+        out2 = hip_experts_forward(m, x.to(gpu), idx.to(gpu), w.to(gpu))
+    assert torch.equal(out.detach(), out2)
