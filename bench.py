@@ -1,6 +1,6 @@
 """Benchmark: Q38 MoE-layer forward (one Qwen3_8MoeSparseMoeBlock) on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--no-cpu-baseline]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--no-cpu-baseline] [--backward]
 
 A step is one fused block forward (router, permutation, grouped gate/up + SwiGLU, grouped down x
 routing weight, shared expert, gated combine) over the workload's packed tokens, inputs resident in
@@ -297,6 +297,103 @@ def prefill_bench(args):
     print(json.dumps(res), flush=True)
 
 
+def backward_bench(args):
+    """Routed experts forward + backward (q38.hip.autograd.experts, the differentiable counterpart
+    of the reference's padded experts path) on the workload's tokens: gradients of x,
+    top_k_weights, gate_up_proj and down_proj. Reports tokens/s of the training step and each
+    backward kernel's average duration, relaunched alone on the stream."""
+    import torch
+    from q38 import workloads
+    from q38.hip import autograd, ops
+
+    wl = workloads.get(args.workload)
+    dev = torch.device("cuda:0")
+    x, params, bias = workloads.make(wl, device="cpu")
+    x = x.to(dev)
+    d = {n: p.to(dev).contiguous() for n, p in params.items()}
+    T, h, E, k, I = wl.tokens, wl.hidden, wl.experts, wl.topk, wl.inter
+    P = T * k
+    with torch.inference_mode():
+        _, idx, w, _, _ = ops.route(x, d["gate.weight"], k, w_shared_gate=d["shared_expert_gate.weight"],
+                                    logit_bias=bias, want_hist=True)
+    idx, w = idx.clone(), w.clone()
+    leaves = [x.clone().requires_grad_(True), w.requires_grad_(True),
+              d["experts.gate_up_proj"].clone().requires_grad_(True), d["experts.down_proj"].clone().requires_grad_(True)]
+    dout = (torch.randn(T, h, device=dev) * 0.05).to(torch.bfloat16)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        for t in leaves:
+            t.grad = None
+        out = autograd.experts(leaves[0], idx, *leaves[1:])
+        out.backward(dout)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    log(f"[bench] timed {args.steps} forward+backward steps: {ms:.4f} ms/step")
+
+    # Backward stages alone, on the saved forward state.
+    with torch.no_grad():
+        xb, wb, wgu, wdn = (t.detach() for t in leaves)
+        hist = ops.histogram(idx, E)
+        counts, starts, perm, inv, tiles, tcount = ops.permute(idx, hist, E)
+        H = ops.gate_up(xb, wgu, perm, tiles, tcount, k)
+        Y = ops.down(H, wdn, tiles, tcount, T, k)
+        d_raw = ops.gather_rows(dout, perm, starts, counts, k, w=wb)
+        wdn_t, wgu_t = wdn.transpose(1, 2).contiguous(), wgu.transpose(1, 2).contiguous()
+        dH = ops.down(d_raw, wdn_t, tiles, tcount, T, k)
+        GU = ops.gather_gemm(xb, perm, wgu, tiles, tcount, k)
+        dGU = ops.swiglu_backward(dH, GU)
+        dxp = ops.down(dGU, wgu_t, tiles, tcount, T, k)
+        ones = torch.ones_like(wb)
+        it = args.kernel_iters
+        fl = lambda n: {"work": n, "unit": "TFLOP/s", "peak": PEAK_BF16 / 1e12, "bound": "mfma"}
+        by = lambda n: {"work": n, "unit": "GB/s", "peak": PEAK_HBM / 1e9, "bound": "hbm"}
+        stages = {
+            "pair_dots": (lambda: ops.pair_dots(dout, Y, inv, idx, E), by(2 * (T * h + P * h) + 2 * P)),
+            "gather_rows": (lambda: ops.gather_rows(dout, perm, starts, counts, k, w=wb), by(2 * 2 * P * h)),
+            "dH_down_t": (lambda: ops.down(d_raw, wdn_t, tiles, tcount, T, k), fl(2 * P * h * I)),
+            "gate_up_recompute": (lambda: ops.gather_gemm(xb, perm, wgu, tiles, tcount, k), fl(2 * P * h * 2 * I)),
+            "swiglu_backward": (lambda: ops.swiglu_backward(dH, GU), by(2 * (P * I + 2 * P * 2 * I))),
+            "dx_down_t": (lambda: ops.down(dGU, wgu_t, tiles, tcount, T, k), fl(2 * P * 2 * I * h)),
+            "dx_combine": (lambda: ops.combine(dxp, inv, ones, E, idx=idx), by(2 * (P * h + T * h))),
+            "wgrad_gate_up": (lambda: ops.expert_wgrad(dGU, xb, starts, counts, k, perm=perm), fl(2 * P * 2 * I * h)),
+            "wgrad_down": (lambda: ops.expert_wgrad(d_raw, H, starts, counts, k), fl(2 * P * h * I)),
+        }
+        kernels = {}
+        for name, (fn, meta) in stages.items():
+            fn()
+            sec = time_stream(fn, it, stream)
+            scale = 1e12 if meta["unit"] == "TFLOP/s" else 1e9
+            ach = meta["work"] / sec / scale
+            kernels[name] = {"us": round(sec * 1e6, 2), "bound": meta["bound"], "achieved": round(ach, 1),
+                             "peak": meta["peak"], "unit": meta["unit"], "frac": round(ach / meta["peak"], 4),
+                             "work": meta["work"]}
+    log("[bench] backward kernels: " + ", ".join(f"{n} {v['us']}us" for n, v in kernels.items()))
+    flops = 22 * P * h * I  # forward 6 P h I (gate/up 4, down 2) + backward 16 P h I
+    res = {
+        "metric": "routed-experts forward+backward tokens/sec (1 GPU)",
+        "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, N(0,0.05) output gradient)",
+        "config": {"workload": f"{wl.name}: routed experts forward+backward, {wl.batch}x{wl.seq} packed tokens",
+                   "tokens": T, "hidden": h, "experts": E, "top_k": k, "expert_inter": I,
+                   "parallelism": "single GPU"},
+        "mfma_frac_step": round(flops / (ms * 1e-3) / PEAK_BF16, 4),
+        "kernels": kernels,
+    }
+    print(json.dumps(res), flush=True)
+
+
 def moe_block_flops(cfg, T):
     """MoE block FLOPs for T tokens: routed experts, shared expert, router (flops.py:25, 38-40)."""
     h, I, Is, E, k = cfg.hidden, cfg.moe_ffn, cfg.shared_ffn, cfg.experts, cfg.topk
@@ -311,6 +408,8 @@ def main():
     ap.add_argument("--workload", default="c2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=20)
+    ap.add_argument("--backward", action="store_true",
+                    help="time the routed experts forward + backward (training step) instead")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="end with one copy of this many MiB (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -321,6 +420,9 @@ def main():
 
     if args.workload == "c5":
         prefill_bench(args)
+        return
+    if args.backward:
+        backward_bench(args)
         return
     import torch
     from q38 import workloads

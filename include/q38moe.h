@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define Q38MOE_ABI_VERSION 4
+#define Q38MOE_ABI_VERSION 5
 
 #define Q38MOE_OK 0
 #define Q38MOE_EINVAL (-1)   /* bad shape, null pointer, misalignment, unsupported dtype */
@@ -279,12 +279,29 @@ int q38moe_pair_dots(const void* dout, const void* Y, const int32_t* inv, const 
 
 /*
  * Rows in sorted order: dst[r] = bf16(src[perm[r] / k] * w[perm[r]]), or the plain gathered row
- * when w is NULL (the routed raw rows' gradient dout * top_k_weights, or the gathered activation
- * rows of the weight gradients), for r < rows: the sorted rows the permutation filled (sum of the
- * per-expert counts; T*k when no index was dropped). src [T,h], w [T*k], dst [rows,h] bf16.
+ * when w is NULL (the routed raw rows' gradient dout * top_k_weights), for the rows
+ * r < starts[E-1] + counts[E-1] that the permutation filled (fewer than T*k when indices outside
+ * [0,E) were dropped; the count is read on the device, no host synchronisation). src [T,h],
+ * w [T*k], starts/counts [E] from q38moe_permute, dst [T*k,h] bf16 (rows past the filled ones are
+ * left unwritten).
  */
-int q38moe_gather_rows(const void* src, const int32_t* perm, const void* w, void* dst, int64_t rows,
-                       int32_t h, int32_t k, void* stream);
+int q38moe_gather_rows(const void* src, const int32_t* perm, const void* w, const int32_t* starts,
+                       const int32_t* counts, void* dst, int64_t T, int32_t h, int32_t E, int32_t k,
+                       void* stream);
+
+/*
+ * Expert weight gradients (the per-expert weight products of the padded path's bmm backward,
+ * inference.py:374-380): dW[e][m][n] = bf16(sum over expert e's sorted rows r of G[r][m] * X[s(r)][n])
+ * with the rows of e = [starts[e], starts[e] + counts[e]) and s(r) = perm[r] / k (X = the tokens
+ * [T,N], gathered) or s(r) = r when perm is NULL (X = sorted rows [T*k,N]). G [T*k,M], dW [E,M,N]
+ * bf16, every element written (experts without rows, and every expert when T = 0, get zeros);
+ * M, N multiples of 64.
+ *   gate_up_proj's gradient: G = [d_g | d_u] (M = 2I), X = x, perm given      -> [E, 2I, h]
+ *   down_proj's gradient:    G = routed rows' gradient (M = h), X = H, no perm -> [E, h, I]
+ */
+int q38moe_expert_wgrad(const void* G, const void* X, const int32_t* perm, const int32_t* starts,
+                        const int32_t* counts, void* dW, int64_t T, int32_t M, int32_t N, int32_t E,
+                        int32_t k, void* stream);
 
 /*
  * SwiGLU backward (act = bf16(silu(g)), h = bf16(act * u), inference.py:378):

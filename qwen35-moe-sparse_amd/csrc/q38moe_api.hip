@@ -383,21 +383,47 @@ int q38moe_pair_dots(const void* dout, const void* Y, const int32_t* inv, const 
   return Q38MOE_OK;
 }
 
-int q38moe_gather_rows(const void* src, const int32_t* perm, const void* w, void* dst, int64_t rows,
-                       int32_t h, int32_t k, void* stream) {
+int q38moe_gather_rows(const void* src, const int32_t* perm, const void* w, const int32_t* starts,
+                       const int32_t* counts, void* dst, int64_t T, int32_t h, int32_t E, int32_t k,
+                       void* stream) {
   g_err[0] = 0;
-  if (k < 1 || k > 8) return fail(Q38MOE_EINVAL, "k must be in [1, 8] (got %d)", k);
+  Q38_CHECK(check_routing(T, E, k));
   Q38_CHECK(check_dim(h, "h"));
-  if (rows < 0) return fail(Q38MOE_EINVAL, "rows must be >= 0");
-  if (rows == 0) return Q38MOE_OK;
-  if (rows * (int64_t)h >= (int64_t)1 << 31) return fail(Q38MOE_EINVAL, "rows * h must be < 2^31");
+  if (T == 0) return Q38MOE_OK;
+  Q38_CHECK(check_rows(T, h, k));
   Q38_CHECK(check_ptr(src, "src"));
   Q38_CHECK(check_ptr(dst, "dst"));
-  if (perm == nullptr) return fail(Q38MOE_EINVAL, "perm must not be NULL");
+  if (perm == nullptr || starts == nullptr || counts == nullptr)
+    return fail(Q38MOE_EINVAL, "perm, starts and counts must not be NULL");
   (void)hipGetLastError();
-  Q38_HIP(q38::launch_gather_rows(static_cast<const uint16_t*>(src), perm, static_cast<const uint16_t*>(w),
-                                  static_cast<uint16_t*>(dst), rows, h, k, static_cast<hipStream_t>(stream)),
+  Q38_HIP(q38::launch_gather_rows(static_cast<const uint16_t*>(src), perm, static_cast<const uint16_t*>(w), starts,
+                                  counts, static_cast<uint16_t*>(dst), T * k, h, E, k,
+                                  static_cast<hipStream_t>(stream)),
           "gather rows launch");
+  return Q38MOE_OK;
+}
+
+int q38moe_expert_wgrad(const void* G, const void* X, const int32_t* perm, const int32_t* starts,
+                        const int32_t* counts, void* dW, int64_t T, int32_t M, int32_t N, int32_t E,
+                        int32_t k, void* stream) {
+  g_err[0] = 0;
+  Q38_CHECK(check_routing(T, E, k));
+  Q38_CHECK(check_dim(M, "M"));
+  Q38_CHECK(check_dim(N, "N"));
+  Q38_CHECK(check_ptr(dW, "dW"));
+  if ((int64_t)E * M * N >= (int64_t)1 << 40) return fail(Q38MOE_EINVAL, "E * M * N is too large");
+  if (T > 0) {
+    Q38_CHECK(check_rows(T, M > N ? M : N, k));
+    Q38_CHECK(check_ptr(G, "G"));
+    Q38_CHECK(check_ptr(X, "X"));
+  }
+  if (T > 0 && (starts == nullptr || counts == nullptr))
+    return fail(Q38MOE_EINVAL, "starts and counts must not be NULL");
+  (void)hipGetLastError();
+  Q38_HIP(q38::launch_expert_wgrad(static_cast<const uint16_t*>(G), static_cast<const uint16_t*>(X), perm, starts,
+                                   counts, static_cast<uint16_t*>(dW), T * k, E, M, N, k,
+                                   static_cast<hipStream_t>(stream)),
+          "expert wgrad launch");
   return Q38MOE_OK;
 }
 

@@ -11,6 +11,10 @@
 
 namespace q38 {
 
+constexpr int WG_T = 128;              // weight-gradient output tile (rows and columns)
+constexpr int WG_K = 64;               // sorted rows per LDS slice
+constexpr int WG_PITCH = 2 * WG_K + 16;  // bytes per staged column: 64 bf16 + 16 bytes of padding
+
 __device__ __forceinline__ float wave_sum_f(float v) {
 #pragma unroll
   for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
@@ -54,16 +58,20 @@ __global__ __launch_bounds__(256) void pair_dots_kernel(const uint16_t* __restri
 
 // dst[r] = bf16(src[perm[r] / k] * w[perm[r]]) (w == nullptr: the plain gathered row), rows r in
 // expert-sorted order: the gradient of the routed raw rows (dout scaled by the routing weight,
-// inference.py:381) or the gathered activation rows of the weight gradients. One wave per row.
+// inference.py:381). Only the rows r < starts[E-1] + counts[E-1] that the permutation filled (pairs
+// routed outside [0, E) hold no row); one wave per row.
 __global__ __launch_bounds__(256) void gather_rows_kernel(const uint16_t* __restrict__ src,
                                                           const int32_t* __restrict__ perm,
                                                           const uint16_t* __restrict__ w,
+                                                          const int32_t* __restrict__ starts,
+                                                          const int32_t* __restrict__ counts,
                                                           uint16_t* __restrict__ dst, int64_t P, int h,
-                                                          int k) {
+                                                          int E, int k) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int64_t r = (int64_t)blockIdx.x * 4 + wave;
-  if (r >= P) return;
+  const int64_t filled = (int64_t)starts[E - 1] + counts[E - 1];
+  if (r >= P || r >= filled) return;
   const int64_t pair = perm[r];
   const uint16_t* sr = src + (pair / k) * h;
   uint16_t* dr = dst + r * h;
@@ -118,6 +126,134 @@ __global__ __launch_bounds__(256) void swiglu_backward_kernel(const uint16_t* __
   st16(dGU + r * 2 * I + I + c, du);
 }
 
+// Expert weight gradients dW[e][m][n] = sum over the rows r of expert e (sorted order, r in
+// [starts[e], starts[e] + counts[e])) of G[r][m] * X[src(r)][n], rounded once to bf16; src(r) =
+// perm[r] / k (X = the tokens, gathered) or r (X already in sorted order). With G = [d_g | d_u] and
+// X = x this is gate_up_proj's gradient [E, 2I, h]; with G = the routed output rows' gradient and
+// X = H it is down_proj's [E, h, I] (torch's bf16 mm: fp32 accumulation, one rounding).
+//
+// The reduction runs over rows, which are the strided dimension of both operands, so each 64-row
+// slice is transposed on its way into LDS: a thread loads an 8 x 8 block (8 rows, 16 bytes each),
+// transposes it in registers and writes 8 column-major 16-byte runs, after which the MFMA
+// fragments (8 consecutive rows of one column) are single 16-byte LDS reads. One 256-thread block
+// per 128 x 128 output tile: waves 0-1 stage G, waves 2-3 stage X, every wave multiplies a 64 x 64
+// quarter (2 x 2 blocks of mfma_f32_32x32x16_bf16, X as the A operand so that a lane's
+// accumulators are 4 consecutive output columns). LDS rows are padded to 144 bytes, which makes
+// the 16-byte fragment reads conflict-free. Two LDS stages; the next slice's global loads are in
+// flight during this slice's MFMAs. Blocks are numbered so that the tiles of one expert run on one
+// XCD (workgroups go to the 8 XCDs round robin) and share its L2.
+__device__ __forceinline__ void transpose8x8(const u32x4_t (&a)[8], u32x4_t (&b)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t lo = a[2 * q][j >> 1], hi = a[2 * q + 1][j >> 1];
+      b[j][q] = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+    }
+}
+
+template <bool GATHER>
+__global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* __restrict__ G,
+                                                           const uint16_t* __restrict__ X,
+                                                           const int32_t* __restrict__ perm,
+                                                           const int32_t* __restrict__ starts,
+                                                           const int32_t* __restrict__ counts,
+                                                           uint16_t* __restrict__ dW, int64_t P, int M,
+                                                           int N, int k, int tm, int tn) {
+  __shared__ __align__(16) uint8_t lds[2][2][WG_T * WG_PITCH];  // [stage][G, X][column][row]
+  const int nb = gridDim.x, b = blockIdx.x;
+  const int L = (nb & 7) == 0 ? (b & 7) * (nb >> 3) + (b >> 3) : b;
+  const int e = L / (tm * tn), rem = L - e * tm * tn;
+  const int m0 = (rem / tn) * WG_T, n0 = (rem % tn) * WG_T;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Rows of expert e, kept inside the P sorted rows (P = 0: no rows, counts never read).
+  const int64_t r0 = P > 0 ? starts[e] : 0;
+  const int cnt = P > 0 ? (int)max((int64_t)0, min((int64_t)counts[e], P - r0)) : 0;
+  const int nsl = (cnt + WG_K - 1) / WG_K;
+
+  // Staging role: an 8-row x 8-column block of G (waves 0-1) or X (waves 2-3).
+  const bool stage_x = wave >= 2;
+  const int st = tid & 127, cb = st & 15, rb = st >> 4;
+  const int col = (stage_x ? n0 : m0) + 8 * cb;
+  const bool col_ok = col < (stage_x ? N : M);
+  const uint16_t* const base = stage_x ? X : G;
+  const int ld = stage_x ? N : M;
+  u32x4_t v[8];
+  auto load = [&](int sl) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rr = sl * WG_K + 8 * rb + i;
+      const bool ok = col_ok && rr < cnt;
+      int64_t row = r0 + rr;
+      if (stage_x && GATHER && ok) row = perm[row] / k;
+      v[i] = ok ? ld16(base + row * ld + col) : (u32x4_t){0u, 0u, 0u, 0u};
+    }
+  };
+  auto store = [&](int buf) {
+    u32x4_t t[8];
+    transpose8x8(v, t);
+    uint8_t* dst = lds[buf][stage_x ? 1 : 0] + (8 * cb) * WG_PITCH + 16 * rb;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4_t*>(dst + j * WG_PITCH) = t[j];
+  };
+
+  const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lh = lane >> 5;
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[a][c][i] = 0.0f;
+
+  if (nsl > 0) {
+    load(0);
+    store(0);
+    __syncthreads();
+  }
+  for (int sl = 0; sl < nsl; ++sl) {
+    const int buf = sl & 1;
+    const bool more = sl + 1 < nsl;
+    if (more) load(sl + 1);
+    const uint8_t* gs = lds[buf][0] + (64 * wm + lr) * WG_PITCH + 16 * lh;
+    const uint8_t* xs = lds[buf][1] + (64 * wn + lr) * WG_PITCH + 16 * lh;
+#pragma unroll
+    for (int s = 0; s < WG_K / 16; ++s) {
+      u32x4_t gf[2], xf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        gf[i] = *reinterpret_cast<const u32x4_t*>(gs + 32 * i * WG_PITCH + 32 * s);
+        xf[i] = *reinterpret_cast<const u32x4_t*>(xs + 32 * i * WG_PITCH + 32 * s);
+      }
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) acc[ni][mi] = mfma32x32x16(xf[ni], gf[mi], acc[ni][mi]);
+    }
+    if (more) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  // acc[ni][mi][i] of lane l: column n = 64wn + 32ni + 8(i/4) + 4(l/32) + i%4, row m = 64wm + 32mi + l%32.
+  uint16_t* const out = dW + (int64_t)e * M * N;
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    const int m = m0 + 64 * wm + 32 * mi + lr;
+    if (m >= M) continue;
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int n = n0 + 64 * wn + 32 * ni + 8 * gq + 4 * lh;
+        if (n < N)
+          *reinterpret_cast<uint2*>(out + (int64_t)m * N + n) =
+              make_uint2(pack_bf16x2(acc[ni][mi][4 * gq], acc[ni][mi][4 * gq + 1]),
+                         pack_bf16x2(acc[ni][mi][4 * gq + 2], acc[ni][mi][4 * gq + 3]));
+      }
+  }
+}
+
 hipError_t launch_pair_dots(const uint16_t* dout, const uint16_t* Y, const int32_t* inv, const void* idx,
                             bool idx64, uint16_t* dw, int64_t T, int h, int E, int k, hipStream_t stream) {
   if (T == 0) return hipSuccess;
@@ -131,11 +267,27 @@ hipError_t launch_pair_dots(const uint16_t* dout, const uint16_t* Y, const int32
   return hipGetLastError();
 }
 
-hipError_t launch_gather_rows(const uint16_t* src, const int32_t* perm, const uint16_t* w, uint16_t* dst,
-                              int64_t P, int h, int k, hipStream_t stream) {
+hipError_t launch_gather_rows(const uint16_t* src, const int32_t* perm, const uint16_t* w, const int32_t* starts,
+                              const int32_t* counts, uint16_t* dst, int64_t P, int h, int E, int k,
+                              hipStream_t stream) {
   if (P == 0) return hipSuccess;
-  hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)((P + 3) / 4)), dim3(256), 0, stream, src, perm, w, dst,
-                     P, h, k);
+  hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)((P + 3) / 4)), dim3(256), 0, stream, src, perm, w, starts,
+                     counts, dst, P, h, E, k);
+  return hipGetLastError();
+}
+
+hipError_t launch_expert_wgrad(const uint16_t* G, const uint16_t* X, const int32_t* perm, const int32_t* starts,
+                               const int32_t* counts, uint16_t* dW, int64_t P, int E, int M, int N, int k,
+                               hipStream_t stream) {
+  const int tm = (M + WG_T - 1) / WG_T, tn = (N + WG_T - 1) / WG_T;
+  const int64_t nb = (int64_t)E * tm * tn;
+  if (nb == 0) return hipSuccess;
+  if (perm != nullptr)
+    hipLaunchKernelGGL(expert_wgrad_kernel<true>, dim3((unsigned)nb), dim3(256), 0, stream, G, X, perm, starts, counts,
+                       dW, P, M, N, k, tm, tn);
+  else
+    hipLaunchKernelGGL(expert_wgrad_kernel<false>, dim3((unsigned)nb), dim3(256), 0, stream, G, X, perm, starts,
+                       counts, dW, P, M, N, k, tm, tn);
   return hipGetLastError();
 }
 

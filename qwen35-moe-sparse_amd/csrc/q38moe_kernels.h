@@ -46,8 +46,14 @@ hipError_t launch_gather_gemm(const uint16_t* A, const int32_t* perm, const int4
 // Experts backward element-wise steps (q38moe_backward.hip).
 hipError_t launch_pair_dots(const uint16_t* dout, const uint16_t* Y, const int32_t* inv, const void* idx,
                             bool idx64, uint16_t* dw, int64_t T, int h, int E, int k, hipStream_t stream);
-hipError_t launch_gather_rows(const uint16_t* src, const int32_t* perm, const uint16_t* w, uint16_t* dst,
-                              int64_t P, int h, int k, hipStream_t stream);
+hipError_t launch_gather_rows(const uint16_t* src, const int32_t* perm, const uint16_t* w, const int32_t* starts,
+                              const int32_t* counts, uint16_t* dst, int64_t P, int h, int E, int k,
+                              hipStream_t stream);
+// dW[e] = G_e^T . X_e over each expert's sorted rows (X gathered through perm / k, or sorted rows
+// when perm is NULL); G [P, M], dW [E, M, N] bf16.
+hipError_t launch_expert_wgrad(const uint16_t* G, const uint16_t* X, const int32_t* perm, const int32_t* starts,
+                               const int32_t* counts, uint16_t* dW, int64_t P, int E, int M, int N, int k,
+                               hipStream_t stream);
 hipError_t launch_swiglu_backward(const uint16_t* dH, const uint16_t* GU, uint16_t* dGU, int64_t rows, int I,
                                   hipStream_t stream);
 

@@ -13,8 +13,11 @@ the backward runs, with Y' = dout[t] * w[p] (the routed raw rows' gradient) in s
   dGU     = SwiGLU backward (dH, g, u)            q38moe_swiglu_backward
   dx_p    = dGU . gate_up_proj[e]                 q38moe_down on gate_up_proj^T [E, h, 2I]
   dx[t]   = sum_j dx_p[inv[t*k+j]]                q38moe_combine with unit weights
-  d down_proj[e]    = Y'_e^T . H_e                per-expert library GEMMs on the sorted rows
-  d gate_up_proj[e] = dGU_e^T . x_e               (expert row ranges from the counts, one sync)
+  d down_proj[e]    = Y'_e^T . H_e                q38moe_expert_wgrad (sorted rows)
+  d gate_up_proj[e] = dGU_e^T . x_e               q38moe_expert_wgrad (tokens gathered via perm)
+
+Expert row ranges stay on the device (starts/counts of the permutation): the backward makes no
+host synchronisation.
 
 All tensors bf16 (the grads in the parameters' dtype), indices int32/int64 as in the forward.
 """
@@ -45,34 +48,21 @@ class HipExperts(torch.autograd.Function):
         E, twoI, _ = w_gate_up.shape
         dout = dout.to(torch.bfloat16).contiguous()
         need_x, _, need_w, need_gu, need_dn = ctx.needs_input_grad
-        # Host copies of the expert row ranges (the one synchronisation, like the reference's
-        # capacity read, inference.py:372).
-        c_host = counts.cpu().tolist()
-        s_host = starts.cpu().tolist()
-        rows = int(sum(c_host))
         dw = ops.pair_dots(dout, Y, inv, idx, E) if need_w else None
         dx = dgu_w = ddn_w = None
         if need_x or need_gu or need_dn:
-            d_raw = ops.gather_rows(dout, perm, k, rows, w=w)
-            dH = ops.down(d_raw, w_down.transpose(1, 2).contiguous(), tiles, tcount, T, k)
-            GU = ops.gather_gemm(x, perm, w_gate_up, tiles, tcount, k)
-            dGU = ops.swiglu_backward(dH, GU)
-            if need_x:
-                dxp = ops.down(dGU, w_gate_up.transpose(1, 2).contiguous(), tiles, tcount, T, k)
-                dx = ops.combine(dxp, inv, torch.ones_like(w), E, idx=idx)
-            if need_gu or need_dn:
-                xs = ops.gather_rows(x, perm, k, rows) if need_gu else None
-                dgu_w = torch.zeros_like(w_gate_up) if need_gu else None
-                ddn_w = torch.zeros_like(w_down) if need_dn else None
-                for e in range(E):
-                    a, b = s_host[e], s_host[e] + c_host[e]
-                    if b == a:
-                        continue
-                    # Plain row-major operands (the transposed slices are copied first).
-                    if need_gu:
-                        torch.mm(dGU[a:b].t().contiguous(), xs[a:b], out=dgu_w[e])
-                    if need_dn:
-                        torch.mm(d_raw[a:b].t().contiguous(), H[a:b], out=ddn_w[e])
+            d_raw = ops.gather_rows(dout, perm, starts, counts, k, w=w)
+            if need_dn:
+                ddn_w = ops.expert_wgrad(d_raw, H, starts, counts, k)
+            if need_x or need_gu:
+                dH = ops.down(d_raw, w_down.transpose(1, 2).contiguous(), tiles, tcount, T, k)
+                GU = ops.gather_gemm(x, perm, w_gate_up, tiles, tcount, k)
+                dGU = ops.swiglu_backward(dH, GU)
+                if need_gu:
+                    dgu_w = ops.expert_wgrad(dGU, x, starts, counts, k, perm=perm)
+                if need_x:
+                    dxp = ops.down(dGU, w_gate_up.transpose(1, 2).contiguous(), tiles, tcount, T, k)
+                    dx = ops.combine(dxp, inv, torch.ones_like(w), E, idx=idx)
         return dx, None, dw, dgu_w, ddn_w
 
 

@@ -244,21 +244,47 @@ def pair_dots(dout, Y, inv, idx, E):
     return dw
 
 
-def gather_rows(src, perm, k, rows, w=None):
-    """Sorted rows r < rows: bf16(src[perm[r] // k] * w[perm[r]]) (w [T,k] or None), in a
-    [perm.numel(), h] bf16 tensor whose rows from `rows` on (the slots of dropped pairs) are left
-    unwritten. rows = the number of sorted rows the permutation filled."""
+def gather_rows(src, perm, starts, counts, k, w=None):
+    """Sorted rows bf16(src[perm[r] // k] * w[perm[r]]) (w [T,k] or None) in a [T*k, h] bf16 tensor;
+    only the rows the permutation filled (starts[E-1] + counts[E-1], read on the device) are
+    written, the slots of dropped pairs are left as they were."""
     _need(src, "src", ndim=2)
     _need(perm, "perm", dtype=torch.int32)
+    _need(starts, "starts", dtype=torch.int32)
+    _need(counts, "counts", dtype=torch.int32)
     if w is not None:
         _need(w, "w")
-    h = src.shape[1]
-    if rows > perm.numel():
-        raise ValueError("rows exceeds the permutation")
-    dst = torch.empty(perm.numel(), h, dtype=torch.bfloat16, device=src.device)
-    check(lib.q38moe_gather_rows(_ptr(src), _ptr(perm), _ptr(w), _ptr(dst), rows, h, k, _stream(src.device)),
-          "q38moe_gather_rows")
+    T, h = src.shape
+    if perm.numel() != T * k:
+        raise ValueError("perm must hold T*k entries")
+    dst = torch.empty(T * k, h, dtype=torch.bfloat16, device=src.device)
+    check(lib.q38moe_gather_rows(_ptr(src), _ptr(perm), _ptr(w), _ptr(starts), _ptr(counts), _ptr(dst), T, h,
+                                 counts.numel(), k, _stream(src.device)), "q38moe_gather_rows")
     return dst
+
+
+def expert_wgrad(G, X, starts, counts, k, perm=None):
+    """Expert weight gradients dW[e] = G_e^T . X_e over each expert's sorted rows: X [T,N] tokens
+    gathered through perm (gate_up_proj's gradient, G = [d_g | d_u]) or, with perm None, X [T*k,N]
+    in sorted order (down_proj's, X = H). G [T*k, M]. Returns [E, M, N] bf16."""
+    _need(G, "G", ndim=2)
+    _need(X, "X", ndim=2)
+    _need(starts, "starts", dtype=torch.int32)
+    _need(counts, "counts", dtype=torch.int32)
+    P, M = G.shape
+    N = X.shape[1]
+    E = counts.numel()
+    if perm is not None:
+        _need(perm, "perm", dtype=torch.int32)
+        if perm.numel() != P or P != X.shape[0] * k:
+            raise ValueError("perm must hold T*k entries for X [T, N]")
+    elif X.shape[0] != P:
+        raise ValueError("without perm, X must hold the G's sorted rows")
+    T = P // k
+    dW = torch.empty(E, M, N, dtype=torch.bfloat16, device=G.device)
+    check(lib.q38moe_expert_wgrad(_ptr(G), _ptr(X), _ptr(perm), _ptr(starts), _ptr(counts), _ptr(dW), T, M, N, E, k,
+                                  _stream(G.device)), "q38moe_expert_wgrad")
+    return dW
 
 
 def swiglu_backward(dH, GU):

@@ -11,7 +11,7 @@ The forward output keeps the forward tolerance (tests/_util.py).
 import pytest
 import torch
 
-from _util import assert_bf16_close
+from _util import assert_bf16_close, assert_gemm_bf16_rounding
 from oracle import moe_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -107,3 +107,54 @@ def test_registered_experts_train(gpu):
     with torch.inference_mode():
         out2 = hip_experts_forward(m, x.to(gpu), idx.to(gpu), w.to(gpu))
     assert torch.equal(out.detach(), out2)
+
+
+@pytest.mark.parametrize("E,k,T,h,I,drop", [(64, 5, 2048, 1024, 256, 0), (8, 2, 301, 64, 64, 17),
+                                            (16, 3, 999, 192, 320, 50), (4, 1, 5, 128, 64, 0)])
+def test_expert_wgrad(gpu, E, k, T, h, I, drop):
+    """q38moe_expert_wgrad in both forms against exact per-expert products: every element within
+    one bf16 ulp of the exact value plus an fp32 accumulation allowance (one rounding of an fp32
+    accumulation); experts without rows get zeros; the permutation equals the oracle's."""
+    from q38.hip import ops
+    g = torch.Generator().manual_seed(E * 1000 + T)
+    idx = torch.randint(0, E, (T, k), generator=g, dtype=torch.int32)
+    if E > 4:
+        idx[idx == 1] = 2  # expert 1 gets no rows
+    if drop:
+        idx.view(-1)[torch.randperm(T * k, generator=g)[:drop]] = E
+    x = torch.randn(T, h, generator=g).to(torch.bfloat16)
+    G = torch.randn(T * k, 2 * I, generator=g).to(torch.bfloat16)
+    Gd = torch.randn(T * k, h, generator=g).to(torch.bfloat16)
+    Hs = torch.randn(T * k, I, generator=g).to(torch.bfloat16)
+    di = idx.to(gpu)
+    counts, starts, perm, _, _, _ = ops.permute(di, ops.histogram(di, E), E)
+    dgu = ops.expert_wgrad(G.to(gpu), x.to(gpu), starts, counts, k, perm=perm)
+    ddn = ops.expert_wgrad(Gd.to(gpu), Hs.to(gpu), starts, counts, k)
+    torch.cuda.synchronize()
+    assert dgu.shape == (E, 2 * I, h) and ddn.shape == (E, h, I)
+    c_ref, s_ref, p_ref = orc.permute_cpu(idx.numpy(), E)
+    assert torch.equal(perm.cpu()[: int(c_ref.sum())], torch.from_numpy(p_ref.astype("int32")))
+    assert torch.equal(counts.cpu(), torch.from_numpy(c_ref.astype("int32")))
+    for e in range(E):
+        s0, c = int(s_ref[e]), int(c_ref[e])
+        rows = torch.from_numpy(p_ref[s0:s0 + c].astype("int64"))
+        if c == 0:
+            assert not dgu[e].any() and not ddn[e].any(), f"expert {e} has no rows but a nonzero gradient"
+            continue
+        assert_gemm_bf16_rounding(dgu[e].cpu(), G[s0:s0 + c].float().T.contiguous(),
+                                  x[rows // k].float().T.contiguous(), what=f"d gate_up_proj[{e}]")
+        assert_gemm_bf16_rounding(ddn[e].cpu(), Gd[s0:s0 + c].float().T.contiguous(),
+                                  Hs[s0:s0 + c].float().T.contiguous(),
+                                  what=f"d down_proj[{e}]")
+
+
+def test_expert_wgrad_no_rows(gpu):
+    """T = 0: every expert's gradient is zero (the counts are not read)."""
+    from q38.hip import ops
+    E, k = 8, 2
+    z = torch.zeros(E, dtype=torch.int32, device=gpu)
+    dW = ops.expert_wgrad(torch.empty(0, 128, dtype=torch.bfloat16, device=gpu),
+                          torch.empty(0, 64, dtype=torch.bfloat16, device=gpu), z, z, k,
+                          perm=torch.empty(0, dtype=torch.int32, device=gpu))
+    torch.cuda.synchronize()
+    assert dW.shape == (E, 128, 64) and not dW.any()
