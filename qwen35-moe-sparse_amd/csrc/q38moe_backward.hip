@@ -6,6 +6,8 @@
 //
 // Rounding follows torch's bf16 autograd of the reference ops: every product of two bf16 tensors is
 // rounded to bf16, reductions accumulate in fp32 and round once.
+#include <type_traits>
+
 #include "q38moe_common.h"
 #include "q38moe_kernels.h"
 
@@ -139,9 +141,9 @@ __global__ __launch_bounds__(256) void swiglu_backward_kernel(const uint16_t* __
 // per 128 x 128 output tile: waves 0-1 stage G, waves 2-3 stage X, every wave multiplies a 64 x 64
 // quarter (2 x 2 blocks of mfma_f32_32x32x16_bf16, X as the A operand so that a lane's
 // accumulators are 4 consecutive output columns). LDS rows are padded to 144 bytes, which makes
-// the 16-byte fragment reads conflict-free. Two LDS stages; the next slice's global loads are in
-// flight during this slice's MFMAs. Blocks are numbered so that the tiles of one expert run on one
-// XCD (workgroups go to the 8 XCDs round robin) and share its L2.
+// the 16-byte fragment reads conflict-free. Two LDS stages and two register stages (below).
+// Blocks are numbered so that the tiles of one expert run on one XCD (workgroups go to the 8 XCDs
+// round robin) and share its L2.
 __device__ __forceinline__ void transpose8x8(const u32x4_t (&a)[8], u32x4_t (&b)[8]) {
 #pragma unroll
   for (int j = 0; j < 8; ++j)
@@ -172,32 +174,7 @@ __global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* __res
   const int cnt = P > 0 ? (int)max((int64_t)0, min((int64_t)counts[e], P - r0)) : 0;
   const int nsl = (cnt + WG_K - 1) / WG_K;
 
-  // Staging role: an 8-row x 8-column block of G (waves 0-1) or X (waves 2-3).
-  const bool stage_x = wave >= 2;
   const int st = tid & 127, cb = st & 15, rb = st >> 4;
-  const int col = (stage_x ? n0 : m0) + 8 * cb;
-  const bool col_ok = col < (stage_x ? N : M);
-  const uint16_t* const base = stage_x ? X : G;
-  const int ld = stage_x ? N : M;
-  u32x4_t v[8];
-  auto load = [&](int sl) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int rr = sl * WG_K + 8 * rb + i;
-      const bool ok = col_ok && rr < cnt;
-      int64_t row = r0 + rr;
-      if (stage_x && GATHER && ok) row = perm[row] / k;
-      v[i] = ok ? ld16(base + row * ld + col) : (u32x4_t){0u, 0u, 0u, 0u};
-    }
-  };
-  auto store = [&](int buf) {
-    u32x4_t t[8];
-    transpose8x8(v, t);
-    uint8_t* dst = lds[buf][stage_x ? 1 : 0] + (8 * cb) * WG_PITCH + 16 * rb;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4_t*>(dst + j * WG_PITCH) = t[j];
-  };
-
   const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lh = lane >> 5;
   f32x16_t acc[2][2];
 #pragma unroll
@@ -206,16 +183,7 @@ __global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* __res
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[a][c][i] = 0.0f;
-
-  if (nsl > 0) {
-    load(0);
-    store(0);
-    __syncthreads();
-  }
-  for (int sl = 0; sl < nsl; ++sl) {
-    const int buf = sl & 1;
-    const bool more = sl + 1 < nsl;
-    if (more) load(sl + 1);
+  auto compute = [&](int buf) {
     const uint8_t* gs = lds[buf][0] + (64 * wm + lr) * WG_PITCH + 16 * lh;
     const uint8_t* xs = lds[buf][1] + (64 * wn + lr) * WG_PITCH + 16 * lh;
 #pragma unroll
@@ -231,9 +199,74 @@ __global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* __res
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi) acc[ni][mi] = mfma32x32x16(xf[ni], gf[mi], acc[ni][mi]);
     }
-    if (more) store(buf ^ 1);
+  };
+
+  // Staging role (a compile-time constant inside `run`, so that neither role branches around the
+  // other's loads): an 8-row x 8-column block of G (waves 0-1) or X (waves 2-3) per thread.
+  //
+  // Every global load is issued unconditionally from a clamped in-bounds address (rows past the
+  // expert's count read its last row, columns past the edge column 0) and its result is always
+  // consumed: the zero mask is applied at the transpose. With a fixed number of loads per slice,
+  // the compiler's vmcnt waits count only the loads that are needed (a load under a branch makes
+  // it wait for all of them).
+  //
+  // Pipeline: while slice s is multiplied from LDS, slice s+1 (loaded during the previous slice)
+  // waits in registers for its transpose into the other LDS stage, slice s+2's loads are in flight
+  // and slice s+3's gathered row indices are being fetched: a load has two slices of MFMA work to
+  // arrive in. Register sets alternate between even and odd slices; slices past the last one are
+  // masked to zero (the last two steps write such a slice into the stage that is no longer read).
+  auto run = [&](auto role) {
+    constexpr bool XR = decltype(role)::value;
+    const int col = (XR ? n0 : m0) + 8 * cb;
+    const bool col_ok = col < (XR ? N : M);
+    const int col_ld = col_ok ? col : 0;
+    const uint16_t* const base = XR ? X : G;
+    const int ld = XR ? N : M;
+    auto rows_of = [&](int sl, int (&src)[8]) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int rr = min(sl * WG_K + 8 * rb + i, cnt - 1);
+        src[i] = (GATHER && XR) ? perm[r0 + rr] / k : (int)r0 + rr;
+      }
+    };
+    auto load = [&](const int (&src)[8], u32x4_t (&v)[8]) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = ld16(base + (int64_t)src[i] * ld + col_ld);
+    };
+    auto store = [&](int buf, int sl, const u32x4_t (&v)[8]) {
+      u32x4_t w[8], t[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        w[i] = col_ok && sl * WG_K + 8 * rb + i < cnt ? v[i] : (u32x4_t){0u, 0u, 0u, 0u};
+      transpose8x8(w, t);
+      uint8_t* dst = lds[buf][XR ? 1 : 0] + (8 * cb) * WG_PITCH + 16 * rb;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4_t*>(dst + j * WG_PITCH) = t[j];
+    };
+    u32x4_t va[8], vb[8];
+    int pa[8], pb[8];
+    auto step = [&](int s, u32x4_t (&r1)[8], u32x4_t (&r2)[8], int (&p1)[8], int (&p2)[8]) {
+      rows_of(s + 3, p2);
+      load(p1, r2);
+      compute(s & 1);
+      store((s + 1) & 1, s + 1, r1);
+      __syncthreads();
+    };
+    if (nsl == 0) return;
+    rows_of(0, pa);
+    rows_of(1, pb);
+    load(pa, va);
+    load(pb, vb);
+    rows_of(2, pa);
+    store(0, 0, va);
     __syncthreads();
-  }
+    for (int s = 0; s < nsl; s += 2) {
+      step(s, vb, va, pa, pb);
+      if (s + 1 < nsl) step(s + 1, va, vb, pb, pa);
+    }
+  };
+  if (wave >= 2) run(std::true_type{});
+  else run(std::false_type{});
 
   // acc[ni][mi][i] of lane l: column n = 64wn + 32ni + 8(i/4) + 4(l/32) + i%4, row m = 64wm + 32mi + l%32.
   uint16_t* const out = dW + (int64_t)e * M * N;
