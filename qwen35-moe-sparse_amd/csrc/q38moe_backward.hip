@@ -15,7 +15,18 @@ namespace q38 {
 
 constexpr int WG_T = 128;              // weight-gradient output tile (rows and columns)
 constexpr int WG_K = 64;               // sorted rows per LDS slice
-constexpr int WG_PITCH = 2 * WG_K + 16;  // bytes per staged column: 64 bf16 + 16 bytes of padding
+constexpr int WG_PITCH = 2 * WG_K;     // bytes per staged column: 64 bf16 in 8 16-byte chunks
+
+// LDS byte offset of 16-byte row chunk q (0..7) of staged column c. Columns 2p and 2p+1 share a
+// 256-byte line of 16 chunk slots; slot (8 (c & 1) + q) ^ key(p), key(p) = ((p >> 2) ^ (p & 7)) & 15.
+// The LDS serves a 16-byte access 16 lanes per pass over its 64 banks (16 slots of 16 bytes), and
+// both access patterns fill all 16 slots per pass: the transpose writes (16 lanes = 16 column
+// blocks 8cb + j, one chunk: key runs over 16 values with cb) and the fragment reads (16 lanes = 16
+// consecutive columns, one chunk: c & 1 and the low 3 key bits run over 2 x 8 values).
+__device__ __forceinline__ int wg_slot(int c, int q) {
+  const int p = c >> 1;
+  return p * 256 + 16 * (((c & 1) * 8 + q) ^ (((p >> 2) ^ (p & 7)) & 15));
+}
 
 __device__ __forceinline__ float wave_sum_f(float v) {
 #pragma unroll
@@ -137,11 +148,12 @@ __global__ __launch_bounds__(256) void swiglu_backward_kernel(const uint16_t* __
 // The reduction runs over rows, which are the strided dimension of both operands, so each 64-row
 // slice is transposed on its way into LDS: a thread loads an 8 x 8 block (8 rows, 16 bytes each),
 // transposes it in registers and writes 8 column-major 16-byte runs, after which the MFMA
-// fragments (8 consecutive rows of one column) are single 16-byte LDS reads. One 256-thread block
+// fragments (8 consecutive rows of one column) are single 16-byte LDS reads, without bank
+// conflicts on either side (wg_slot). One 256-thread block
 // per 128 x 128 output tile: waves 0-1 stage G, waves 2-3 stage X, every wave multiplies a 64 x 64
 // quarter (2 x 2 blocks of mfma_f32_32x32x16_bf16, X as the A operand so that a lane's
-// accumulators are 4 consecutive output columns). LDS rows are padded to 144 bytes, which makes
-// the 16-byte fragment reads conflict-free. Two LDS stages and two register stages (below).
+// accumulators are 4 consecutive output columns).
+// Two LDS stages and two register stages (below).
 // Blocks are numbered so that the tiles of one expert run on one XCD (workgroups go to the 8 XCDs
 // round robin) and share its L2.
 __device__ __forceinline__ void transpose8x8(const u32x4_t (&a)[8], u32x4_t (&b)[8]) {
@@ -155,9 +167,10 @@ __device__ __forceinline__ void transpose8x8(const u32x4_t (&a)[8], u32x4_t (&b)
 }
 
 template <bool GATHER>
-__global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* __restrict__ G,
-                                                           const uint16_t* __restrict__ X,
-                                                           const int32_t* __restrict__ perm,
+// G, X and perm are not declared __restrict__: loads from restrict read-only arguments count as
+// unclobbered and may be moved across the workgroup barriers, which undoes the slice pipeline.
+__global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* G, const uint16_t* X,
+                                                           const int32_t* perm,
                                                            const int32_t* __restrict__ starts,
                                                            const int32_t* __restrict__ counts,
                                                            uint16_t* __restrict__ dW, int64_t P, int M,
@@ -184,15 +197,14 @@ __global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* __res
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[a][c][i] = 0.0f;
   auto compute = [&](int buf) {
-    const uint8_t* gs = lds[buf][0] + (64 * wm + lr) * WG_PITCH + 16 * lh;
-    const uint8_t* xs = lds[buf][1] + (64 * wn + lr) * WG_PITCH + 16 * lh;
+    // Fragment of column 64w + 32i + lr, k-chunk 2s + lh.
 #pragma unroll
     for (int s = 0; s < WG_K / 16; ++s) {
       u32x4_t gf[2], xf[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        gf[i] = *reinterpret_cast<const u32x4_t*>(gs + 32 * i * WG_PITCH + 32 * s);
-        xf[i] = *reinterpret_cast<const u32x4_t*>(xs + 32 * i * WG_PITCH + 32 * s);
+        gf[i] = *reinterpret_cast<const u32x4_t*>(lds[buf][0] + wg_slot(64 * wm + 32 * i + lr, 2 * s + lh));
+        xf[i] = *reinterpret_cast<const u32x4_t*>(lds[buf][1] + wg_slot(64 * wn + 32 * i + lr, 2 * s + lh));
       }
 #pragma unroll
       for (int ni = 0; ni < 2; ++ni)
@@ -215,6 +227,10 @@ __global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* __res
   // and slice s+3's gathered row indices are being fetched: a load has two slices of MFMA work to
   // arrive in. Register sets alternate between even and odd slices; slices past the last one are
   // masked to zero (the last two steps write such a slice into the stage that is no longer read).
+  // perm[r] / k as a multiply-high by ceil(2^32 / k): exact for every pair index below 2^29
+  // (the error term p * (ceil(2^32/k) * k - 2^32) / (k 2^32) stays below 1/k), and pair indices
+  // are below 2^25 here (P * 64 < 2^31).
+  const uint32_t kmagic = k > 1 ? (uint32_t)((0x100000000ull + (uint32_t)k - 1) / (uint32_t)k) : 0u;
   auto run = [&](auto role) {
     constexpr bool XR = decltype(role)::value;
     const int col = (XR ? n0 : m0) + 8 * cb;
@@ -226,7 +242,12 @@ __global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* __res
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int rr = min(sl * WG_K + 8 * rb + i, cnt - 1);
-        src[i] = (GATHER && XR) ? perm[r0 + rr] / k : (int)r0 + rr;
+        if (GATHER && XR) {
+          const uint32_t pr = (uint32_t)perm[r0 + rr];
+          src[i] = (int)(k > 1 ? __umulhi(pr, kmagic) : pr);
+        } else {
+          src[i] = (int)r0 + rr;
+        }
       }
     };
     auto load = [&](const int (&src)[8], u32x4_t (&v)[8]) {
@@ -239,9 +260,10 @@ __global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* __res
       for (int i = 0; i < 8; ++i)
         w[i] = col_ok && sl * WG_K + 8 * rb + i < cnt ? v[i] : (u32x4_t){0u, 0u, 0u, 0u};
       transpose8x8(w, t);
-      uint8_t* dst = lds[buf][XR ? 1 : 0] + (8 * cb) * WG_PITCH + 16 * rb;
+      // Columns 8cb + j, row chunk rb.
+      uint8_t* dst = lds[buf][XR ? 1 : 0];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4_t*>(dst + j * WG_PITCH) = t[j];
+      for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4_t*>(dst + wg_slot(8 * cb + j, rb)) = t[j];
     };
     u32x4_t va[8], vb[8];
     int pa[8], pb[8];
@@ -253,16 +275,19 @@ __global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* __res
       __syncthreads();
     };
     if (nsl == 0) return;
+    // The prologue leaves the same loads outstanding, in the same order, as the loop's back edge
+    // (slice 2's row indices, then slice 1's data), and the loop always runs whole pairs of steps
+    // (an odd count multiplies one zero slice more), so the waits at the loop head stay partial.
     rows_of(0, pa);
     rows_of(1, pb);
     load(pa, va);
-    load(pb, vb);
     rows_of(2, pa);
+    load(pb, vb);
     store(0, 0, va);
     __syncthreads();
     for (int s = 0; s < nsl; s += 2) {
       step(s, vb, va, pa, pb);
-      if (s + 1 < nsl) step(s + 1, va, vb, pb, pa);
+      step(s + 1, va, vb, pb, pa);
     }
   };
   if (wave >= 2) run(std::true_type{});
