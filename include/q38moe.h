@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define Q38MOE_ABI_VERSION 5
+#define Q38MOE_ABI_VERSION 6
 
 #define Q38MOE_OK 0
 #define Q38MOE_EINVAL (-1)   /* bad shape, null pointer, misalignment, unsupported dtype */
@@ -299,6 +299,14 @@ int q38moe_gather_rows(const void* src, const int32_t* perm, const void* w, cons
  *   gate_up_proj's gradient: G = [d_g | d_u] (M = 2I), X = x, perm given      -> [E, 2I, h]
  *   down_proj's gradient:    G = routed rows' gradient (M = h), X = H, no perm -> [E, h, I]
  */
+/*
+ * Per-expert transpose dst[e] = src[e]^T, bf16 [E,R,C] -> [E,C,R], R and C multiples of 64: the
+ * expert weights as the operand of the input-gradient products (the transposes inside the
+ * padded path's bmm backward, inference.py:374-380): down_proj [E,h,I] -> [E,I,h] for dH,
+ * gate_up_proj [E,2I,h] -> [E,h,2I] for the input rows' gradient. src and dst must not overlap.
+ */
+int q38moe_transpose_experts(const void* src, void* dst, int32_t E, int32_t R, int32_t C, void* stream);
+
 int q38moe_expert_wgrad(const void* G, const void* X, const int32_t* perm, const int32_t* starts,
                         const int32_t* counts, void* dW, int64_t T, int32_t M, int32_t N, int32_t E,
                         int32_t k, void* stream);

@@ -403,6 +403,24 @@ int q38moe_gather_rows(const void* src, const int32_t* perm, const void* w, cons
   return Q38MOE_OK;
 }
 
+int q38moe_transpose_experts(const void* src, void* dst, int32_t E, int32_t R, int32_t C, void* stream) {
+  g_err[0] = 0;
+  if (E < 0) return fail(Q38MOE_EINVAL, "E must be >= 0 (got %d)", E);
+  Q38_CHECK(check_dim(R, "R"));
+  Q38_CHECK(check_dim(C, "C"));
+  if (E == 0) return Q38MOE_OK;
+  if ((int64_t)E * R * C >= (int64_t)1 << 40) return fail(Q38MOE_EINVAL, "E * R * C is too large");
+  Q38_CHECK(check_ptr(src, "src"));
+  Q38_CHECK(check_ptr(dst, "dst"));
+  const uintptr_t s0 = (uintptr_t)src, d0 = (uintptr_t)dst, n = (uintptr_t)E * R * C * 2;
+  if (s0 < d0 + n && d0 < s0 + n) return fail(Q38MOE_EINVAL, "src and dst overlap");
+  (void)hipGetLastError();
+  Q38_HIP(q38::launch_transpose_experts(static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), E, R, C,
+                                        static_cast<hipStream_t>(stream)),
+          "transpose launch");
+  return Q38MOE_OK;
+}
+
 int q38moe_expert_wgrad(const void* G, const void* X, const int32_t* perm, const int32_t* starts,
                         const int32_t* counts, void* dW, int64_t T, int32_t M, int32_t N, int32_t E,
                         int32_t k, void* stream) {

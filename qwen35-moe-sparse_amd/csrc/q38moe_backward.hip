@@ -312,6 +312,40 @@ __global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* G, co
   }
 }
 
+// dst[e] = src[e]^T for bf16 matrices [E, R, C] -> [E, C, R] (the expert weights as the K-major
+// operand of the input-gradient products). One wave per 64 x 64 tile: lane l moves the 8 x 8 block
+// at source rows 8 (l % 8), columns 8 (l / 8) through registers (8 16-byte loads, transpose8x8,
+// 8 16-byte stores), so every load instruction covers 8 source rows x 128 contiguous bytes and
+// every store 8 destination rows x 128 bytes: whole lines both ways, no LDS.
+__global__ __launch_bounds__(256) void transpose_experts_kernel(const uint16_t* __restrict__ src,
+                                                                uint16_t* __restrict__ dst, int E, int R,
+                                                                int C) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int tr = R / 64, tc = C / 64;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
+  if (tile >= (int64_t)E * tr * tc) return;
+  const int e = (int)(tile / (tr * tc));
+  const int rem = (int)(tile - (int64_t)e * tr * tc);
+  const int r0 = (rem / tc) * 64 + 8 * (lane & 7), c0 = (rem % tc) * 64 + 8 * (lane >> 3);
+  const uint16_t* s = src + (int64_t)e * R * C + (int64_t)r0 * C + c0;
+  uint16_t* d = dst + (int64_t)e * R * C + (int64_t)c0 * R + r0;
+  u32x4_t a[8], b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = ld16(s + (int64_t)i * C);
+  transpose8x8(a, b);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) st16(d + (int64_t)j * R, b[j]);
+}
+
+hipError_t launch_transpose_experts(const uint16_t* src, uint16_t* dst, int E, int R, int C, hipStream_t stream) {
+  const int64_t tiles = (int64_t)E * (R / 64) * (C / 64);
+  if (tiles == 0) return hipSuccess;
+  hipLaunchKernelGGL(transpose_experts_kernel, dim3((unsigned)((tiles + 3) / 4)), dim3(256), 0, stream, src, dst, E,
+                     R, C);
+  return hipGetLastError();
+}
+
 hipError_t launch_pair_dots(const uint16_t* dout, const uint16_t* Y, const int32_t* inv, const void* idx,
                             bool idx64, uint16_t* dw, int64_t T, int h, int E, int k, hipStream_t stream) {
   if (T == 0) return hipSuccess;

@@ -49,6 +49,8 @@ hipError_t launch_pair_dots(const uint16_t* dout, const uint16_t* Y, const int32
 hipError_t launch_gather_rows(const uint16_t* src, const int32_t* perm, const uint16_t* w, const int32_t* starts,
                               const int32_t* counts, uint16_t* dst, int64_t P, int h, int E, int k,
                               hipStream_t stream);
+// dst[e] = src[e]^T, bf16 [E, R, C] -> [E, C, R]; R, C multiples of 64.
+hipError_t launch_transpose_experts(const uint16_t* src, uint16_t* dst, int E, int R, int C, hipStream_t stream);
 // dW[e] = G_e^T . X_e over each expert's sorted rows (X gathered through perm / k, or sorted rows
 // when perm is NULL); G [P, M], dW [E, M, N] bf16.
 hipError_t launch_expert_wgrad(const uint16_t* G, const uint16_t* X, const int32_t* perm, const int32_t* starts,

@@ -263,6 +263,15 @@ def gather_rows(src, perm, starts, counts, k, w=None):
     return dst
 
 
+def transpose_experts(w):
+    """w [E, R, C] bf16 -> contiguous [E, C, R] (each expert's matrix transposed)."""
+    _need(w, "w", ndim=3)
+    E, R, C = w.shape
+    out = torch.empty(E, C, R, dtype=w.dtype, device=w.device)
+    check(lib.q38moe_transpose_experts(_ptr(w), _ptr(out), E, R, C, _stream(w.device)), "q38moe_transpose_experts")
+    return out
+
+
 def expert_wgrad(G, X, starts, counts, k, perm=None):
     """Expert weight gradients dW[e] = G_e^T . X_e over each expert's sorted rows: X [T,N] tokens
     gathered through perm (gate_up_proj's gradient, G = [d_g | d_u]) or, with perm None, X [T*k,N]

@@ -158,3 +158,13 @@ def test_expert_wgrad_no_rows(gpu):
                           perm=torch.empty(0, dtype=torch.int32, device=gpu))
     torch.cuda.synchronize()
     assert dW.shape == (E, 128, 64) and not dW.any()
+
+
+@pytest.mark.parametrize("E,R,C", [(64, 1024, 256), (64, 512, 1024), (3, 64, 192), (1, 320, 64)])
+def test_transpose_experts(gpu, E, R, C):
+    """q38moe_transpose_experts is a bit-exact per-expert transpose."""
+    from q38.hip import ops
+    w = torch.randn(E, R, C, generator=torch.Generator().manual_seed(R + C)).to(torch.bfloat16)
+    out = ops.transpose_experts(w.to(gpu))
+    torch.cuda.synchronize()
+    assert out.shape == (E, C, R) and torch.equal(out.cpu(), w.transpose(1, 2).contiguous())
