@@ -358,8 +358,7 @@ def backward_bench(args):
         fl = lambda n: {"work": n, "unit": "TFLOP/s", "peak": PEAK_BF16 / 1e12, "bound": "mfma"}
         by = lambda n: {"work": n, "unit": "GB/s", "peak": PEAK_HBM / 1e9, "bound": "hbm"}
         stages = {
-            "pair_dots": (lambda: ops.pair_dots(dout, Y, inv, idx, E), by(2 * (T * h + P * h) + 2 * P)),
-            "gather_rows": (lambda: ops.gather_rows(dout, perm, starts, counts, k, w=wb), by(2 * 2 * P * h)),
+            "pair_dots_rows": (lambda: ops.pair_dots(dout, Y, inv, idx, E, w=wb), by(2 * (T * h + 2 * P * h) + 4 * P)),
             "transpose_down_proj": (lambda: ops.transpose_experts(wdn), by(2 * 2 * E * h * I)),
             "dH_down_t": (lambda: ops.down(d_raw, wdn_t, tiles, tcount, T, k), fl(2 * P * h * I)),
             "gate_up_recompute": (lambda: ops.gather_gemm(xb, perm, wgu, tiles, tcount, k), fl(2 * P * h * 2 * I)),

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define Q38MOE_ABI_VERSION 6
+#define Q38MOE_ABI_VERSION 7
 
 #define Q38MOE_OK 0
 #define Q38MOE_EINVAL (-1)   /* bad shape, null pointer, misalignment, unsupported dtype */
@@ -272,10 +272,13 @@ int q38moe_gather_gemm(const void* x, const int32_t* perm, const void* w, const 
  * Routing-weight gradient (routed = raw * top_k_weights, inference.py:381):
  *   dw[p] = bf16(sum_c fp32(bf16(dout[t,c] * Y[inv[p],c])))   for pairs p = t*k + j,
  * Y the unweighted down rows in sorted order [T*k,h]; pairs whose expert lies outside [0,E) get 0.
+ * With d_raw (and topk_w [T*k] bf16) given, the same pass writes the routed raw rows' gradient in
+ * sorted order, d_raw[inv[p]] = bf16(dout[t] * topk_w[p]) (as q38moe_gather_rows with w), rows of
+ * dropped pairs left unwritten; d_raw [T*k,h] bf16. topk_w and d_raw may be NULL.
  */
 int q38moe_pair_dots(const void* dout, const void* Y, const int32_t* inv, const void* topk_idx,
-                     int32_t idx_is_int64, void* dw, int64_t T, int32_t h, int32_t E, int32_t k,
-                     void* stream);
+                     int32_t idx_is_int64, const void* topk_w, void* dw, void* d_raw, int64_t T, int32_t h,
+                     int32_t E, int32_t k, void* stream);
 
 /*
  * Rows in sorted order: dst[r] = bf16(src[perm[r] / k] * w[perm[r]]), or the plain gathered row

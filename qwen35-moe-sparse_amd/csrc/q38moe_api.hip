@@ -365,8 +365,8 @@ int q38moe_gather_gemm(const void* x, const int32_t* perm, const void* w, const 
 }
 
 int q38moe_pair_dots(const void* dout, const void* Y, const int32_t* inv, const void* topk_idx,
-                     int32_t idx_is_int64, void* dw, int64_t T, int32_t h, int32_t E, int32_t k,
-                     void* stream) {
+                     int32_t idx_is_int64, const void* topk_w, void* dw, void* d_raw, int64_t T, int32_t h,
+                     int32_t E, int32_t k, void* stream) {
   g_err[0] = 0;
   Q38_CHECK(check_routing(T, E, k));
   Q38_CHECK(check_dim(h, "h"));
@@ -374,11 +374,13 @@ int q38moe_pair_dots(const void* dout, const void* Y, const int32_t* inv, const 
   Q38_CHECK(check_rows(T, h, k));
   Q38_CHECK(check_ptr(dout, "dout"));
   Q38_CHECK(check_ptr(Y, "Y"));
-  if (inv == nullptr || dw == nullptr) return fail(Q38MOE_EINVAL, "inv and dw must not be NULL");
+  if (inv == nullptr || dw == nullptr || topk_idx == nullptr)
+    return fail(Q38MOE_EINVAL, "inv, topk_idx and dw must not be NULL");
+  if (d_raw != nullptr && topk_w == nullptr) return fail(Q38MOE_EINVAL, "d_raw needs topk_w");
   (void)hipGetLastError();
   Q38_HIP(q38::launch_pair_dots(static_cast<const uint16_t*>(dout), static_cast<const uint16_t*>(Y), inv, topk_idx,
-                                idx_is_int64 != 0, static_cast<uint16_t*>(dw), T, h, E, k,
-                                static_cast<hipStream_t>(stream)),
+                                idx_is_int64 != 0, static_cast<const uint16_t*>(topk_w), static_cast<uint16_t*>(dw),
+                                static_cast<uint16_t*>(d_raw), T, h, E, k, static_cast<hipStream_t>(stream)),
           "pair dots launch");
   return Q38MOE_OK;
 }

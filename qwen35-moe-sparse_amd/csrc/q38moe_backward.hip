@@ -36,36 +36,62 @@ __device__ __forceinline__ float wave_sum_f(float v) {
 
 // dw[p] = bf16(sum_c fp32(bf16(dout[t, c] * Y[inv[p], c]))) for the pairs p = t*k + j of token t (the
 // gradient of routed = raw * top_k_weights, inference.py:381); pairs whose expert lies outside
-// [0, E) get 0. One wave per token; lane l covers columns 8l + 512i.
-template <typename IdxT>
+// [0, E) get 0. With w and d_raw given, the same pass also writes the routed raw rows' gradient in
+// sorted order, d_raw[inv[p]] = bf16(dout[t] * w[p]) (what gather_rows_kernel computes), reading
+// each dout row once for both. One wave per token; lane l covers columns 8l + 512i.
+template <typename IdxT, int KT>
 __global__ __launch_bounds__(256) void pair_dots_kernel(const uint16_t* __restrict__ dout,
                                                         const uint16_t* __restrict__ Y,
                                                         const int32_t* __restrict__ inv,
                                                         const IdxT* __restrict__ idx,
-                                                        uint16_t* __restrict__ dw, int64_t T, int h,
-                                                        int E, int k) {
+                                                        const uint16_t* __restrict__ w,
+                                                        uint16_t* __restrict__ dw,
+                                                        uint16_t* __restrict__ d_raw, int64_t T, int h,
+                                                        int E) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + wave;
   if (t >= T) return;
-  for (int j = 0; j < k; ++j) {
-    const int64_t p = t * k + j;
-    const int64_t e = idx != nullptr ? (int64_t)idx[p] : 0;
-    float acc = 0.0f;
-    if (e >= 0 && e < E) {  // wave-uniform
-      const uint16_t* yr = Y + (int64_t)inv[p] * h;
-      const uint16_t* dr = dout + t * h;
-      for (int c = lane * 8; c < h; c += 512) {
-        const u32x4_t a = ld16(dr + c), b = ld16(yr + c);
+  // The token's KT pairs: every Y row load of a column chunk is issued before any is used.
+  bool ok[KT];
+  int64_t row[KT];
+  float s[KT], acc[KT];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc += round_bf16(bf16_to_f32(a[i] & 0xffffu) * bf16_to_f32(b[i] & 0xffffu));
-          acc += round_bf16(bf16_to_f32(a[i] >> 16) * bf16_to_f32(b[i] >> 16));
-        }
+  for (int j = 0; j < KT; ++j) {
+    const int64_t p = t * KT + j;
+    const int e = __builtin_amdgcn_readfirstlane((int)idx[p]);
+    ok[j] = e >= 0 && e < E;  // wave-uniform
+    row[j] = ok[j] ? (int64_t)__builtin_amdgcn_readfirstlane(inv[p]) : 0;
+    s[j] = d_raw != nullptr ? bf16_to_f32(w[p]) : 0.0f;
+    acc[j] = 0.0f;
+  }
+  const uint16_t* dr = dout + t * h;
+  for (int c = lane * 8; c < h; c += 512) {
+    const u32x4_t a = ld16(dr + c);
+    u32x4_t b[KT];
+#pragma unroll
+    for (int j = 0; j < KT; ++j) b[j] = ok[j] ? ld16(Y + row[j] * h + c) : (u32x4_t){0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+      if (!ok[j]) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[j] += round_bf16(bf16_to_f32(a[i] & 0xffffu) * bf16_to_f32(b[j][i] & 0xffffu));
+        acc[j] += round_bf16(bf16_to_f32(a[i] >> 16) * bf16_to_f32(b[j][i] >> 16));
+      }
+      if (d_raw != nullptr) {
+        u32x4_t v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          v[i] = pack_bf16x2(bf16_to_f32(a[i] & 0xffffu) * s[j], bf16_to_f32(a[i] >> 16) * s[j]);
+        st16(d_raw + row[j] * h + c, v);
       }
     }
-    acc = wave_sum_f(acc);
-    if (lane == 0) dw[p] = (uint16_t)f32_to_bf16_rne(acc);
+  }
+#pragma unroll
+  for (int j = 0; j < KT; ++j) {
+    const float r = wave_sum_f(acc[j]);
+    if (lane == 0) dw[t * KT + j] = (uint16_t)f32_to_bf16_rne(r);
   }
 }
 
@@ -346,17 +372,31 @@ hipError_t launch_transpose_experts(const uint16_t* src, uint16_t* dst, int E, i
   return hipGetLastError();
 }
 
-hipError_t launch_pair_dots(const uint16_t* dout, const uint16_t* Y, const int32_t* inv, const void* idx,
-                            bool idx64, uint16_t* dw, int64_t T, int h, int E, int k, hipStream_t stream) {
-  if (T == 0) return hipSuccess;
+template <typename IdxT>
+static hipError_t launch_pair_dots_t(const uint16_t* dout, const uint16_t* Y, const int32_t* inv, const IdxT* idx,
+                                     const uint16_t* w, uint16_t* dw, uint16_t* d_raw, int64_t T, int h, int E, int k,
+                                     hipStream_t stream) {
   const dim3 grid((unsigned)((T + 3) / 4));
-  if (idx64)
-    hipLaunchKernelGGL(pair_dots_kernel<int64_t>, grid, dim3(256), 0, stream, dout, Y, inv,
-                       static_cast<const int64_t*>(idx), dw, T, h, E, k);
-  else
-    hipLaunchKernelGGL(pair_dots_kernel<int32_t>, grid, dim3(256), 0, stream, dout, Y, inv,
-                       static_cast<const int32_t*>(idx), dw, T, h, E, k);
+#define Q38_PD(KT)                                                                                              \
+  case KT:                                                                                                      \
+    hipLaunchKernelGGL((pair_dots_kernel<IdxT, KT>), grid, dim3(256), 0, stream, dout, Y, inv, idx, w, dw, d_raw, \
+                       T, h, E);                                                                                \
+    break;
+  switch (k) {
+    Q38_PD(1) Q38_PD(2) Q38_PD(3) Q38_PD(4) Q38_PD(5) Q38_PD(6) Q38_PD(7) Q38_PD(8)
+    default: return hipErrorInvalidValue;
+  }
+#undef Q38_PD
   return hipGetLastError();
+}
+
+hipError_t launch_pair_dots(const uint16_t* dout, const uint16_t* Y, const int32_t* inv, const void* idx,
+                            bool idx64, const uint16_t* w, uint16_t* dw, uint16_t* d_raw, int64_t T, int h, int E,
+                            int k, hipStream_t stream) {
+  if (T == 0) return hipSuccess;
+  if (idx64)
+    return launch_pair_dots_t(dout, Y, inv, static_cast<const int64_t*>(idx), w, dw, d_raw, T, h, E, k, stream);
+  return launch_pair_dots_t(dout, Y, inv, static_cast<const int32_t*>(idx), w, dw, d_raw, T, h, E, k, stream);
 }
 
 hipError_t launch_gather_rows(const uint16_t* src, const int32_t* perm, const uint16_t* w, const int32_t* starts,

@@ -45,7 +45,8 @@ hipError_t launch_gather_gemm(const uint16_t* A, const int32_t* perm, const int4
 
 // Experts backward element-wise steps (q38moe_backward.hip).
 hipError_t launch_pair_dots(const uint16_t* dout, const uint16_t* Y, const int32_t* inv, const void* idx,
-                            bool idx64, uint16_t* dw, int64_t T, int h, int E, int k, hipStream_t stream);
+                            bool idx64, const uint16_t* w, uint16_t* dw, uint16_t* d_raw, int64_t T, int h, int E,
+                            int k, hipStream_t stream);
 hipError_t launch_gather_rows(const uint16_t* src, const int32_t* perm, const uint16_t* w, const int32_t* starts,
                               const int32_t* counts, uint16_t* dst, int64_t P, int h, int E, int k,
                               hipStream_t stream);

@@ -12,7 +12,7 @@ import torch  # noqa: F401  (loads the HIP runtime first)
 
 LIB_PATH = Path(os.environ.get("Q38MOE_LIB", Path(__file__).resolve().parent / "libq38moe.so"))
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 BF16 = 1
 
 _c_int, _c_i32, _c_i64, _c_size, _vp = ctypes.c_int, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
@@ -51,7 +51,7 @@ SIGNATURES = {
     "q38moe_block_fp8_workspace_bytes": (_c_int, [_c_i64, _c_i32, _c_i32, _c_i32, _c_i32, ctypes.POINTER(_c_size)]),
     "q38moe_block_forward_fp8": (_c_int, [_vp] * 18 + [_c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _vp, _c_size, _vp]),
     "q38moe_gather_gemm": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _vp]),
-    "q38moe_pair_dots": (_c_int, [_vp, _vp, _vp, _vp, _c_i32, _vp, _c_i64, _c_i32, _c_i32, _c_i32, _vp]),
+    "q38moe_pair_dots": (_c_int, [_vp] * 4 + [_c_i32, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _c_i32, _vp]),
     "q38moe_gather_rows": (_c_int, [_vp] * 6 + [_c_i64, _c_i32, _c_i32, _c_i32, _vp]),
     "q38moe_transpose_experts": (_c_int, [_vp, _vp, _c_i32, _c_i32, _c_i32, _vp]),
     "q38moe_expert_wgrad": (_c_int, [_vp] * 6 + [_c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _vp]),

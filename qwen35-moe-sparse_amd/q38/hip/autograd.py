@@ -7,7 +7,7 @@ scripts/check_q38_kernels.py:19-27 compares. Here the forward is the inference p
 permutation, grouped gate/up + SwiGLU, grouped down, combine) keeping the sorted H and Y rows, and
 the backward runs, with Y' = dout[t] * w[p] (the routed raw rows' gradient) in sorted order:
 
-  dw[p]   = <dout[t], Y[p]>                       q38moe_pair_dots
+  dw[p]   = <dout[t], Y[p]>                       q38moe_pair_dots (which also writes Y')
   [g | u] = x[t] . gate_up_proj[e]^T              q38moe_gather_gemm (recomputed, sorted rows)
   dH      = Y' . down_proj[e]                     q38moe_down on down_proj^T [E, I, h] (q38moe_transpose_experts)
   dGU     = SwiGLU backward (dH, g, u)            q38moe_swiglu_backward
@@ -48,10 +48,16 @@ class HipExperts(torch.autograd.Function):
         E, twoI, _ = w_gate_up.shape
         dout = dout.to(torch.bfloat16).contiguous()
         need_x, _, need_w, need_gu, need_dn = ctx.needs_input_grad
-        dw = ops.pair_dots(dout, Y, inv, idx, E) if need_w else None
-        dx = dgu_w = ddn_w = None
-        if need_x or need_gu or need_dn:
+        need_rows = need_x or need_gu or need_dn
+        dw = d_raw = None
+        if need_w and need_rows:
+            dw, d_raw = ops.pair_dots(dout, Y, inv, idx, E, w=w)  # one pass over dout for both
+        elif need_w:
+            dw = ops.pair_dots(dout, Y, inv, idx, E)
+        elif need_rows:
             d_raw = ops.gather_rows(dout, perm, starts, counts, k, w=w)
+        dx = dgu_w = ddn_w = None
+        if need_rows:
             if need_dn:
                 ddn_w = ops.expert_wgrad(d_raw, H, starts, counts, k)
             if need_x or need_gu:

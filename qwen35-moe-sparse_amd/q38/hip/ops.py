@@ -230,8 +230,10 @@ def gather_gemm(x, perm, w, tiles, tile_count, k):
     return C
 
 
-def pair_dots(dout, Y, inv, idx, E):
-    """Routing-weight gradient dw[t, j] = <dout[t], Y[inv[t*k+j]]> (bf16 products, fp32 sum): [T,k] bf16."""
+def pair_dots(dout, Y, inv, idx, E, w=None):
+    """Routing-weight gradient dw[t, j] = <dout[t], Y[inv[t*k+j]]> (bf16 products, fp32 sum): [T,k] bf16.
+    With w (top_k_weights [T,k]) also returns, from the same pass, the routed raw rows' gradient in
+    sorted order, d_raw[inv[p]] = bf16(dout[t] * w[p]) [T*k, h] (rows of dropped pairs unwritten)."""
     _need(dout, "dout", ndim=2)
     _need(Y, "Y", ndim=2)
     _need(inv, "inv", dtype=torch.int32)
@@ -239,9 +241,13 @@ def pair_dots(dout, Y, inv, idx, E):
     T, h = dout.shape
     k = idx.shape[1]
     dw = torch.empty(T, k, dtype=torch.bfloat16, device=dout.device)
-    check(lib.q38moe_pair_dots(_ptr(dout), _ptr(Y), _ptr(inv), _ptr(idx), _idx_flag(idx), _ptr(dw), T, h, E, k,
-                               _stream(dout.device)), "q38moe_pair_dots")
-    return dw
+    d_raw = None
+    if w is not None:
+        _need(w, "topk_w", ndim=2)
+        d_raw = torch.empty(T * k, h, dtype=torch.bfloat16, device=dout.device)
+    check(lib.q38moe_pair_dots(_ptr(dout), _ptr(Y), _ptr(inv), _ptr(idx), _idx_flag(idx), _ptr(w), _ptr(dw),
+                               _ptr(d_raw), T, h, E, k, _stream(dout.device)), "q38moe_pair_dots")
+    return dw if w is None else (dw, d_raw)
 
 
 def gather_rows(src, perm, starts, counts, k, w=None):

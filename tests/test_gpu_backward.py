@@ -168,3 +168,22 @@ def test_transpose_experts(gpu, E, R, C):
     out = ops.transpose_experts(w.to(gpu))
     torch.cuda.synchronize()
     assert out.shape == (E, C, R) and torch.equal(out.cpu(), w.transpose(1, 2).contiguous())
+
+
+@pytest.mark.parametrize("name,T,drop", [("c2", 2048, 0), ("c1", 700, 40)])
+def test_pair_dots_rows_fused(gpu, name, T, drop):
+    """pair_dots with top_k_weights writes the same routed-row gradient as gather_rows and the same
+    weight gradient as pair_dots alone, bit for bit (same roundings, one pass)."""
+    from q38.hip import ops
+    wl, x, idx, w, wgu, wdn, dout = _inputs(name, T, drop)
+    E, k = wl.experts, wl.topk
+    di, dw_, dd = idx.to(gpu), w.to(gpu), dout.to(gpu)
+    counts, starts, perm, inv, _, _ = ops.permute(di, ops.histogram(di, E), E)
+    Y = torch.randn(T * k, wl.hidden, device=gpu).to(torch.bfloat16)
+    dw_alone = ops.pair_dots(dd, Y, inv, di, E)
+    dw_fused, d_raw = ops.pair_dots(dd, Y, inv, di, E, w=dw_)
+    rows = ops.gather_rows(dd, perm, starts, counts, k, w=dw_)
+    torch.cuda.synchronize()
+    filled = int(counts.sum())
+    assert torch.equal(dw_alone, dw_fused)
+    assert torch.equal(d_raw[:filled], rows[:filled])
