@@ -338,6 +338,155 @@ __global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* G, co
   }
 }
 
+// Sorted-row form of the weight gradients with asynchronous staging: both operands' rows are in
+// sorted order (X = H, or the tokens already gathered into sorted order), so 32-row slices of
+// G[:, m0 .. m0+127] and X[:, n0 .. n0+127] are copied global -> LDS by global_load_lds_dwordx4 into
+// a 4-slot ring (three slices in flight, no register staging) and the MFMA fragments are read
+// straight from the row-major slices with the gfx950 transposing LDS read ds_read_b64_tr_b16:
+// within each 16-lane group, component j of lane i is element i % 4 of the 8 bytes that lane
+// 4j + i/4 addresses, so lanes addressing rows k0 + s/4, columns c0 + 4 (s % 4) receive rows
+// k0 .. k0+3 of column c0 + i; two such reads are one 8-row fragment. Slices are row-major, 256
+// bytes per row (128 columns), 16-byte chunk c of row r at chunk c ^ 4 (r % 4): the 32 lanes of a
+// half-wave read 4 rows x 64 bytes and cover the 64 banks once. Rows past the expert's count are
+// copied from its last row (in bounds) and zeroed in the fragments of the last slice; columns past
+// M or N are copied from column 0 and never stored. One 256-thread block per 128 x 128 tile as in
+// expert_wgrad_kernel (same accumulator layout and epilogue).
+constexpr int WD_BK = 32;  // rows per slice
+constexpr int WD_NS = 4;   // ring slots
+
+__device__ __forceinline__ uint32_t wd_lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
+}
+// global_load_lds_dwordx4 from inline asm (M0 = the wave's LDS base; lane l lands at +16 l). The
+// compiler does not see these loads: their completion is ordered by the explicit vmcnt waits below.
+__device__ __forceinline__ void wd_dma16(const void* gsrc, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(gsrc)
+               : "memory", "m0");
+}
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 wd_read_tr(const uint8_t* lds) {
+  const i16x4_t v =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(uintptr_t)(
+          (const __attribute__((address_space(3))) uint8_t*)lds));
+  return __builtin_bit_cast(uint2, v);
+}
+__device__ __forceinline__ int wd_off(int row, int col) {  // byte offset of (row, col) in a slice
+  return row * 256 + 16 * ((col >> 3) ^ (4 * (row & 3))) + 2 * (col & 7);
+}
+
+__global__ __launch_bounds__(256) void expert_wgrad_dma_kernel(const uint16_t* G, const uint16_t* X,
+                                                               const int32_t* __restrict__ starts,
+                                                               const int32_t* __restrict__ counts,
+                                                               uint16_t* __restrict__ dW, int64_t P, int M,
+                                                               int N, int tm, int tn) {
+  __shared__ __align__(16) uint8_t ring[WD_NS][2][WD_BK * 256];  // [slot][G, X][row][column]
+  const int nb = gridDim.x, b = blockIdx.x;
+  const int L = (nb & 7) == 0 ? (b & 7) * (nb >> 3) + (b >> 3) : b;
+  const int e = L / (tm * tn), rem = L - e * tm * tn;
+  const int m0 = (rem / tn) * WG_T, n0 = (rem % tn) * WG_T;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t r0 = P > 0 ? starts[e] : 0;
+  const int cnt = P > 0 ? (int)max((int64_t)0, min((int64_t)counts[e], P - r0)) : 0;
+  const int nsl = (cnt + WD_BK - 1) / WD_BK;
+  const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lh = lane >> 5;
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[a][c][i] = 0.0f;
+
+  if (nsl > 0) {
+    // Copies: wave w fills slice rows 8w .. 8w+7 of both operands, 4 rows per instruction; lane l
+    // writes row 4q + l/16, position l % 16, i.e. global chunk (l % 16) ^ 4 (row % 4).
+    const int crow = lane >> 4;
+    const int pos = lane & 15;
+    auto issue = [&](int sl) {
+      const int slot = sl & (WD_NS - 1);
+#pragma unroll
+      for (int op = 0; op < 2; ++op) {
+        const uint16_t* base = op ? X : G;
+        const int ld = op ? N : M, c0 = op ? n0 : m0;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int row = 8 * wave + 4 * q + crow;
+          const int col = c0 + 8 * (pos ^ (4 * (row & 3)));
+          const int64_t grow = r0 + min(sl * WD_BK + row, cnt - 1);
+          wd_dma16(base + grow * ld + (col < ld ? col : 0), wd_lds_addr(&ring[slot][op][(8 * wave + 4 * q) * 256]));
+        }
+      }
+    };
+    issue(0);
+    issue(1);
+    issue(2);
+    const int g = lane >> 4, gi = lane & 15;
+    for (int s = 0; s < nsl; ++s) {
+      // This wave's copies of slice s are done when at most slices s+1 and s+2 (4 copies each)
+      // are outstanding; the barrier makes that true of every wave and orders the LDS reads of
+      // slice s-1 (drained by the lgkmcnt wait) before its slot is refilled with slice s+3.
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+      issue(s + 3);
+      const uint8_t* sg = ring[s & (WD_NS - 1)][0];
+      const uint8_t* sx = ring[s & (WD_NS - 1)][1];
+      const int left = cnt - s * WD_BK;  // rows of this slice that exist (mask when < 32)
+#pragma unroll
+      for (int u = 0; u < WD_BK / 16; ++u) {
+        u32x4_t gf[2], xf[2];
+        const int k0 = 16 * u + 8 * (g >> 1);
+        const int row = k0 + (gi >> 2), colo = 16 * (g & 1) + 4 * (gi & 3);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int cg = 64 * wm + 32 * i + colo, cx = 64 * wn + 32 * i + colo;
+          const uint2 g0 = wd_read_tr(sg + wd_off(row, cg)), g1 = wd_read_tr(sg + wd_off(row + 4, cg));
+          const uint2 x0 = wd_read_tr(sx + wd_off(row, cx)), x1 = wd_read_tr(sx + wd_off(row + 4, cx));
+          gf[i] = (u32x4_t){g0.x, g0.y, g1.x, g1.y};
+          xf[i] = (u32x4_t){x0.x, x0.y, x1.x, x1.y};
+        }
+        if (left < WD_BK) {  // last, partial slice: rows k >= left are copies of the last row
+          const int kb = 16 * u + 8 * lh;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const uint32_t keep = (kb + 2 * d < left ? 0xffffu : 0u) | (kb + 2 * d + 1 < left ? 0xffff0000u : 0u);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+              gf[i][d] &= keep;
+              xf[i][d] &= keep;
+            }
+          }
+        }
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+          for (int mi = 0; mi < 2; ++mi) acc[ni][mi] = mfma32x32x16(xf[ni], gf[mi], acc[ni][mi]);
+      }
+    }
+    // The copies of the three slices past the end are still in flight: complete them before the
+    // block's LDS can be released.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+
+  uint16_t* const out = dW + (int64_t)e * M * N;
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    const int m = m0 + 64 * wm + 32 * mi + lr;
+    if (m >= M) continue;
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int n = n0 + 64 * wn + 32 * ni + 8 * gq + 4 * lh;
+        if (n < N)
+          *reinterpret_cast<uint2*>(out + (int64_t)m * N + n) =
+              make_uint2(pack_bf16x2(acc[ni][mi][4 * gq], acc[ni][mi][4 * gq + 1]),
+                         pack_bf16x2(acc[ni][mi][4 * gq + 2], acc[ni][mi][4 * gq + 3]));
+      }
+  }
+}
+
 // dst[e] = src[e]^T for bf16 matrices [E, R, C] -> [E, C, R] (the expert weights as the K-major
 // operand of the input-gradient products). One wave per 64 x 64 tile: lane l moves the 8 x 8 block
 // at source rows 8 (l % 8), columns 8 (l / 8) through registers (8 16-byte loads, transpose8x8,
@@ -414,6 +563,11 @@ hipError_t launch_expert_wgrad(const uint16_t* G, const uint16_t* X, const int32
   const int tm = (M + WG_T - 1) / WG_T, tn = (N + WG_T - 1) / WG_T;
   const int64_t nb = (int64_t)E * tm * tn;
   if (nb == 0) return hipSuccess;
+  if (perm == nullptr) {
+    hipLaunchKernelGGL(expert_wgrad_dma_kernel, dim3((unsigned)nb), dim3(256), 0, stream, G, X, starts, counts, dW, P,
+                       M, N, tm, tn);
+    return hipGetLastError();
+  }
   if (perm != nullptr)
     hipLaunchKernelGGL(expert_wgrad_kernel<true>, dim3((unsigned)nb), dim3(256), 0, stream, G, X, perm, starts, counts,
                        dW, P, M, N, k, tm, tn);
