@@ -341,18 +341,19 @@ __global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* G, co
 // Sorted-row form of the weight gradients with asynchronous staging: both operands' rows are in
 // sorted order (X = H, or the tokens already gathered into sorted order), so 32-row slices of
 // G[:, m0 .. m0+127] and X[:, n0 .. n0+127] are copied global -> LDS by global_load_lds_dwordx4 into
-// a 4-slot ring (three slices in flight, no register staging) and the MFMA fragments are read
+// a WD_NS-slot ring (WD_NS - 1 slices in flight, no register staging) and the MFMA fragments are read
 // straight from the row-major slices with the gfx950 transposing LDS read ds_read_b64_tr_b16:
 // within each 16-lane group, component j of lane i is element i % 4 of the 8 bytes that lane
 // 4j + i/4 addresses, so lanes addressing rows k0 + s/4, columns c0 + 4 (s % 4) receive rows
 // k0 .. k0+3 of column c0 + i; two such reads are one 8-row fragment. Slices are row-major, 256
-// bytes per row (128 columns), 16-byte chunk c of row r at chunk c ^ 4 (r % 4): the 32 lanes of a
-// half-wave read 4 rows x 64 bytes and cover the 64 banks once. Rows past the expert's count are
+// or 512 bytes per row (128 or 256 columns), 16-byte chunk c of row r at chunk c ^ 4 (r % 4): the
+// 32 lanes of a half-wave read 4 rows x 64 bytes and cover the 64 banks once. Rows past the expert's count are
 // copied from its last row (in bounds) and zeroed in the fragments of the last slice; columns past
-// M or N are copied from column 0 and never stored. One 256-thread block per 128 x 128 tile as in
-// expert_wgrad_kernel (same accumulator layout and epilogue).
-constexpr int WD_BK = 32;  // rows per slice
-constexpr int WD_NS = 4;   // ring slots
+// M or N are copied from column 0 and never stored. One 256-thread block per 128 (G) x 256 (X)
+// tile; each wave multiplies 64 x 128 (2 x 4 blocks of mfma_f32_32x32x16_bf16, X as the A operand).
+constexpr int WD_BK = 32;   // rows per slice
+constexpr int WD_NS = 3;    // ring slots (72 KB: two blocks per CU)
+constexpr int WD_TN = 256;  // X columns per tile (G columns: WG_T = 128)
 
 __device__ __forceinline__ uint32_t wd_lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane(
@@ -371,8 +372,10 @@ __device__ __forceinline__ uint2 wd_read_tr(const uint8_t* lds) {
           (const __attribute__((address_space(3))) uint8_t*)lds));
   return __builtin_bit_cast(uint2, v);
 }
-__device__ __forceinline__ int wd_off(int row, int col) {  // byte offset of (row, col) in a slice
-  return row * 256 + 16 * ((col >> 3) ^ (4 * (row & 3))) + 2 * (col & 7);
+// Byte offset of (row, col) in a slice of PITCH-byte rows: 16-byte chunk c of row r at c ^ 4 (r % 4).
+template <int PITCH>
+__device__ __forceinline__ int wd_off(int row, int col) {
+  return row * PITCH + 16 * ((col >> 3) ^ (4 * (row & 3))) + 2 * (col & 7);
 }
 
 __global__ __launch_bounds__(256) void expert_wgrad_dma_kernel(const uint16_t* G, const uint16_t* X,
@@ -380,70 +383,77 @@ __global__ __launch_bounds__(256) void expert_wgrad_dma_kernel(const uint16_t* G
                                                                const int32_t* __restrict__ counts,
                                                                uint16_t* __restrict__ dW, int64_t P, int M,
                                                                int N, int tm, int tn) {
-  __shared__ __align__(16) uint8_t ring[WD_NS][2][WD_BK * 256];  // [slot][G, X][row][column]
+  __shared__ __align__(16) uint8_t ring_g[WD_NS][WD_BK * 2 * WG_T];   // [slot][row][128 columns]
+  __shared__ __align__(16) uint8_t ring_x[WD_NS][WD_BK * 2 * WD_TN];  // [slot][row][256 columns]
   const int nb = gridDim.x, b = blockIdx.x;
   const int L = (nb & 7) == 0 ? (b & 7) * (nb >> 3) + (b >> 3) : b;
   const int e = L / (tm * tn), rem = L - e * tm * tn;
-  const int m0 = (rem / tn) * WG_T, n0 = (rem % tn) * WG_T;
+  const int m0 = (rem / tn) * WG_T, n0 = (rem % tn) * WD_TN;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t r0 = P > 0 ? starts[e] : 0;
   const int cnt = P > 0 ? (int)max((int64_t)0, min((int64_t)counts[e], P - r0)) : 0;
   const int nsl = (cnt + WD_BK - 1) / WD_BK;
+  // Wave (wm, wn) owns G columns 64 wm .. +63 and X columns 128 wn .. +127 of the tile.
   const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lh = lane >> 5;
-  f32x16_t acc[2][2];
+  f32x16_t acc[4][2];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[a][c][i] = 0.0f;
 
   if (nsl > 0) {
-    // Copies: wave w fills slice rows 8w .. 8w+7 of both operands, 4 rows per instruction; lane l
-    // writes row 4q + l/16, position l % 16, i.e. global chunk (l % 16) ^ 4 (row % 4).
-    const int crow = lane >> 4;
-    const int pos = lane & 15;
+    // Copies: wave w fills slice rows 8w .. 8w+7 of both operands: G in 2 instructions of 4
+    // 256-byte rows (lane l: row 4q + l/16, position l % 16), X in 4 instructions of 2 512-byte
+    // rows (lane l: row 2q + l/32, position l % 32); position p of row r holds chunk p ^ 4 (r % 4).
     auto issue = [&](int sl) {
-      const int slot = sl & (WD_NS - 1);
+      const int slot = sl % WD_NS;
 #pragma unroll
-      for (int op = 0; op < 2; ++op) {
-        const uint16_t* base = op ? X : G;
-        const int ld = op ? N : M, c0 = op ? n0 : m0;
+      for (int q = 0; q < 2; ++q) {
+        const int row = 8 * wave + 4 * q + (lane >> 4);
+        const int col = m0 + 8 * ((lane & 15) ^ (4 * (row & 3)));
+        const int64_t grow = r0 + min(sl * WD_BK + row, cnt - 1);
+        wd_dma16(G + grow * M + (col < M ? col : 0), wd_lds_addr(&ring_g[slot][(8 * wave + 4 * q) * 2 * WG_T]));
+      }
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const int row = 8 * wave + 4 * q + crow;
-          const int col = c0 + 8 * (pos ^ (4 * (row & 3)));
-          const int64_t grow = r0 + min(sl * WD_BK + row, cnt - 1);
-          wd_dma16(base + grow * ld + (col < ld ? col : 0), wd_lds_addr(&ring[slot][op][(8 * wave + 4 * q) * 256]));
-        }
+      for (int q = 0; q < 4; ++q) {
+        const int row = 8 * wave + 2 * q + (lane >> 5);
+        const int col = n0 + 8 * ((lane & 31) ^ (4 * (row & 3)));
+        const int64_t grow = r0 + min(sl * WD_BK + row, cnt - 1);
+        wd_dma16(X + grow * N + (col < N ? col : 0), wd_lds_addr(&ring_x[slot][(8 * wave + 2 * q) * 2 * WD_TN]));
       }
     };
-    issue(0);
-    issue(1);
-    issue(2);
+#pragma unroll
+    for (int sl = 0; sl < WD_NS - 1; ++sl) issue(sl);
     const int g = lane >> 4, gi = lane & 15;
     for (int s = 0; s < nsl; ++s) {
-      // This wave's copies of slice s are done when at most slices s+1 and s+2 (4 copies each)
-      // are outstanding; the barrier makes that true of every wave and orders the LDS reads of
-      // slice s-1 (drained by the lgkmcnt wait) before its slot is refilled with slice s+3.
+      // This wave's copies of slice s are done when at most those of slices s+1 .. s+NS-2 (6
+      // each) are outstanding; the barrier makes that true of every wave and orders the LDS reads
+      // of slice s-1 (drained by the lgkmcnt wait) before its slot is refilled with slice s+NS-1.
       __builtin_amdgcn_s_waitcnt(0xC07F);
-      asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
-      issue(s + 3);
-      const uint8_t* sg = ring[s & (WD_NS - 1)][0];
-      const uint8_t* sx = ring[s & (WD_NS - 1)][1];
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(6 * (WD_NS - 2)) : "memory");
+      issue(s + WD_NS - 1);
+      const uint8_t* sg = ring_g[s % WD_NS];
+      const uint8_t* sx = ring_x[s % WD_NS];
       const int left = cnt - s * WD_BK;  // rows of this slice that exist (mask when < 32)
 #pragma unroll
       for (int u = 0; u < WD_BK / 16; ++u) {
-        u32x4_t gf[2], xf[2];
-        const int k0 = 16 * u + 8 * (g >> 1);
-        const int row = k0 + (gi >> 2), colo = 16 * (g & 1) + 4 * (gi & 3);
+        u32x4_t gf[2], xf[4];
+        const int row = 16 * u + 8 * (g >> 1) + (gi >> 2), colo = 16 * (g & 1) + 4 * (gi & 3);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-          const int cg = 64 * wm + 32 * i + colo, cx = 64 * wn + 32 * i + colo;
-          const uint2 g0 = wd_read_tr(sg + wd_off(row, cg)), g1 = wd_read_tr(sg + wd_off(row + 4, cg));
-          const uint2 x0 = wd_read_tr(sx + wd_off(row, cx)), x1 = wd_read_tr(sx + wd_off(row + 4, cx));
+          const int cg = 64 * wm + 32 * i + colo;
+          const uint2 g0 = wd_read_tr(sg + wd_off<2 * WG_T>(row, cg));
+          const uint2 g1 = wd_read_tr(sg + wd_off<2 * WG_T>(row + 4, cg));
           gf[i] = (u32x4_t){g0.x, g0.y, g1.x, g1.y};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int cx = 128 * wn + 32 * i + colo;
+          const uint2 x0 = wd_read_tr(sx + wd_off<2 * WD_TN>(row, cx));
+          const uint2 x1 = wd_read_tr(sx + wd_off<2 * WD_TN>(row + 4, cx));
           xf[i] = (u32x4_t){x0.x, x0.y, x1.x, x1.y};
         }
         if (left < WD_BK) {  // last, partial slice: rows k >= left are copies of the last row
@@ -452,33 +462,33 @@ __global__ __launch_bounds__(256) void expert_wgrad_dma_kernel(const uint16_t* G
           for (int d = 0; d < 4; ++d) {
             const uint32_t keep = (kb + 2 * d < left ? 0xffffu : 0u) | (kb + 2 * d + 1 < left ? 0xffff0000u : 0u);
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-              gf[i][d] &= keep;
-              xf[i][d] &= keep;
-            }
+            for (int i = 0; i < 2; ++i) gf[i][d] &= keep;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xf[i][d] &= keep;
           }
         }
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
+        for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
           for (int mi = 0; mi < 2; ++mi) acc[ni][mi] = mfma32x32x16(xf[ni], gf[mi], acc[ni][mi]);
       }
     }
-    // The copies of the three slices past the end are still in flight: complete them before the
+    // The copies of the NS - 1 slices past the end are still in flight: complete them before the
     // block's LDS can be released.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 
+  // acc[ni][mi][i] of lane l: column n = 128 wn + 32 ni + 8 (i/4) + 4 (l/32) + i%4, row m = 64 wm + 32 mi + l%32.
   uint16_t* const out = dW + (int64_t)e * M * N;
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
     const int m = m0 + 64 * wm + 32 * mi + lr;
     if (m >= M) continue;
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni)
+    for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
-        const int n = n0 + 64 * wn + 32 * ni + 8 * gq + 4 * lh;
+        const int n = n0 + 128 * wn + 32 * ni + 8 * gq + 4 * lh;
         if (n < N)
           *reinterpret_cast<uint2*>(out + (int64_t)m * N + n) =
               make_uint2(pack_bf16x2(acc[ni][mi][4 * gq], acc[ni][mi][4 * gq + 1]),
@@ -564,8 +574,9 @@ hipError_t launch_expert_wgrad(const uint16_t* G, const uint16_t* X, const int32
   const int64_t nb = (int64_t)E * tm * tn;
   if (nb == 0) return hipSuccess;
   if (perm == nullptr) {
-    hipLaunchKernelGGL(expert_wgrad_dma_kernel, dim3((unsigned)nb), dim3(256), 0, stream, G, X, starts, counts, dW, P,
-                       M, N, tm, tn);
+    const int tnd = (N + WD_TN - 1) / WD_TN;
+    hipLaunchKernelGGL(expert_wgrad_dma_kernel, dim3((unsigned)((int64_t)E * tm * tnd)), dim3(256), 0, stream, G, X,
+                       starts, counts, dW, P, M, N, tm, tnd);
     return hipGetLastError();
   }
   if (perm != nullptr)
