@@ -169,7 +169,8 @@ __global__ __launch_bounds__(256) void swiglu_backward_kernel(const uint16_t* __
 // [starts[e], starts[e] + counts[e])) of G[r][m] * X[src(r)][n], rounded once to bf16; src(r) =
 // perm[r] / k (X = the tokens, gathered) or r (X already in sorted order). With G = [d_g | d_u] and
 // X = x this is gate_up_proj's gradient [E, 2I, h]; with G = the routed output rows' gradient and
-// X = H it is down_proj's [E, h, I] (torch's bf16 mm: fp32 accumulation, one rounding).
+// X = H it is down_proj's [E, h, I] (torch's bf16 mm: fp32 accumulation, one rounding). The sorted
+// form runs expert_wgrad_dma_kernel (below); this kernel is the gathered form.
 //
 // The reduction runs over rows, which are the strided dimension of both operands, so each 64-row
 // slice is transposed on its way into LDS: a thread loads an 8 x 8 block (8 rows, 16 bytes each),
@@ -192,7 +193,6 @@ __device__ __forceinline__ void transpose8x8(const u32x4_t (&a)[8], u32x4_t (&b)
     }
 }
 
-template <bool GATHER>
 // G, X and perm are not declared __restrict__: loads from restrict read-only arguments count as
 // unclobbered and may be moved across the workgroup barriers, which undoes the slice pipeline.
 __global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* G, const uint16_t* X,
@@ -268,7 +268,7 @@ __global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* G, co
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int rr = min(sl * WG_K + 8 * rb + i, cnt - 1);
-        if (GATHER && XR) {
+        if (XR) {
           const uint32_t pr = (uint32_t)perm[r0 + rr];
           src[i] = (int)(k > 1 ? __umulhi(pr, kmagic) : pr);
         } else {
@@ -579,12 +579,8 @@ hipError_t launch_expert_wgrad(const uint16_t* G, const uint16_t* X, const int32
                        starts, counts, dW, P, M, N, tm, tnd);
     return hipGetLastError();
   }
-  if (perm != nullptr)
-    hipLaunchKernelGGL(expert_wgrad_kernel<true>, dim3((unsigned)nb), dim3(256), 0, stream, G, X, perm, starts, counts,
-                       dW, P, M, N, k, tm, tn);
-  else
-    hipLaunchKernelGGL(expert_wgrad_kernel<false>, dim3((unsigned)nb), dim3(256), 0, stream, G, X, perm, starts,
-                       counts, dW, P, M, N, k, tm, tn);
+  hipLaunchKernelGGL(expert_wgrad_kernel, dim3((unsigned)nb), dim3(256), 0, stream, G, X, perm, starts, counts, dW, P,
+                     M, N, k, tm, tn);
   return hipGetLastError();
 }
 
