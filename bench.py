@@ -367,10 +367,8 @@ def backward_bench(args):
             "transpose_gate_up_proj": (lambda: ops.transpose_experts(wgu), by(2 * 2 * E * 2 * I * h)),
             "dx_down_t": (lambda: ops.down(dGU, wgu_t, tiles, tcount, T, k), fl(2 * P * 2 * I * h)),
             "dx_combine": (lambda: ops.combine(dxp, inv, ones, E, idx=idx), by(2 * (P * h + T * h))),
-            "gather_x_sorted": (lambda: ops.gather_rows(xb, perm, starts, counts, k), by(2 * (T * h + P * h))),
-            "wgrad_gate_up": (lambda: ops.expert_wgrad(dGU, xs, starts, counts, k), fl(2 * P * 2 * I * h)),
-            "wgrad_gate_up_gathered": (lambda: ops.expert_wgrad(dGU, xb, starts, counts, k, perm=perm),
-                                       fl(2 * P * 2 * I * h)),
+            "wgrad_gate_up": (lambda: ops.expert_wgrad(dGU, xb, starts, counts, k, perm=perm), fl(2 * P * 2 * I * h)),
+            "wgrad_gate_up_presorted": (lambda: ops.expert_wgrad(dGU, xs, starts, counts, k), fl(2 * P * 2 * I * h)),
             "wgrad_down": (lambda: ops.expert_wgrad(d_raw, H, starts, counts, k), fl(2 * P * h * I)),
         }
         kernels = {}

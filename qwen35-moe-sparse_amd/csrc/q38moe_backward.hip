@@ -13,20 +13,7 @@
 
 namespace q38 {
 
-constexpr int WG_T = 128;              // weight-gradient output tile (rows and columns)
-constexpr int WG_K = 64;               // sorted rows per LDS slice
-constexpr int WG_PITCH = 2 * WG_K;     // bytes per staged column: 64 bf16 in 8 16-byte chunks
-
-// LDS byte offset of 16-byte row chunk q (0..7) of staged column c. Columns 2p and 2p+1 share a
-// 256-byte line of 16 chunk slots; slot (8 (c & 1) + q) ^ key(p), key(p) = ((p >> 2) ^ (p & 7)) & 15.
-// The LDS serves a 16-byte access 16 lanes per pass over its 64 banks (16 slots of 16 bytes), and
-// both access patterns fill all 16 slots per pass: the transpose writes (16 lanes = 16 column
-// blocks 8cb + j, one chunk: key runs over 16 values with cb) and the fragment reads (16 lanes = 16
-// consecutive columns, one chunk: c & 1 and the low 3 key bits run over 2 x 8 values).
-__device__ __forceinline__ int wg_slot(int c, int q) {
-  const int p = c >> 1;
-  return p * 256 + 16 * (((c & 1) * 8 + q) ^ (((p >> 2) ^ (p & 7)) & 15));
-}
+constexpr int WG_T = 128;  // weight-gradient output tile: G columns (X columns: WD_TN)
 
 __device__ __forceinline__ float wave_sum_f(float v) {
 #pragma unroll
@@ -169,186 +156,20 @@ __global__ __launch_bounds__(256) void swiglu_backward_kernel(const uint16_t* __
 // [starts[e], starts[e] + counts[e])) of G[r][m] * X[src(r)][n], rounded once to bf16; src(r) =
 // perm[r] / k (X = the tokens, gathered) or r (X already in sorted order). With G = [d_g | d_u] and
 // X = x this is gate_up_proj's gradient [E, 2I, h]; with G = the routed output rows' gradient and
-// X = H it is down_proj's [E, h, I] (torch's bf16 mm: fp32 accumulation, one rounding). The sorted
-// form runs expert_wgrad_dma_kernel (below); this kernel is the gathered form.
+// X = H it is down_proj's [E, h, I] (torch's bf16 mm: fp32 accumulation, one rounding). The
+// reduction runs over rows, the strided dimension of both operands.
 //
-// The reduction runs over rows, which are the strided dimension of both operands, so each 64-row
-// slice is transposed on its way into LDS: a thread loads an 8 x 8 block (8 rows, 16 bytes each),
-// transposes it in registers and writes 8 column-major 16-byte runs, after which the MFMA
-// fragments (8 consecutive rows of one column) are single 16-byte LDS reads, without bank
-// conflicts on either side (wg_slot). One 256-thread block
-// per 128 x 128 output tile: waves 0-1 stage G, waves 2-3 stage X, every wave multiplies a 64 x 64
-// quarter (2 x 2 blocks of mfma_f32_32x32x16_bf16, X as the A operand so that a lane's
-// accumulators are 4 consecutive output columns).
-// Two LDS stages and two register stages (below).
-// Blocks are numbered so that the tiles of one expert run on one XCD (workgroups go to the 8 XCDs
-// round robin) and share its L2.
-__device__ __forceinline__ void transpose8x8(const u32x4_t (&a)[8], u32x4_t (&b)[8]) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t lo = a[2 * q][j >> 1], hi = a[2 * q + 1][j >> 1];
-      b[j][q] = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-    }
-}
-
-// G, X and perm are not declared __restrict__: loads from restrict read-only arguments count as
-// unclobbered and may be moved across the workgroup barriers, which undoes the slice pipeline.
-__global__ __launch_bounds__(256) void expert_wgrad_kernel(const uint16_t* G, const uint16_t* X,
-                                                           const int32_t* perm,
-                                                           const int32_t* __restrict__ starts,
-                                                           const int32_t* __restrict__ counts,
-                                                           uint16_t* __restrict__ dW, int64_t P, int M,
-                                                           int N, int k, int tm, int tn) {
-  __shared__ __align__(16) uint8_t lds[2][2][WG_T * WG_PITCH];  // [stage][G, X][column][row]
-  const int nb = gridDim.x, b = blockIdx.x;
-  const int L = (nb & 7) == 0 ? (b & 7) * (nb >> 3) + (b >> 3) : b;
-  const int e = L / (tm * tn), rem = L - e * tm * tn;
-  const int m0 = (rem / tn) * WG_T, n0 = (rem % tn) * WG_T;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // Rows of expert e, kept inside the P sorted rows (P = 0: no rows, counts never read).
-  const int64_t r0 = P > 0 ? starts[e] : 0;
-  const int cnt = P > 0 ? (int)max((int64_t)0, min((int64_t)counts[e], P - r0)) : 0;
-  const int nsl = (cnt + WG_K - 1) / WG_K;
-
-  const int st = tid & 127, cb = st & 15, rb = st >> 4;
-  const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lh = lane >> 5;
-  f32x16_t acc[2][2];
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[a][c][i] = 0.0f;
-  auto compute = [&](int buf) {
-    // Fragment of column 64w + 32i + lr, k-chunk 2s + lh.
-#pragma unroll
-    for (int s = 0; s < WG_K / 16; ++s) {
-      u32x4_t gf[2], xf[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        gf[i] = *reinterpret_cast<const u32x4_t*>(lds[buf][0] + wg_slot(64 * wm + 32 * i + lr, 2 * s + lh));
-        xf[i] = *reinterpret_cast<const u32x4_t*>(lds[buf][1] + wg_slot(64 * wn + 32 * i + lr, 2 * s + lh));
-      }
-#pragma unroll
-      for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi) acc[ni][mi] = mfma32x32x16(xf[ni], gf[mi], acc[ni][mi]);
-    }
-  };
-
-  // Staging role (a compile-time constant inside `run`, so that neither role branches around the
-  // other's loads): an 8-row x 8-column block of G (waves 0-1) or X (waves 2-3) per thread.
-  //
-  // Every global load is issued unconditionally from a clamped in-bounds address (rows past the
-  // expert's count read its last row, columns past the edge column 0) and its result is always
-  // consumed: the zero mask is applied at the transpose. With a fixed number of loads per slice,
-  // the compiler's vmcnt waits count only the loads that are needed (a load under a branch makes
-  // it wait for all of them).
-  //
-  // Pipeline: while slice s is multiplied from LDS, slice s+1 (loaded during the previous slice)
-  // waits in registers for its transpose into the other LDS stage, slice s+2's loads are in flight
-  // and slice s+3's gathered row indices are being fetched: a load has two slices of MFMA work to
-  // arrive in. Register sets alternate between even and odd slices; slices past the last one are
-  // masked to zero (the last two steps write such a slice into the stage that is no longer read).
-  // perm[r] / k as a multiply-high by ceil(2^32 / k): exact for every pair index below 2^29
-  // (the error term p * (ceil(2^32/k) * k - 2^32) / (k 2^32) stays below 1/k), and pair indices
-  // are below 2^25 here (P * 64 < 2^31).
-  const uint32_t kmagic = k > 1 ? (uint32_t)((0x100000000ull + (uint32_t)k - 1) / (uint32_t)k) : 0u;
-  auto run = [&](auto role) {
-    constexpr bool XR = decltype(role)::value;
-    const int col = (XR ? n0 : m0) + 8 * cb;
-    const bool col_ok = col < (XR ? N : M);
-    const int col_ld = col_ok ? col : 0;
-    const uint16_t* const base = XR ? X : G;
-    const int ld = XR ? N : M;
-    auto rows_of = [&](int sl, int (&src)[8]) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int rr = min(sl * WG_K + 8 * rb + i, cnt - 1);
-        if (XR) {
-          const uint32_t pr = (uint32_t)perm[r0 + rr];
-          src[i] = (int)(k > 1 ? __umulhi(pr, kmagic) : pr);
-        } else {
-          src[i] = (int)r0 + rr;
-        }
-      }
-    };
-    auto load = [&](const int (&src)[8], u32x4_t (&v)[8]) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = ld16(base + (int64_t)src[i] * ld + col_ld);
-    };
-    auto store = [&](int buf, int sl, const u32x4_t (&v)[8]) {
-      u32x4_t w[8], t[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        w[i] = col_ok && sl * WG_K + 8 * rb + i < cnt ? v[i] : (u32x4_t){0u, 0u, 0u, 0u};
-      transpose8x8(w, t);
-      // Columns 8cb + j, row chunk rb.
-      uint8_t* dst = lds[buf][XR ? 1 : 0];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4_t*>(dst + wg_slot(8 * cb + j, rb)) = t[j];
-    };
-    u32x4_t va[8], vb[8];
-    int pa[8], pb[8];
-    auto step = [&](int s, u32x4_t (&r1)[8], u32x4_t (&r2)[8], int (&p1)[8], int (&p2)[8]) {
-      rows_of(s + 3, p2);
-      load(p1, r2);
-      compute(s & 1);
-      store((s + 1) & 1, s + 1, r1);
-      __syncthreads();
-    };
-    if (nsl == 0) return;
-    // The prologue leaves the same loads outstanding, in the same order, as the loop's back edge
-    // (slice 2's row indices, then slice 1's data), and the loop always runs whole pairs of steps
-    // (an odd count multiplies one zero slice more), so the waits at the loop head stay partial.
-    rows_of(0, pa);
-    rows_of(1, pb);
-    load(pa, va);
-    rows_of(2, pa);
-    load(pb, vb);
-    store(0, 0, va);
-    __syncthreads();
-    for (int s = 0; s < nsl; s += 2) {
-      step(s, vb, va, pa, pb);
-      step(s + 1, va, vb, pb, pa);
-    }
-  };
-  if (wave >= 2) run(std::true_type{});
-  else run(std::false_type{});
-
-  // acc[ni][mi][i] of lane l: column n = 64wn + 32ni + 8(i/4) + 4(l/32) + i%4, row m = 64wm + 32mi + l%32.
-  uint16_t* const out = dW + (int64_t)e * M * N;
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-    const int m = m0 + 64 * wm + 32 * mi + lr;
-    if (m >= M) continue;
-#pragma unroll
-    for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const int n = n0 + 64 * wn + 32 * ni + 8 * gq + 4 * lh;
-        if (n < N)
-          *reinterpret_cast<uint2*>(out + (int64_t)m * N + n) =
-              make_uint2(pack_bf16x2(acc[ni][mi][4 * gq], acc[ni][mi][4 * gq + 1]),
-                         pack_bf16x2(acc[ni][mi][4 * gq + 2], acc[ni][mi][4 * gq + 3]));
-      }
-  }
-}
-
-// Sorted-row form of the weight gradients with asynchronous staging: both operands' rows are in
-// sorted order (X = H, or the tokens already gathered into sorted order), so 32-row slices of
-// G[:, m0 .. m0+127] and X[:, n0 .. n0+127] are copied global -> LDS by global_load_lds_dwordx4 into
-// a WD_NS-slot ring (WD_NS - 1 slices in flight, no register staging) and the MFMA fragments are read
+// 32-row slices of G[:, m0 .. m0+127] and X[:, n0 .. n0+255] are copied global -> LDS by
+// global_load_lds_dwordx4 into a WD_NS-slot ring (WD_NS - 1 slices in flight, no register
+// staging; gathered X rows through an LDS ring of row indices) and the MFMA fragments are read
 // straight from the row-major slices with the gfx950 transposing LDS read ds_read_b64_tr_b16:
 // within each 16-lane group, component j of lane i is element i % 4 of the 8 bytes that lane
 // 4j + i/4 addresses, so lanes addressing rows k0 + s/4, columns c0 + 4 (s % 4) receive rows
 // k0 .. k0+3 of column c0 + i; two such reads are one 8-row fragment. Slices are row-major, 256
 // or 512 bytes per row (128 or 256 columns), 16-byte chunk c of row r at chunk c ^ 4 (r % 4): the
-// 32 lanes of a half-wave read 4 rows x 64 bytes and cover the 64 banks once. Rows past the expert's count are
-// copied from its last row (in bounds) and zeroed in the fragments of the last slice; columns past
+// 32 lanes of a half-wave read 4 rows x 64 bytes and cover the 64 banks once. Rows past the
+// expert's count are copied from its last row (in bounds) and zeroed in the fragments of the last
+// slice; columns past
 // M or N are copied from column 0 and never stored. One 256-thread block per 128 (G) x 256 (X)
 // tile; each wave multiplies 64 x 128 (2 x 4 blocks of mfma_f32_32x32x16_bf16, X as the A operand).
 constexpr int WD_BK = 32;   // rows per slice
@@ -365,6 +186,10 @@ __device__ __forceinline__ void wd_dma16(const void* gsrc, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(gsrc)
                : "memory", "m0");
 }
+__device__ __forceinline__ void wd_dma4(const void* gsrc, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 1\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(gsrc)
+               : "memory", "m0");
+}
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint2 wd_read_tr(const uint8_t* lds) {
   const i16x4_t v =
@@ -378,13 +203,21 @@ __device__ __forceinline__ int wd_off(int row, int col) {
   return row * PITCH + 16 * ((col >> 3) ^ (4 * (row & 3))) + 2 * (col & 7);
 }
 
+// GX: X rows gathered, X[perm[r] / k] (X = the tokens [T, N]). Each wave copies the 32 row
+// indices of slice t into its own LDS ring (global_load_lds_dword, issued two steps before slice
+// t's data copies, which read them), so the pipeline holds no compiler-visible loads: every step
+// issues the same 7 asynchronous copies per wave (6 data + 1 index) and waits with one constant.
+template <bool GX>
 __global__ __launch_bounds__(256) void expert_wgrad_dma_kernel(const uint16_t* G, const uint16_t* X,
+                                                               const int32_t* perm,
                                                                const int32_t* __restrict__ starts,
                                                                const int32_t* __restrict__ counts,
                                                                uint16_t* __restrict__ dW, int64_t P, int M,
-                                                               int N, int tm, int tn) {
+                                                               int N, int k, int tm, int tn) {
+  static_assert(!GX || WD_NS == 3, "the index lead below is written for a 3-slot ring");
   __shared__ __align__(16) uint8_t ring_g[WD_NS][WD_BK * 2 * WG_T];   // [slot][row][128 columns]
   __shared__ __align__(16) uint8_t ring_x[WD_NS][WD_BK * 2 * WD_TN];  // [slot][row][256 columns]
+  __shared__ __align__(16) int32_t ring_i[GX ? 4 : 1][GX ? 3 : 1][64];  // [wave][slot][row (+32 copies)]
   const int nb = gridDim.x, b = blockIdx.x;
   const int L = (nb & 7) == 0 ? (b & 7) * (nb >> 3) + (b >> 3) : b;
   const int e = L / (tm * tn), rem = L - e * tm * tn;
@@ -408,7 +241,13 @@ __global__ __launch_bounds__(256) void expert_wgrad_dma_kernel(const uint16_t* G
     // Copies: wave w fills slice rows 8w .. 8w+7 of both operands: G in 2 instructions of 4
     // 256-byte rows (lane l: row 4q + l/16, position l % 16), X in 4 instructions of 2 512-byte
     // rows (lane l: row 2q + l/32, position l % 32); position p of row r holds chunk p ^ 4 (r % 4).
-    auto issue = [&](int sl) {
+    // perm[r] / k as a multiply-high by ceil(2^32 / k) (exact for pair indices below 2^29).
+    const uint32_t kmagic = k > 1 ? (uint32_t)((0x100000000ull + (uint32_t)k - 1) / (uint32_t)k) : 0u;
+    auto issue_idx = [&](int sl) {  // slice sl's 32 row indices (lanes 32-63 repeat them)
+      const int64_t r = r0 + min(sl * WD_BK + (lane & 31), cnt - 1);
+      wd_dma4(perm + r, wd_lds_addr(&ring_i[wave][sl % 3][0]));
+    };
+    auto issue = [&](int sl, const int (&xrow)[4]) {
       const int slot = sl % WD_NS;
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
@@ -421,20 +260,45 @@ __global__ __launch_bounds__(256) void expert_wgrad_dma_kernel(const uint16_t* G
       for (int q = 0; q < 4; ++q) {
         const int row = 8 * wave + 2 * q + (lane >> 5);
         const int col = n0 + 8 * ((lane & 31) ^ (4 * (row & 3)));
-        const int64_t grow = r0 + min(sl * WD_BK + row, cnt - 1);
+        const int64_t grow = GX ? (int64_t)xrow[q] : r0 + min(sl * WD_BK + row, cnt - 1);
         wd_dma16(X + grow * N + (col < N ? col : 0), wd_lds_addr(&ring_x[slot][(8 * wave + 2 * q) * 2 * WD_TN]));
       }
     };
+    // This wave's X source rows of slice sl (rows 8 wave + 2q + lane / 32): from memory for the
+    // first two slices (nothing is in flight yet), then from the index ring.
+    auto xrows_direct = [&](int sl, int (&xr)[4]) {
 #pragma unroll
-    for (int sl = 0; sl < WD_NS - 1; ++sl) issue(sl);
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t pr = (uint32_t)perm[r0 + min(sl * WD_BK + 8 * wave + 2 * q + (lane >> 5), cnt - 1)];
+        xr[q] = (int)(k > 1 ? __umulhi(pr, kmagic) : pr);
+      }
+    };
+    auto xrows_ring = [&](int sl, int (&xr)[4]) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t pr = (uint32_t)ring_i[wave][sl % 3][8 * wave + 2 * q + (lane >> 5)];
+        xr[q] = (int)(k > 1 ? __umulhi(pr, kmagic) : pr);
+      }
+    };
+    int xr[4] = {0, 0, 0, 0};
+    // Prologue: the copies of steps -2 and -1 (data of slices 0 and 1, indices of slices 2 and 3).
+#pragma unroll
+    for (int sl = 0; sl < WD_NS - 1; ++sl) {
+      if (GX) xrows_direct(sl, xr);
+      issue(sl, xr);
+      if (GX) issue_idx(sl + WD_NS - 1);
+    }
     const int g = lane >> 4, gi = lane & 15;
     for (int s = 0; s < nsl; ++s) {
-      // This wave's copies of slice s are done when at most those of slices s+1 .. s+NS-2 (6
-      // each) are outstanding; the barrier makes that true of every wave and orders the LDS reads
-      // of slice s-1 (drained by the lgkmcnt wait) before its slot is refilled with slice s+NS-1.
+      // This wave's copies issued up to step s-2 (data of slice s, and with GX the indices of
+      // slice s+2) are done when at most those of step s-1 are outstanding; the barrier makes that
+      // true of every wave and orders the LDS reads of slice s-1 (drained by the lgkmcnt wait)
+      // before its slot is refilled with slice s+NS-1.
       __builtin_amdgcn_s_waitcnt(0xC07F);
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(6 * (WD_NS - 2)) : "memory");
-      issue(s + WD_NS - 1);
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((GX ? 7 : 6) * (WD_NS - 2)) : "memory");
+      if (GX) xrows_ring(s + WD_NS - 1, xr);
+      issue(s + WD_NS - 1, xr);
+      if (GX) issue_idx(s + 2 * (WD_NS - 1));
       const uint8_t* sg = ring_g[s % WD_NS];
       const uint8_t* sx = ring_x[s % WD_NS];
       const int left = cnt - s * WD_BK;  // rows of this slice that exist (mask when < 32)
@@ -495,6 +359,17 @@ __global__ __launch_bounds__(256) void expert_wgrad_dma_kernel(const uint16_t* G
                          pack_bf16x2(acc[ni][mi][4 * gq + 2], acc[ni][mi][4 * gq + 3]));
       }
   }
+}
+
+// 8 x 8 transpose of 16-bit elements held as 8 rows of 16 bytes: b[j] = column j of a.
+__device__ __forceinline__ void transpose8x8(const u32x4_t (&a)[8], u32x4_t (&b)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t lo = a[2 * q][j >> 1], hi = a[2 * q + 1][j >> 1];
+      b[j][q] = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+    }
 }
 
 // dst[e] = src[e]^T for bf16 matrices [E, R, C] -> [E, C, R] (the expert weights as the K-major
@@ -573,14 +448,14 @@ hipError_t launch_expert_wgrad(const uint16_t* G, const uint16_t* X, const int32
   const int tm = (M + WG_T - 1) / WG_T, tn = (N + WG_T - 1) / WG_T;
   const int64_t nb = (int64_t)E * tm * tn;
   if (nb == 0) return hipSuccess;
-  if (perm == nullptr) {
-    const int tnd = (N + WD_TN - 1) / WD_TN;
-    hipLaunchKernelGGL(expert_wgrad_dma_kernel, dim3((unsigned)((int64_t)E * tm * tnd)), dim3(256), 0, stream, G, X,
-                       starts, counts, dW, P, M, N, tm, tnd);
-    return hipGetLastError();
-  }
-  hipLaunchKernelGGL(expert_wgrad_kernel, dim3((unsigned)nb), dim3(256), 0, stream, G, X, perm, starts, counts, dW, P,
-                     M, N, k, tm, tn);
+  const int tnd = (N + WD_TN - 1) / WD_TN;
+  const dim3 grid((unsigned)((int64_t)E * tm * tnd));
+  if (perm == nullptr)
+    hipLaunchKernelGGL(expert_wgrad_dma_kernel<false>, grid, dim3(256), 0, stream, G, X, perm, starts, counts, dW, P,
+                       M, N, k, tm, tnd);
+  else
+    hipLaunchKernelGGL(expert_wgrad_dma_kernel<true>, grid, dim3(256), 0, stream, G, X, perm, starts, counts, dW, P,
+                       M, N, k, tm, tnd);
   return hipGetLastError();
 }
 

@@ -14,7 +14,7 @@ the backward runs, with Y' = dout[t] * w[p] (the routed raw rows' gradient) in s
   dx_p    = dGU . gate_up_proj[e]                 q38moe_down on gate_up_proj^T [E, h, 2I]
   dx[t]   = sum_j dx_p[inv[t*k+j]]                q38moe_combine with unit weights
   d down_proj[e]    = Y'_e^T . H_e                q38moe_expert_wgrad (sorted rows)
-  d gate_up_proj[e] = dGU_e^T . x_e               q38moe_gather_rows (x in sorted order), q38moe_expert_wgrad
+  d gate_up_proj[e] = dGU_e^T . x_e               q38moe_expert_wgrad (x rows gathered through perm)
 
 Expert row ranges stay on the device (starts/counts of the permutation): the backward makes no
 host synchronisation.
@@ -65,10 +65,7 @@ class HipExperts(torch.autograd.Function):
                 GU = ops.gather_gemm(x, perm, w_gate_up, tiles, tcount, k)
                 dGU = ops.swiglu_backward(dH, GU)
                 if need_gu:
-                    # x rows in sorted order first: the sorted form stages both operands with
-                    # asynchronous copies, which beats gathering inside the product.
-                    xs = ops.gather_rows(x, perm, starts, counts, k)
-                    dgu_w = ops.expert_wgrad(dGU, xs, starts, counts, k)
+                    dgu_w = ops.expert_wgrad(dGU, x, starts, counts, k, perm=perm)
                 if need_x:
                     dxp = ops.down(dGU, ops.transpose_experts(w_gate_up), tiles, tcount, T, k)
                     dx = ops.combine(dxp, inv, torch.ones_like(w), E, idx=idx)
