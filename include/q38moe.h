@@ -51,10 +51,16 @@ const char* q38moe_last_error(void);
  * Router, R1-R2: replaces Qwen3_8MoeTopKRouter.forward (modeling:805-813).
  *   logits[t,e] = bf16(sum_c x[t,c] * w_router[e,c])                         (F.linear, :807)
  *   probs = softmax(float(logits) (+ logit_bias), fp32)                       (:808)
+ *     -- computed bit for bit as torch's CPU softmax (AVX512 kernel) computes it: SLEEF expf_u10
+ *        of x - max, the 16-lane vector reduction order of the sum, multiply by 1/sum.
  *   (v, topk_idx) = torch CPU topk(probs, k, largest, sorted)                 (:809)
- *     -- tie order reproduces ATen/native/TopKImpl.h (std::nth_element + std::sort with a
- *        value-only comparator, NaN first; std::partial_sort when k*64 <= E).
+ *     -- selection on those probabilities with the tie order of ATen/native/TopKImpl.h
+ *        (std::nth_element + std::sort with a value-only comparator, NaN first;
+ *        std::partial_sort when k*64 <= E), so distinct logits whose probabilities round to
+ *        one fp32 value tie exactly as on the CPU.
  *   topk_w = bf16(v / sum(v))                                                 (:810-811)
+ *     -- sum(v) in torch's CPU row-sum order (4-way interleaved for k = 5..7, else left to
+ *        right), then IEEE division: weights bit-identical to the CPU's.
  * Optional extras:
  *   w_shared_gate [h] (NULL to skip): shared_gate_logit[t] = bf16(x[t] . w_shared_gate), the
  *     shared_expert_gate projection of modeling:831, computed from the same pass over x.

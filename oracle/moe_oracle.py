@@ -8,6 +8,9 @@ modeling_qwen3_8_moe.py, "inference" = q38/inference.py):
 
   topk_cpu        torch CPU top-k tie order, ATen/native/TopKImpl.h:45-76, via the C restatement
                   in q38_oracle.cpp (liboracle.so) that calls libstdc++'s nth_element/sort.
+  softmax_torch_order  torch's CPU fp32 softmax restated operation by operation (C); the router
+                  kernel computes its probabilities the same way. router() itself calls
+                  torch.softmax, the reference's op.
   permute_cpu     stable counting sort = torch.sort(ids, stable=True) + searchsorted,
                   inference:163-171 (C, q38_oracle.cpp).
   tile_table      the per-expert BM-row blocks of inference:39-50,174-183 in the GEMM's order.
@@ -44,8 +47,8 @@ def build():
     """Compile q38_oracle.cpp with g++ into oracle/_build/liboracle.so."""
     (ORACLE_DIR / "_build").mkdir(exist_ok=True)
     tmp = LIB_PATH.with_suffix(".so.tmp")
-    subprocess.run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC", str(ORACLE_DIR / "q38_oracle.cpp"), "-o",
-                    str(tmp)], check=True)
+    subprocess.run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", "-shared", "-fPIC",
+                    str(ORACLE_DIR / "q38_oracle.cpp"), "-o", str(tmp)], check=True)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 
@@ -65,6 +68,8 @@ def _load():
         lib.oracle_permute.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p,
                                        ctypes.c_void_p, ctypes.c_void_p]
         lib.oracle_permute.restype = None
+        lib.oracle_softmax_rows.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
+        lib.oracle_softmax_rows.restype = None
         _lib = lib
     return _lib
 
@@ -77,6 +82,16 @@ def topk_cpu(values, k):
     oi = np.empty((R, k), np.int64)
     _load().oracle_topk(v.ctypes.data, R, n, k, ov.ctypes.data, oi.ctypes.data)
     return ov, oi
+
+
+def softmax_torch_order(z):
+    """fp32 softmax over the last dimension restated as torch's CPU kernel computes it
+    (q38_oracle.cpp oracle_softmax_rows); pinned bit for bit against torch.softmax."""
+    v = np.ascontiguousarray(np.asarray(z, dtype=np.float32))
+    R, n = v.shape
+    out = np.empty_like(v)
+    _load().oracle_softmax_rows(v.ctypes.data, R, n, out.ctypes.data)
+    return out
 
 
 def permute_cpu(ids, E):

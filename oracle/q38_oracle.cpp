@@ -10,13 +10,85 @@
 //   The libstdc++ algorithms are the specification, so they are called, not re-implemented.
 // oracle_permute: stable counting sort of pair ids, the closed form of
 //   torch.sort(ids, stable=True) + searchsorted in q38/inference.py:163-171.
+// oracle_softmax_rows: torch 2.10's CPU softmax over the last dimension in fp32 (the AVX512
+//   kernel that torch.softmax(z, dim=-1) dispatches to on this image), restated from its measured
+//   behaviour: the row max; e_i = SLEEF's expf_u10 (the published xexpf algorithm, with the fused
+//   multiply-adds of its vector form) of x_i - max; the sum in the order of a 16-lane vector
+//   reduction (accumulator l adds x_l, x_{l+16}, ... in turn, then lanes fold l^8, l^4, l^2, l^1;
+//   rows narrower than 16 sum left to right); p_i = e_i * (1 / sum). tests/test_oracle.py checks
+//   it bit for bit against torch.softmax; the router kernel computes its probabilities this way.
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstring>
 #include <utility>
 #include <vector>
 
+namespace {
+
+float sleef_expf_u10(float d) {
+  const float qf = std::rint(d * 1.442695040888963407359924681001892137426645954152985934135449406931f);
+  const int q = (int)qf;
+  float s = std::fma(qf, -0.693145751953125f, d);
+  s = std::fma(qf, -1.428606765330187045e-06f, s);
+  float u = 0.000198527617612853646278381f;
+  u = std::fma(u, s, 0.00139304355252534151077271f);
+  u = std::fma(u, s, 0.00833336077630519866943359f);
+  u = std::fma(u, s, 0.0416664853692054748535156f);
+  u = std::fma(u, s, 0.166666671633720397949219f);
+  u = std::fma(u, s, 0.5f);
+  const float s2 = s * s;
+  u = 1.0f + std::fma(s2, u, s);
+  const int q1 = q >> 1, q2 = q - q1;
+  uint32_t b1 = (uint32_t)(q1 + 127) << 23, b2 = (uint32_t)(q2 + 127) << 23;
+  float f1, f2;
+  std::memcpy(&f1, &b1, 4);
+  std::memcpy(&f2, &b2, 4);
+  u = u * f1;
+  u = u * f2;
+  if (d < -104.0f) u = 0.0f;
+  if (d > 100.0f) u = INFINITY;
+  return std::isnan(d) ? d : u;
+}
+
+// max propagating NaN, as the vector maximum does
+float max_nan(float a, float b) { return (std::isnan(a) || std::isnan(b)) ? NAN : (a > b ? a : b); }
+
+// reduction in the order of a 16-lane vector reduce: accumulators, then folds l^8, l^4, l^2, l^1
+template <typename Op>
+float reduce16(const float* x, int64_t n, Op op) {
+  if (n < 16) {
+    float a = x[0];
+    for (int64_t i = 1; i < n; ++i) a = op(a, x[i]);
+    return a;
+  }
+  float acc[16];
+  for (int l = 0; l < 16; ++l) acc[l] = x[l];
+  for (int64_t d = 16; d < n; d += 16)
+    for (int l = 0; l < 16 && d + l < n; ++l) acc[l] = op(acc[l], x[d + l]);
+  for (int s = 8; s >= 1; s >>= 1) {
+    float nxt[16];
+    for (int l = 0; l < 16; ++l) nxt[l] = op(acc[l], acc[l ^ s]);
+    std::memcpy(acc, nxt, sizeof(acc));
+  }
+  return acc[0];
+}
+
+}  // namespace
+
 extern "C" {
+
+void oracle_softmax_rows(const float* x, int64_t rows, int64_t n, float* out) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * n;
+    float* yr = out + r * n;
+    const float m = reduce16(xr, n, max_nan);
+    for (int64_t i = 0; i < n; ++i) yr[i] = sleef_expf_u10(xr[i] - m);
+    const float s = reduce16(yr, n, [](float a, float b) { return a + b; });
+    const float rs = 1.0f / s;
+    for (int64_t i = 0; i < n; ++i) yr[i] = yr[i] * rs;
+  }
+}
 
 void oracle_topk(const float* values, int64_t rows, int64_t n, int64_t k, float* out_values,
                  int64_t* out_indices) {

@@ -10,15 +10,70 @@
 // match the CPU library bit for bit. Rows whose k+1 largest values are all distinct have a unique
 // answer and take a fast path (k+1 wave arg-max rounds).
 //
-// Selection compares the bf16 logits (plus the optional fp32 bias) rather than the fp32
-// probabilities: softmax is monotone, so the order is the same whenever the CPU softmax keeps
-// distinct logits distinct; this keeps indices independent of the exp() implementation.
+// Selection compares the fp32 probabilities themselves, computed bit for bit as torch's CPU
+// softmax computes them (torch_softmax_* below), so rows whose distinct logits collapse to equal
+// probabilities (x - max rounding to one value, or exp / the 1/sum scaling merging neighbours) tie
+// exactly where the CPU's do.
 #include "q38moe_common.h"
 #include "q38moe_kernels.h"
 
 namespace q38 {
 
 constexpr int KMAX = 8;
+
+// ---- torch 2.10 CPU softmax over a row of fp32 values (the AVX512 kernel torch dispatches to),
+// restated operation by operation; verified bit for bit against torch.softmax on the CPU over
+// millions of rows of widths 1..64, wide ranges, +-inf and NaN (tests/test_oracle.py restates it
+// in C and checks it there):
+//   m = max(x); e_i = expf_u10(x_i - m); s = sum of e_i in the order of a 16-lane vector
+//   reduction (lane l accumulates e_l, e_{l+16}, e_{l+32}, e_{l+48} in turn, then the lanes are
+//   folded l ^ 8, l ^ 4, l ^ 2, l ^ 1; rows narrower than 16 sum left to right); p_i = e_i * (1/s).
+// expf_u10 is SLEEF's single-precision u10 exponential (the published xexpf algorithm: round
+// x/ln2 to an integer q, two-part Cody-Waite reduction, degree-6 polynomial, scale by 2^q in two
+// halves; 0 below -104, inf above 100), fused multiply-adds where SLEEF's vector form uses them.
+__device__ __forceinline__ float torch_cpu_expf(float d) {
+#pragma clang fp contract(off)
+  const float qf = __builtin_rintf(d * 1.442695040888963407359924681001892137426645954152985934135449406931f);
+  const int q = (int)qf;
+  float s = __builtin_fmaf(qf, -0.693145751953125f, d);
+  s = __builtin_fmaf(qf, -1.428606765330187045e-06f, s);
+  float u = 0.000198527617612853646278381f;
+  u = __builtin_fmaf(u, s, 0.00139304355252534151077271f);
+  u = __builtin_fmaf(u, s, 0.00833336077630519866943359f);
+  u = __builtin_fmaf(u, s, 0.0416664853692054748535156f);
+  u = __builtin_fmaf(u, s, 0.166666671633720397949219f);
+  u = __builtin_fmaf(u, s, 0.5f);
+  const float s2 = s * s;
+  u = 1.0f + __builtin_fmaf(s2, u, s);
+  const int q1 = q >> 1, q2 = q - q1;
+  u = u * __int_as_float((q1 + 127) << 23);
+  u = u * __int_as_float((q2 + 127) << 23);
+  u = d < -104.0f ? 0.0f : u;
+  u = d > 100.0f ? __builtin_inff() : u;
+  return __builtin_isnan(d) ? d : u;
+}
+
+// torch's CPU sum over the last dimension of a contiguous [rows, k] fp32 tensor (the top-k
+// renormalisation, modeling:810), as measured bit for bit against torch.sum on the CPU: k in 5..7
+// take the 4-way interleaved row sum ((v0 + v4 [+ v5 [+ v6]]) + v1 + v2 + v3, left to right);
+// every other k <= 8 sums left to right.
+template <int K>
+__device__ __forceinline__ float torch_topk_sum(const float* v) {
+  float t;
+  if constexpr (K >= 5 && K <= 7) {
+    t = v[0] + v[4];
+#pragma unroll
+    for (int r = 5; r < K; ++r) t = t + v[r];
+    t = t + v[1];
+    t = t + v[2];
+    t = t + v[3];
+  } else {
+    t = v[0];
+#pragma unroll
+    for (int r = 1; r < K; ++r) t = t + v[r];
+  }
+  return t;
+}
 
 __device__ __forceinline__ bool cmp_gt(float a, float b) {
   return (__builtin_isnan(a) && !__builtin_isnan(b)) || (a > b);
@@ -47,9 +102,6 @@ __device__ __forceinline__ float wave_reduce(float v, Op op) {
 }
 __device__ __forceinline__ float wave_max(float v) {
   return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
-}
-__device__ __forceinline__ float wave_sum(float v) {
-  return wave_reduce(v, [](float a, float b) { return a + b; });
 }
 
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -258,12 +310,14 @@ __device__ void nth_element_then_sort(float& qv, int& qi, int lane, int n, int k
   insertion_sort_slots(qv, qi, lane, 0, k - 1);
 }
 
-// Route one token held by the calling wave. z: selection value of expert `lane` (lanes >= E
-// ignored). Lane r < k receives the r-th selected expert and its renormalised weight.
-__device__ void route_token(float z, int lane, int E, int k, bool known_tie, int& out_idx, float& out_w,
-                            float* sv, int* si) {
+// Route one token held by the calling wave. z: selection input of expert `lane` (bf16 logit plus
+// the optional bias; lanes >= E ignored). The fp32 probabilities follow torch's CPU softmax bit
+// for bit, and the selection replays libstdc++ on them. Lane r < K receives the r-th selected
+// expert and its renormalised weight.
+template <int K>
+__device__ void route_token(float z, int lane, int E, int& out_idx, float& out_w, float* sv, int* si) {
   const bool valid = lane < E;
-  z = z + 0.0f;  // -0 -> +0: the comparator treats them as equal
+  z = z + 0.0f;  // -0 -> +0 (the CPU adds the bias or a zero the same way; exp(+-0) is 1 either way)
   const bool has_nan = ballot64(valid && __builtin_isnan(z)) != 0ull;
   const float m = wave_max(valid ? z : -INFINITY);
   const bool all_nan = has_nan || !__builtin_isfinite(m);  // softmax is NaN everywhere then
@@ -271,57 +325,48 @@ __device__ void route_token(float z, int lane, int E, int k, bool known_tie, int
   if (all_nan) {
     p = __builtin_nanf("");
   } else {
-    const float ex = valid ? expf(z - m) : 0.0f;
-    const float s = wave_sum(ex);
-    p = ex * (1.0f / s);
+    const float ex = valid ? torch_cpu_expf(z - m) : 0.0f;
+    float sum;
+    if (E >= 16) {
+      // Lane l < 16 accumulates experts l, l+16, l+32, l+48 (absent ones add +0, exactly), then
+      // the 16 partial sums fold l ^ 8, l ^ 4, l ^ 2, l ^ 1.
+      float acc = ex;
+      acc = acc + __shfl(ex, (lane + 16) & 63);
+      acc = acc + __shfl(ex, (lane + 32) & 63);
+      acc = acc + __shfl(ex, (lane + 48) & 63);
+      acc = acc + __shfl_xor(acc, 8);
+      acc = acc + __shfl_xor(acc, 4);
+      acc = acc + __shfl_xor(acc, 2);
+      acc = acc + __shfl_xor(acc, 1);
+      sum = lane_f(acc, 0);
+    } else {
+      sum = lane_f(ex, 0);
+      for (int e = 1; e < E; ++e) sum = sum + lane_f(ex, e);
+    }
+    p = ex * (1.0f / sum);
   }
-  const float sel = all_nan ? __builtin_nanf("") : z;
-  float qv = sel;
+  float qv = valid ? p : -INFINITY;
   int qi = lane;
 
-  if (k * 64 <= E) {
-    // std::partial_sort path (k == 1, E == 64): first slot whose value is cmp-greater than all
+  if (K * 64 <= E) {
+    // std::partial_sort path (K == 1, E == 64): first slot whose value is cmp-greater than all
     // before it = lowest-index maximum (slot 0 when every value is NaN).
     int best = 0;
     if (!all_nan) {
-      const uint64_t key = valid ? ((uint64_t)order_key(sel) << 32) | (uint32_t)(63 - lane) : 0ull;
+      const uint64_t key = valid ? ((uint64_t)order_key(qv) << 32) | (uint32_t)(63 - lane) : 0ull;
       best = 63 - (int)(uint32_t)wave_max_u64(key);
     }
     qi = best;
   } else {
-    bool tie = all_nan || known_tie;
-    if (!tie) {
-      const int rounds = min(k + 1, E);
-      uint64_t key = valid ? ((uint64_t)order_key(sel) << 32) | (uint32_t)(63 - lane) : 0ull;
-      uint32_t prev_key = 0;
-      int top_lane[KMAX];
-#pragma unroll
-      for (int r = 0; r < KMAX + 1; ++r) {
-        if (r < rounds) {
-          const uint64_t best = wave_max_u64(key);
-          const int bl = 63 - (int)(uint32_t)best;
-          const uint32_t bk = (uint32_t)(best >> 32);
-          if (r > 0 && bk == prev_key) tie = true;
-          prev_key = bk;
-          if (r < KMAX) top_lane[r] = bl;
-          if (lane == bl) key = 0ull;
-        }
-      }
-      if (!tie) {
-#pragma unroll
-        for (int r = 0; r < KMAX; ++r) {
-          if (lane == r) qi = top_lane[r];
-        }
-      }
-    }
-    if (tie) nth_element_then_sort(qv, qi, lane, E, k, sv, si);
+    nth_element_then_sort(qv, qi, lane, E, K, sv, si);
   }
-  // Renormalise over the selected probabilities, summed in selection order.
+  // Renormalise over the selected probabilities with torch's row-sum order, then divide.
   const float pr = __shfl(p, qi & 63);
-  float s = 0.0f;
-  for (int r = 0; r < k; ++r) s += lane_f(pr, r);
+  float v[K];
+#pragma unroll
+  for (int r = 0; r < K; ++r) v[r] = lane_f(pr, r);
   out_idx = qi;
-  out_w = pr / s;
+  out_w = pr / torch_topk_sum<K>(v);
 }
 
 constexpr int ROUTE_TOKENS = 64;   // per block: 4 MFMA waves x 16 tokens
@@ -401,22 +446,25 @@ __device__ __forceinline__ void merge_round(float (&v)[NP], int (&id)[NP], int& 
 }
 
 // Per-token selection by a group of SEL_LANES lanes (lane s of the group holds experts s,
-// s + SEL_LANES, ...). Each lane sorts its 8 values; the groups' sorted lists of NP >= KP1 are
-// merged by xor-shuffle rounds, each keeping the NP largest of two lists (elementwise max of one
-// list and the other reversed is a bitonic sequence holding them) and re-sorting them with a
-// bitonic merge. Equal values are kept as often as they occur, so duplicates among the k+1
-// largest are seen. Returns false when the k+1 largest values are not all distinct (or the row
-// has NaN / non-finite max); such tokens need the libstdc++ replay. Every lane of the group
-// returns the same answer.
+// s + SEL_LANES, ...). The group computes the row's fp32 probabilities as torch's CPU softmax does
+// (the 16 partial sums of its vector reduction are lanes s and s + 8 of the two interleaved
+// halves of each lane's experts, folded l ^ 8 locally, then across lanes ^ 4, ^ 2, ^ 1). Each lane
+// sorts its 8 probabilities; the groups' sorted lists of NP >= KP1 are merged by xor-shuffle rounds,
+// each keeping the NP largest of two lists (elementwise max of one list and the other reversed is a
+// bitonic sequence holding them) and re-sorting them with a bitonic merge. Equal values are kept as
+// often as they occur, so duplicates among the k+1 largest are seen. Returns false when the k+1
+// largest probabilities are not all distinct (or the row has a NaN / non-finite max); such tokens
+// need the libstdc++ replay. Every lane of the group returns the same answer.
 template <int KP1>
-__device__ __forceinline__ bool group_select(const float* row, const float* bias, int E, int k, int s,
+__device__ __forceinline__ bool group_select(const float* row, const float* bias, int E, int s,
                                              int* out_idx, float* out_w) {
+  constexpr int K = KP1 - 1;
   constexpr int PER = 64 / SEL_LANES;  // 8 values per lane
   constexpr int NP = KP1 <= 8 ? 8 : 16;
-  float v[NP];
-  int id[NP];
+  static_assert(SEL_LANES == 8, "the reduction and merge rounds below are for 8 lanes per token");
   float z[PER];
   int nan = 0;
+  float mx = -INFINITY;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int e = s + SEL_LANES * j;
@@ -424,14 +472,48 @@ __device__ __forceinline__ bool group_select(const float* row, const float* bias
     if (e < E) {
       z[j] = row[e] + (bias != nullptr ? bias[e] : 0.0f) + 0.0f;
       nan |= __builtin_isnan(z[j]);
+      mx = fmaxf(mx, z[j]);
     }
   }
+  mx = fmaxf(mx, xor_lanes_f<1>(mx));
+  mx = fmaxf(mx, xor_lanes_f<2>(mx));
+  mx = fmaxf(mx, xor_lanes_f<4>(mx));
+  nan |= xor_lanes<1>(nan);
+  nan |= xor_lanes<2>(nan);
+  nan |= xor_lanes<4>(nan);
+  if (nan || !__builtin_isfinite(mx)) return false;
+  float ex[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) ex[j] = s + SEL_LANES * j < E ? torch_cpu_expf(z[j] - mx) : 0.0f;
+  float sum;
+  if (E >= 16) {
+    float a = ex[0], b = ex[1];
+#pragma unroll
+    for (int j = 2; j < PER; j += 2) {
+      a = a + ex[j];
+      b = b + ex[j + 1];
+    }
+    sum = a + b;
+    sum = sum + xor_lanes_f<4>(sum);
+    sum = sum + xor_lanes_f<2>(sum);
+    sum = sum + xor_lanes_f<1>(sum);
+  } else {
+    // Rows narrower than one vector: left to right over the experts.
+    sum = 0.0f;
+    for (int e = 0; e < E; ++e) {
+      const float ee = torch_cpu_expf(row[e] + (bias != nullptr ? bias[e] : 0.0f) + 0.0f - mx);
+      sum = e == 0 ? ee : sum + ee;
+    }
+  }
+  const float rs = 1.0f / sum;
+  float v[NP];
+  int id[NP];
   {
     float lv[8];
     int li[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      lv[j] = __builtin_isnan(z[j]) ? -INFINITY : z[j];
+      lv[j] = s + SEL_LANES * j < E ? ex[j] * rs : -INFINITY;
       li[j] = s + SEL_LANES * j;
     }
     sort8_desc(lv, li);
@@ -441,39 +523,21 @@ __device__ __forceinline__ bool group_select(const float* row, const float* bias
       id[r] = r < 8 ? li[r & 7] : -1;
     }
   }
-  static_assert(SEL_LANES == 8, "merge rounds below are for 8 lanes per token");
-  merge_round<1>(v, id, nan);
-  merge_round<2>(v, id, nan);
-  merge_round<4>(v, id, nan);
-  const float m = v[0];
-  if (nan || !__builtin_isfinite(m)) return false;
-  const int lim = min(k, E - 1);
+  int dummy = 0;
+  merge_round<1>(v, id, dummy);
+  merge_round<2>(v, id, dummy);
+  merge_round<4>(v, id, dummy);
+  const int lim = min(K, E - 1);
 #pragma unroll
   for (int r = 0; r < KP1 - 1; ++r) {
     if (r < lim && v[r] == v[r + 1]) return false;
-    if (r == k - 1 && v[r] == -INFINITY) return false;  // fewer than k finite values: replay
+    if (r == K - 1 && v[r] == -INFINITY) return false;  // fewer than k experts: replay
   }
-  float sum = 0.0f;
+  const float tot = torch_topk_sum<K>(v);
 #pragma unroll
-  for (int j = 0; j < PER; ++j)
-    if (s + SEL_LANES * j < E) sum += expf(z[j] - m);
-  sum += xor_lanes_f<1>(sum);
-  sum += xor_lanes_f<2>(sum);
-  sum += xor_lanes_f<4>(sum);
-  const float inv = 1.0f / sum;
-  float pr[KP1];
-  float tot = 0.0f;
-#pragma unroll
-  for (int r = 0; r < KP1 - 1; ++r) {
-    pr[r] = expf(v[r] - m) * inv;
-    if (r < k) tot += pr[r];
-  }
-#pragma unroll
-  for (int r = 0; r < KP1 - 1; ++r) {
-    if (r < k) {
-      out_idx[r] = id[r];
-      out_w[r] = pr[r] / tot;
-    }
+  for (int r = 0; r < K; ++r) {
+    out_idx[r] = id[r];
+    out_w[r] = v[r] / tot;
   }
   return true;
 }
@@ -619,8 +683,8 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     if (t < T) {  // uniform over the token's lanes
       int oi[KMAX];
       float ow[KMAX];
-      const bool ok = group_select<KT + 1>(s_logit[tl], bias != nullptr ? s_bias : nullptr, E, k,
-                                     lane % SEL_LANES, oi, ow);
+      const bool ok = group_select<KT + 1>(s_logit[tl], bias != nullptr ? s_bias : nullptr, E,
+                                           lane % SEL_LANES, oi, ow);
       if (lane % SEL_LANES == 0) {
         if (ok) {
           for (int r = 0; r < k; ++r) {
@@ -644,7 +708,7 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     const float z = lane < E ? s_logit[tl][lane] + s_bias[lane] : -INFINITY;
     int oi;
     float ow;
-    route_token(z, lane, E, k, true, oi, ow, s_sv[wave], s_si[wave]);
+    route_token<KT>(z, lane, E, oi, ow, s_sv[wave], s_si[wave]);
     if (lane < k) {
       idx_out[t * k + lane] = oi;
       w_out[t * k + lane] = (uint16_t)f32_to_bf16_rne(ow);

@@ -41,3 +41,40 @@ def assert_gemm_bf16_rounding(actual, x, w, what="logits"):
     err = (a.reshape(exact.shape) - exact).abs()
     bad = err > bound
     assert not bool(bad.any()), f"{what}: {int(bad.sum())} values off; worst excess {float((err - bound).max()):.3e}"
+
+
+def collision_logits(rows, E=64, k=5, seed=0):
+    """bf16 router logits whose distinct values collide in the fp32 softmax: a few logits at 1.0
+    (fewer than k, so the k-th pick falls among the rest), several distinct tiny logits in
+    [2^-34, 2^-25] with random signs (x - max rounds them to one fp32 value, so their
+    probabilities tie although their logits differ), and -3 elsewhere; random positions."""
+    import numpy as np
+    rng = np.random.RandomState(seed)
+    z = np.full((rows, E), -3.0)
+    for r in range(rows):
+        pos = rng.permutation(E)
+        n_big = rng.randint(1, k)
+        n_tiny = rng.randint(2, min(9, E - n_big + 1))
+        z[r, pos[:n_big]] = 1.0
+        tiny = 2.0 ** rng.uniform(-34, -25, n_tiny) * rng.choice([-1.0, 1.0], n_tiny)
+        z[r, pos[n_big:n_big + n_tiny]] = tiny
+    return torch.from_numpy(z).to(torch.bfloat16)
+
+
+def collision_bias(E=64, seed=0):
+    """fp32 logit bias whose neighbouring entries differ by one or two fp32 ulps around -0.3, and
+    bf16 logits drawn from {0, 0.5}: the biased values then differ by a few ulps, so exp() and the
+    1/sum scaling merge neighbours into equal fp32 probabilities."""
+    import numpy as np
+    rng = np.random.RandomState(seed)
+    steps = np.cumsum(rng.randint(1, 3, E)).astype(np.uint32)
+    # -0.3 moved towards zero by `steps` ulps (the bit pattern of a negative float falls)
+    bias = (np.float32(-0.3).view(np.uint32) - steps).view(np.float32)
+    return torch.from_numpy(rng.permutation(bias).astype(np.float32))
+
+
+def collision_bias_logits(rows, E=64, seed=0):
+    """The bf16 logits that go with collision_bias: 0 or 0.5 (one in ten)."""
+    import numpy as np
+    rng = np.random.RandomState(seed + 1)
+    return torch.from_numpy(rng.choice([0.0, 0.5], size=(rows, E), p=[0.9, 0.1])).to(torch.bfloat16)

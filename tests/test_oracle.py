@@ -191,3 +191,57 @@ def test_tile_table_blocks(seed, bm, shared):
     nfull = sum(s == bm for s in sizes)
     assert all(s == bm for s in sizes[:nfull])
     assert all(a >= b for a, b in zip(sizes[nfull:], sizes[nfull + 1:]))
+
+
+def _same_bits(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return (a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))
+
+
+@pytest.mark.parametrize("n", [64, 8, 17, 33, 16, 15, 48, 1])
+def test_softmax_restatement_is_torch_cpu(n):
+    """The router's probabilities follow torch's CPU softmax operation by operation (SLEEF expf_u10,
+    the 16-lane reduction order, multiply by 1/sum): bit for bit on mixed scales, wide ranges,
+    +-inf and NaN rows, and biased rows."""
+    rng = np.random.RandomState(n)
+    z = (rng.randn(6000, n) * rng.choice([0.05, 0.64, 5.0, 40.0], size=(6000, 1))).astype(np.float32)
+    z[:500] = rng.uniform(-120, 0, (500, n))
+    z[500:1000] += (-0.24 * np.log(rng.permutation(n) + 1)).astype(np.float32)
+    z[1000:1100, 0] = np.nan
+    z[1100:1200] = -np.inf
+    z[1200:1300, n // 2] = np.inf
+    got = orc.softmax_torch_order(z)
+    want = torch.softmax(torch.from_numpy(z), dim=-1).numpy()
+    assert _same_bits(got, want).all(), f"{int((~_same_bits(got, want)).sum())} values differ"
+
+
+def test_topk_renorm_sum_order():
+    """torch's CPU sum over the last dimension of a [rows, k] fp32 tensor, the top-k
+    renormalisation (modeling:810): the 4-way interleaved row sum for k in 5..7, left to right for
+    every other k <= 8 (what the router kernel reproduces)."""
+    rng = np.random.RandomState(5)
+    for k in range(1, 9):
+        v = np.sort(rng.rand(20000, k).astype(np.float32) * 0.3, axis=1)[:, ::-1].copy()
+        if 5 <= k <= 7:
+            s = v[:, 0] + v[:, 4]
+            for r in list(range(5, k)) + [1, 2, 3]:
+                s = (s + v[:, r]).astype(np.float32)
+        else:
+            s = v[:, 0].copy()
+            for r in range(1, k):
+                s = (s + v[:, r]).astype(np.float32)
+        t = torch.from_numpy(v)
+        assert _same_bits(s, t.sum(dim=-1).numpy()).all(), k
+        assert _same_bits(v / s[:, None], (t / t.sum(dim=-1, keepdim=True)).numpy()).all(), k
+
+
+def test_collision_rows_need_probabilities():
+    """The collision row classes of the route tests really separate selection on probabilities
+    from selection on logits: distinct logits there give equal fp32 probabilities, and torch's
+    top-k then breaks those ties by introselect position, not by the larger logit."""
+    from _util import collision_bias, collision_bias_logits, collision_logits
+    for z in (collision_logits(2000).float(), collision_bias_logits(2000).float() + collision_bias()):
+        p = torch.softmax(z, -1)
+        _, on_p = orc.topk_cpu(p.numpy(), 5)
+        _, on_z = orc.topk_cpu(z.numpy(), 5)
+        assert (on_p != on_z).any(axis=1).mean() > 0.1
