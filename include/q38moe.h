@@ -8,7 +8,8 @@
  * Conventions shared by every entry point
  *  - All tensor arguments are device pointers to caller-allocated, contiguous, row-major memory.
  *    The library never allocates or frees device memory; scratch space is a caller-provided
- *    workspace whose size comes from the matching *_workspace_bytes query.
+ *    workspace whose size comes from the matching *_workspace_bytes query (except for
+ *    q38moe_block_forward_noalloc, which uses a static per-GPU array instead).
  *  - bf16 tensors are passed as raw 16-bit storage (torch.bfloat16 bit patterns).
  *  - Expert/token indices produced by the library are int32. q38moe_experts_forward also accepts
  *    the int64 indices torch.topk returns (idx_is_int64 = 1).
@@ -19,8 +20,9 @@
  *  - Shapes: T tokens (T*k < 2^31), hidden h, E experts, top-k k, routed intermediate I, shared
  *    intermediate Is. Supported: 1 <= E <= 64, 1 <= k <= min(8, E), h % 64 == 0,
  *    I % 64 == 0, Is % 64 == 0; every pointer 16-byte aligned. dtype must be Q38MOE_BF16.
- *  - The library keeps no mutable global state, so calls on different streams may overlap as long
- *    as they use different workspaces and outputs.
+ *  - Apart from the static scratch of q38moe_block_forward_noalloc, the library keeps no mutable
+ *    global state, so calls on different streams may overlap as long as they use different
+ *    workspaces and outputs.
  */
 #ifndef Q38MOE_H
 #define Q38MOE_H
@@ -32,7 +34,7 @@
 extern "C" {
 #endif
 
-#define Q38MOE_ABI_VERSION 7
+#define Q38MOE_ABI_VERSION 8
 
 #define Q38MOE_OK 0
 #define Q38MOE_EINVAL (-1)   /* bad shape, null pointer, misalignment, unsupported dtype */
@@ -200,6 +202,27 @@ int q38moe_block_forward(const void* x, const void* w_router, const void* w_gate
                          void* topk_w, int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
                          int32_t Is, void* workspace, size_t workspace_bytes, int32_t dtype,
                          void* stream);
+
+/*
+ * Whole MoE block without a workspace argument and without allocating. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Same arguments, outputs and kernels as
+ * q38moe_block_forward, minus workspace / workspace_bytes; the scratch is a static device array of
+ * Q38MOE_NOALLOC_SCRATCH_BYTES (32 MiB) per GPU, held until the process ends, whose address is
+ * looked up on the first call on each device (which must be the current device, and the stream's).
+ * Shapes whose block workspace (q38moe_block_workspace_bytes) exceeds it are rejected with
+ * Q38MOE_EWORKSPACE (at h = 1024, E = 64, k = 5, I = Is = 256 it holds T <= 2173). Every call on a
+ * GPU shares that GPU's scratch: calls that overlap on one GPU (different streams, or threads)
+ * race and must be serialised by the caller. Nothing carried over from a previous call is read.
+ */
+#define Q38MOE_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+size_t q38moe_block_noalloc_scratch_bytes(void);
+int q38moe_block_forward_noalloc(const void* x, const void* w_router, const void* w_gate_up,
+                                 const void* w_down, const void* w_sh_gate, const void* w_sh_up,
+                                 const void* w_sh_down, const void* w_sh_gate_proj,
+                                 const float* logit_bias, void* out, void* logits, int32_t* topk_idx,
+                                 void* topk_w, int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
+                                 int32_t Is, int32_t dtype, void* stream);
 
 /*
  * FP8 expert path, R14. There is no reference function: the benchmark set's fp8 configuration

@@ -3,6 +3,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "q38moe.h"
 #include "q38moe_kernels.h"
@@ -191,6 +192,98 @@ int run_experts(const void* x, const void* idx, bool idx64, const uint16_t* topk
   Q38_HIP(q38::launch_combine(Y, inv, idx, idx64, topk_w, shared, gate, static_cast<uint16_t*>(out),
                               T, h, E, k, st),
           "combine launch");
+  return Q38MOE_OK;
+}
+
+int check_block_args(const void* x, const void* w_router, const void* w_gate_up, const void* w_down,
+                     const void* w_sh_gate, const void* w_sh_up, const void* w_sh_down, const void* w_sh_gate_proj,
+                     const void* out, int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int32_t Is,
+                     int32_t dtype) {
+  Q38_CHECK(check_dtype(dtype));
+  Q38_CHECK(check_routing(T, E, k));
+  Q38_CHECK(check_dim(h, "h"));
+  Q38_CHECK(check_dim(I, "I"));
+  Q38_CHECK(check_dim(Is, "Is"));
+  if (T == 0) return Q38MOE_OK;
+  Q38_CHECK(check_rows(T, h, k));
+  Q38_CHECK(check_ptr(x, "x"));
+  Q38_CHECK(check_ptr(w_router, "w_router"));
+  Q38_CHECK(check_ptr(w_gate_up, "w_gate_up"));
+  Q38_CHECK(check_ptr(w_down, "w_down"));
+  Q38_CHECK(check_ptr(w_sh_gate, "w_sh_gate"));
+  Q38_CHECK(check_ptr(w_sh_up, "w_sh_up"));
+  Q38_CHECK(check_ptr(w_sh_down, "w_sh_down"));
+  Q38_CHECK(check_ptr(w_sh_gate_proj, "w_sh_gate_proj"));
+  Q38_CHECK(check_ptr(out, "out"));
+  return Q38MOE_OK;
+}
+
+// The whole block (modeling:824-835) on a workspace laid out by block_layout.
+int run_block(const void* x, const void* w_router, const void* w_gate_up, const void* w_down, const void* w_sh_gate,
+              const void* w_sh_up, const void* w_sh_down, const void* w_sh_gate_proj, const float* logit_bias,
+              void* out, void* logits, int32_t* topk_idx, void* topk_w, int64_t T, int32_t h, int32_t E, int32_t k,
+              int32_t I, int32_t Is, void* workspace, const BlockWs& L, hipStream_t st) {
+  int32_t* idx = topk_idx != nullptr ? topk_idx : at<int32_t>(workspace, L.idx);
+  uint16_t* w = topk_w != nullptr ? static_cast<uint16_t*>(topk_w) : at<uint16_t>(workspace, L.w);
+  uint16_t* gate = at<uint16_t>(workspace, L.gate);
+  int32_t* hist = at<int32_t>(workspace, L.ex.hist);
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  const uint16_t* sh_out = nullptr;
+  if (!L.fused) {
+    // Shared expert (modeling:827) as its own dense GEMMs when its width differs from I.
+    uint16_t* Hs = at<uint16_t>(workspace, L.Hs);
+    uint16_t* sh = at<uint16_t>(workspace, L.sh);
+    Q38_HIP(q38::launch_gate_up(xb, nullptr, nullptr, nullptr, 0, T, 0, nullptr,
+                                static_cast<const uint16_t*>(w_sh_gate), static_cast<const uint16_t*>(w_sh_up), Hs,
+                                Is, h, E, 1, st),
+            "shared gate_up launch");
+    Q38_HIP(q38::launch_down(Hs, nullptr, nullptr, 0, T, nullptr, static_cast<const uint16_t*>(w_sh_down), sh, h,
+                             Is, E, st),
+            "shared down launch");
+    sh_out = sh;
+  }
+  // Router + shared gate logit + histogram (modeling:828, 831).
+  Q38_HIP(q38::launch_route(xb, static_cast<const uint16_t*>(w_router), static_cast<const uint16_t*>(w_sh_gate_proj),
+                            nullptr, logit_bias, static_cast<uint16_t*>(logits), idx, w, gate, hist, T, h, E, k, st),
+          "route launch");
+  // Routed experts (+ the shared expert inside the same GEMMs) and the gated sum (modeling:829-833).
+  return run_experts(x, idx, false, w, w_gate_up, w_down,
+                     L.fused ? static_cast<const uint16_t*>(w_sh_gate) : nullptr,
+                     L.fused ? static_cast<const uint16_t*>(w_sh_up) : nullptr,
+                     L.fused ? static_cast<const uint16_t*>(w_sh_down) : nullptr, sh_out, gate, out, T, h, E, k, I,
+                     L.fused ? T : 0, hist, workspace, L.ex, st);
+}
+
+// Static scratch of q38moe_block_forward_noalloc: one copy per GPU, held until the process ends.
+// In host code `scratch` only names the symbol; its device address (different on every GPU) comes
+// from hipGetSymbolAddress with that GPU current, looked up once per device and kept in
+// g_scratch_dev. Nothing in it needs clearing: every buffer the block carves from it is written in
+// full before it is read.
+constexpr size_t kScratchBytes = Q38MOE_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+static __device__ __attribute__((aligned(256))) uint8_t scratch[kScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+int scratch_for_current_device(hipStream_t stream, void** ptr) {
+  int dev = -1;
+  Q38_HIP(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(Q38MOE_EINVAL, "device %d out of range", dev);
+  if (stream != nullptr) {
+    int sdev = -1;
+    Q38_HIP(hipStreamGetDevice(stream, &sdev), "hipStreamGetDevice");
+    if (sdev != dev)
+      return fail(Q38MOE_EINVAL, "stream belongs to device %d but device %d is current; make it current", sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    Q38_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (p == nullptr || reinterpret_cast<uintptr_t>(p) % kAlign != 0)
+      return fail(Q38MOE_EHIP, "static scratch has no 256-byte aligned device address");
+    g_scratch_dev[dev] = p;
+  }
+  *ptr = g_scratch_dev[dev];
   return Q38MOE_OK;
 }
 
@@ -575,58 +668,42 @@ int q38moe_block_forward(const void* x, const void* w_router, const void* w_gate
                          int32_t Is, void* workspace, size_t workspace_bytes, int32_t dtype,
                          void* stream) {
   g_err[0] = 0;
-  Q38_CHECK(check_dtype(dtype));
-  Q38_CHECK(check_routing(T, E, k));
-  Q38_CHECK(check_dim(h, "h"));
-  Q38_CHECK(check_dim(I, "I"));
-  Q38_CHECK(check_dim(Is, "Is"));
+  Q38_CHECK(check_block_args(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_sh_down, w_sh_gate_proj, out, T,
+                             h, E, k, I, Is, dtype));
   if (T == 0) return Q38MOE_OK;
-  Q38_CHECK(check_rows(T, h, k));
-  Q38_CHECK(check_ptr(x, "x"));
-  Q38_CHECK(check_ptr(w_router, "w_router"));
-  Q38_CHECK(check_ptr(w_gate_up, "w_gate_up"));
-  Q38_CHECK(check_ptr(w_down, "w_down"));
-  Q38_CHECK(check_ptr(w_sh_gate, "w_sh_gate"));
-  Q38_CHECK(check_ptr(w_sh_up, "w_sh_up"));
-  Q38_CHECK(check_ptr(w_sh_down, "w_sh_down"));
-  Q38_CHECK(check_ptr(w_sh_gate_proj, "w_sh_gate_proj"));
-  Q38_CHECK(check_ptr(out, "out"));
   const BlockWs L = block_layout(T, h, E, k, I, Is);
   if (workspace == nullptr || workspace_bytes < L.end)
     return fail(Q38MOE_EWORKSPACE, "workspace needs %zu bytes (got %zu)", L.end, workspace_bytes);
   if (reinterpret_cast<uintptr_t>(workspace) % kAlign != 0)
     return fail(Q38MOE_EINVAL, "workspace must be 256-byte aligned");
   (void)hipGetLastError();
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  int32_t* idx = topk_idx != nullptr ? topk_idx : at<int32_t>(workspace, L.idx);
-  uint16_t* w = topk_w != nullptr ? static_cast<uint16_t*>(topk_w) : at<uint16_t>(workspace, L.w);
-  uint16_t* gate = at<uint16_t>(workspace, L.gate);
-  int32_t* hist = at<int32_t>(workspace, L.ex.hist);
-  const uint16_t* xb = static_cast<const uint16_t*>(x);
-  const uint16_t* sh_out = nullptr;
-  if (!L.fused) {
-    // Shared expert (modeling:827) as its own dense GEMMs when its width differs from I.
-    uint16_t* Hs = at<uint16_t>(workspace, L.Hs);
-    uint16_t* sh = at<uint16_t>(workspace, L.sh);
-    Q38_HIP(q38::launch_gate_up(xb, nullptr, nullptr, nullptr, 0, T, 0, nullptr,
-                                static_cast<const uint16_t*>(w_sh_gate), static_cast<const uint16_t*>(w_sh_up), Hs,
-                                Is, h, E, 1, st),
-            "shared gate_up launch");
-    Q38_HIP(q38::launch_down(Hs, nullptr, nullptr, 0, T, nullptr, static_cast<const uint16_t*>(w_sh_down), sh, h,
-                             Is, E, st),
-            "shared down launch");
-    sh_out = sh;
-  }
-  // Router + shared gate logit + histogram (modeling:828, 831).
-  Q38_HIP(q38::launch_route(xb, static_cast<const uint16_t*>(w_router), static_cast<const uint16_t*>(w_sh_gate_proj),
-                            nullptr, logit_bias, static_cast<uint16_t*>(logits), idx, w, gate, hist, T, h, E, k, st),
-          "route launch");
-  // Routed experts (+ the shared expert inside the same GEMMs) and the gated sum (modeling:829-833).
-  return run_experts(x, idx, false, w, w_gate_up, w_down,
-                     L.fused ? static_cast<const uint16_t*>(w_sh_gate) : nullptr,
-                     L.fused ? static_cast<const uint16_t*>(w_sh_up) : nullptr,
-                     L.fused ? static_cast<const uint16_t*>(w_sh_down) : nullptr, sh_out, gate, out, T, h, E, k, I,
-                     L.fused ? T : 0, hist, workspace, L.ex, st);
+  return run_block(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_sh_down, w_sh_gate_proj, logit_bias, out,
+                   logits, topk_idx, topk_w, T, h, E, k, I, Is, workspace, L, static_cast<hipStream_t>(stream));
+}
+
+size_t q38moe_block_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+int q38moe_block_forward_noalloc(const void* x, const void* w_router, const void* w_gate_up,
+                                 const void* w_down, const void* w_sh_gate, const void* w_sh_up,
+                                 const void* w_sh_down, const void* w_sh_gate_proj,
+                                 const float* logit_bias, void* out, void* logits, int32_t* topk_idx,
+                                 void* topk_w, int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
+                                 int32_t Is, int32_t dtype, void* stream) {
+  g_err[0] = 0;
+  Q38_CHECK(check_block_args(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_sh_down, w_sh_gate_proj, out, T,
+                             h, E, k, I, Is, dtype));
+  if (T == 0) return Q38MOE_OK;
+  const BlockWs L = block_layout(T, h, E, k, I, Is);
+  if (L.end > kScratchBytes)
+    return fail(Q38MOE_EWORKSPACE,
+                "q38moe_block_forward_noalloc: this shape needs %zu bytes of scratch, the static scratch holds %zu "
+                "(T=%lld is too large: call q38moe_block_forward with a workspace)",
+                L.end, kScratchBytes, (long long)T);
+  void* ws = nullptr;
+  Q38_CHECK(scratch_for_current_device(static_cast<hipStream_t>(stream), &ws));
+  (void)hipGetLastError();
+  return run_block(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_sh_down, w_sh_gate_proj, logit_bias, out,
+                   logits, topk_idx, topk_w, T, h, E, k, I, Is, ws, L, static_cast<hipStream_t>(stream));
 }
 
 // ---- fp8 expert path (R14) --------------------------------------------------------------------

@@ -12,7 +12,7 @@ import torch  # noqa: F401  (loads the HIP runtime first)
 
 LIB_PATH = Path(os.environ.get("Q38MOE_LIB", Path(__file__).resolve().parent / "libq38moe.so"))
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 BF16 = 1
 
 _c_int, _c_i32, _c_i64, _c_size, _vp = ctypes.c_int, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
@@ -43,6 +43,9 @@ SIGNATURES = {
                                               ctypes.POINTER(_c_size)]),
     "q38moe_block_forward": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                       _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp, _c_size, _c_i32, _vp]),
+    "q38moe_block_noalloc_scratch_bytes": (_c_size, []),
+    "q38moe_block_forward_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                              _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp]),
     "q38moe_quantize_rows": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i32, _vp]),
     "q38moe_gate_up_fp8": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i64,
                                     _c_i32, _c_i32, _c_i32, _c_i32, _vp]),

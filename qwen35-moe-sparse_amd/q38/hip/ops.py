@@ -393,6 +393,42 @@ def block_forward(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_sh_down,
     return out
 
 
+def block_forward_noalloc(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_sh_down, w_sh_gate_proj, k,
+                          logit_bias=None, out=None, logits=None, idx=None, w=None):
+    """block_forward through q38moe_block_forward_noalloc: the library's static per-GPU scratch
+    instead of a workspace, no allocation inside the call. Outputs are the caller's (allocated
+    here only when not given): out [T,h] bf16 and, optionally, logits [T,E] bf16, idx [T,k] int32,
+    w [T,k] bf16. Raises RuntimeError when T exceeds what the scratch holds."""
+    _need(x, "x", ndim=2)
+    T, h = x.shape
+    E = w_router.shape[0]
+    I = w_gate_up.shape[1] // 2
+    Is = w_sh_gate.shape[0]
+    if w_gate_up.shape != (E, 2 * I, h) or w_down.shape != (E, h, I) or w_router.shape != (E, h):
+        raise ValueError("expert weights must be [E,2I,h] and [E,h,I], router [E,h]")
+    if w_sh_gate.shape != (Is, h) or w_sh_up.shape != (Is, h) or w_sh_down.shape != (h, Is):
+        raise ValueError("shared expert weights must be [Is,h], [Is,h], [h,Is]")
+    for t, n in ((w_router, "w_router"), (w_gate_up, "w_gate_up"), (w_down, "w_down"), (w_sh_gate, "w_sh_gate"),
+                 (w_sh_up, "w_sh_up"), (w_sh_down, "w_sh_down"), (w_sh_gate_proj, "w_sh_gate_proj")):
+        _need(t, n)
+    if logit_bias is not None:
+        _need(logit_bias, "logit_bias", dtype=torch.float32, ndim=1)
+    dev = x.device
+    if out is None:
+        out = torch.empty(T, h, dtype=torch.bfloat16, device=dev)
+    for t, n, shape, dt in ((out, "out", (T, h), torch.bfloat16), (logits, "logits", (T, E), torch.bfloat16),
+                            (idx, "idx", (T, k), torch.int32), (w, "w", (T, k), torch.bfloat16)):
+        if t is not None:
+            _need(t, n, dtype=dt)
+            if tuple(t.shape) != shape:
+                raise ValueError(f"{n} must be {shape}")
+    check(lib.q38moe_block_forward_noalloc(_ptr(x), _ptr(w_router), _ptr(w_gate_up), _ptr(w_down), _ptr(w_sh_gate),
+                                           _ptr(w_sh_up), _ptr(w_sh_down), _ptr(w_sh_gate_proj), _ptr(logit_bias),
+                                           _ptr(out), _ptr(logits), _ptr(idx), _ptr(w), T, h, E, k, I, Is, BF16,
+                                           _stream(dev)), "q38moe_block_forward_noalloc")
+    return out
+
+
 # ---- fp8 expert path (R14: e4m3 experts with per-output-channel scales; no reference function) ----
 
 FP8_WEIGHT_NAMES = ("experts.gate_up_proj", "experts.down_proj", "shared_expert.gate_proj.weight",
