@@ -141,46 +141,86 @@ def kernel_breakdown_fp8(wl, x, d, wq, bias, iters, stream):
     return out
 
 
-def cpu_baseline(wl, budget_s=12.0, max_runs=400):
-    """The reference block's own op sequence (eager experts loop) in bf16 on this host's CPU over the
-    same workload: whole block forwards over the first `tokens` tokens (all of them unless one run
-    would exceed the budget), repeated until about `budget_s` seconds of CPU work are done."""
+def _time_cpu_block(wl, dtype, experts, budget_s, max_runs=400):
+    """Median seconds of the reference block's op sequence (oracle.reference_block_forward) on this
+    host's CPU in `dtype` with the given experts implementation: 1 warmup, then runs over a sample
+    of the workload's tokens (all of them unless one run would exceed a third of the budget) until
+    about `budget_s` seconds of work are done, at least 3."""
     import torch
     from oracle import moe_oracle
     from q38 import workloads
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
-    x_all, params, bias = workloads.make(wl)
+    x_all, params, bias = workloads.make(wl, dtype=dtype)
     tokens = min(1024, wl.tokens)
     with torch.inference_mode():
         t0 = time.perf_counter()
-        moe_oracle.reference_block_forward(x_all[:tokens], params, wl.topk, logit_bias=bias)  # warmup + probe
+        moe_oracle.reference_block_forward(x_all[:tokens], params, wl.topk, logit_bias=bias, experts=experts)
         per_tok = (time.perf_counter() - t0) / tokens
-        tokens = int(max(1024, min(wl.tokens, budget_s / 3 / max(per_tok, 1e-9))))
+        tokens = int(max(min(1024, wl.tokens), min(wl.tokens, budget_s / 3 / max(per_tok, 1e-9))))
         x = x_all[:tokens]
+        moe_oracle.reference_block_forward(x, params, wl.topk, logit_bias=bias, experts=experts)  # warmup
         times = []
         start = time.perf_counter()
         while len(times) < 3 or (time.perf_counter() - start < budget_s and len(times) < max_runs):
             t0 = time.perf_counter()
-            moe_oracle.reference_block_forward(x, params, wl.topk, logit_bias=bias)
+            moe_oracle.reference_block_forward(x, params, wl.topk, logit_bias=bias, experts=experts)
             times.append(time.perf_counter() - t0)
-    total = sum(times)
     med = sorted(times)[len(times) // 2]
-    cpu = ""
+    return dict(tokens=tokens, runs=len(times), seconds_total=round(sum(times), 2), seconds_median=round(med, 5),
+                value=round(tokens / med, 1))
+
+
+def _host_cpu():
+    """Model name, family/model/stepping and core counts of this host (lscpu / cpuinfo)."""
+    import subprocess
+    import torch
+    info = {}
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            if key.strip() in ("Model name", "CPU family", "Model", "Stepping", "Socket(s)", "Core(s) per socket",
+                               "Thread(s) per core"):
+                info[key.strip()] = val.strip()
+    except (OSError, subprocess.SubprocessError):
         pass
-    return dict(value=round(tokens / med, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
-                sample=f"{len(times)} block forwards over {tokens} of the {wl.tokens} tokens of {wl.name} "
-                       f"(h={wl.hidden}, E={wl.experts}, k={wl.topk}, I={wl.inter}), {total:.1f} s of CPU work; "
-                       f"bf16 torch CPU running the reference op sequence with the eager experts loop "
-                       f"(modeling_qwen3_8_moe.py:769-793,805-813,824-835); value = tokens / median run",
-                runs=len(times), seconds_total=round(total, 2), seconds_median=round(med, 4),
-                os_cpu_count=os.cpu_count(), cpu_model=cpu)
+    return dict(cpu_model=info.get("Model name", ""), lscpu=info, os_cpu_count=os.cpu_count(),
+                torch_threads=torch.get_num_threads(), torch_cpu_capability=torch.backends.cpu.get_cpu_capability())
+
+
+def cpu_baseline(wl, budget_s=8.0):
+    """The reference block on this host's CPU (BASELINE plan): the primary figure is the eager
+    experts loop (the module's own forward, modeling_qwen3_8_moe.py:769-793) in the workload's
+    dtype over the workload's tokens; `variants` adds transformers' grouped_mm experts (the
+    presets' configured implementation, integrations/moe.py:377-478) on the same tokens, and, for
+    the bf16 workloads, configuration 1 (fp32, h=256) with both implementations."""
+    import torch
+    from q38 import workloads
+    torch.set_num_threads(os.cpu_count() or 1)
+    bf = torch.float32 if wl.dtype == "fp32" else torch.bfloat16
+    dname = "fp32" if bf == torch.float32 else "bf16"
+    runs = {f"eager_{dname}_{wl.name}": (wl, bf, "eager", budget_s),
+            f"grouped_mm_{dname}_{wl.name}": (wl, bf, "grouped_mm", budget_s * 0.75)}
+    if wl.name != "c1":
+        c1 = workloads.get("c1")
+        runs["eager_fp32_c1"] = (c1, torch.float32, "eager", budget_s * 0.4)
+        runs["grouped_mm_fp32_c1"] = (c1, torch.float32, "grouped_mm", budget_s * 0.4)
+    variants = {}
+    for name, (w_, dt, ex, bud) in runs.items():
+        r = _time_cpu_block(w_, dt, ex, bud)
+        r.update(unit="tokens/s", workload=w_.name, dtype="fp32" if dt == torch.float32 else "bf16", experts=ex)
+        variants[name] = r
+        log(f"[bench] cpu {name}: {r['value']} tokens/s ({r['runs']} runs over {r['tokens']} tokens)")
+    prim = variants[f"eager_{dname}_{wl.name}"]
+    host = _host_cpu()
+    return dict(value=prim["value"], unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"{prim['runs']} block forwards over {prim['tokens']} of the {wl.tokens} tokens of {wl.name} "
+                       f"(h={wl.hidden}, E={wl.experts}, k={wl.topk}, I={wl.inter}), {prim['seconds_total']:.1f} s of "
+                       f"CPU work; {dname} torch CPU running the reference op sequence with the eager experts loop "
+                       f"(modeling_qwen3_8_moe.py:769-793,805-813,824-835); value = tokens / median run after one "
+                       f"warmup; variants: grouped_mm experts (transformers integrations/moe.py:377-478) and "
+                       f"configuration 1 in fp32, same protocol",
+                runs=prim["runs"], seconds_total=prim["seconds_total"], seconds_median=prim["seconds_median"],
+                variants=variants, **host)
 
 
 # Kernel symbol prefix of each stage, as rocprofv3 names it (the committed PMC byte counts are keyed

@@ -20,6 +20,8 @@ modeling_qwen3_8_moe.py, "inference" = q38/inference.py):
                   of transformers' grouped_mm path): per-expert fp32 matmuls on gathered rows,
                   bf16 rounding of gate/up, silu, product, down, weight; fp32 k-sum.
   experts_eager   Qwen3_8MoeExperts.forward, modeling:769-793, op for op (index_add_ in D).
+  experts_grouped_mm  transformers' grouped_mm_experts_forward (integrations/moe.py:377-478), the
+                  configured implementation of the presets, on torch.nn.functional.grouped_mm.
   shared_expert   Qwen3_8MoeMLP.forward, modeling:751-753.
   block           Qwen3_8MoeSparseMoeBlock.forward, modeling:824-835.
   reference_block_forward  the whole block computed with the reference's own torch op sequence in
@@ -208,6 +210,35 @@ def experts_eager(x, idx, w, w_gate_up, w_down):
     return final
 
 
+def experts_grouped_mm(x, idx, w, w_gate_up, w_down):
+    """The experts implementation the reference's presets configure (configs/q38_c1.json:22):
+    transformers' grouped_mm_experts_forward (installed integrations/moe.py:377-478), restated on
+    torch.nn.functional.grouped_mm in the dtype of x. Pairs sorted by expert (torch.sort), per-expert
+    row offsets (histc + cumsum), one grouped GEMM over the gathered rows against gate_up_proj^T,
+    silu(gate) * up (moe.py:509-520), one grouped GEMM against down_proj^T, times the routing
+    weight, rows back in pair order, then the k-sum (accumulated in fp32 for bf16 inputs by
+    torch's reduction) cast to x's dtype. Pairs with indices outside [0, E) contribute nothing."""
+    T, h = x.shape
+    k = idx.shape[1]
+    E = w_gate_up.shape[0]
+    ids = idx.reshape(-1)
+    ids_g, perm = torch.sort(ids)
+    rows = x[perm // k]
+    wg = w.reshape(-1)[perm]
+    counts = torch.histc(ids_g.float(), bins=E, min=0, max=E - 1)
+    offs = torch.cumsum(counts, dim=0, dtype=torch.int32)
+    dropped = (ids_g >= E).unsqueeze(-1)
+    rows = rows.masked_fill(dropped, 0.0)
+    gu = F.grouped_mm(rows, w_gate_up.transpose(-2, -1), offs=offs)
+    gate, up = gu.chunk(2, dim=-1)
+    act = F.silu(gate) * up
+    y = F.grouped_mm(act, w_down.transpose(-2, -1), offs=offs)
+    y = (y * wg.unsqueeze(-1)).masked_fill(dropped, 0.0)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    return y[inv].view(T, k, h).sum(dim=1).to(x.dtype)
+
+
 def shared_expert(x, w_gate, w_up, w_down):
     """modeling:751-753 with fp32 matmuls rounded once to bf16 at each linear."""
     g = _f(bf16(_f(x) @ _f(w_gate).T))
@@ -229,11 +260,12 @@ def block(x, params, k, logit_bias=None):
                      gate_logit=gate_logit)
 
 
-def reference_block_forward(x, params, k, logit_bias=None):
+def reference_block_forward(x, params, k, logit_bias=None, experts="eager"):
     """The reference block's own op sequence (modeling:805-813, 769-793, 751-753, 824-835) in the
-    dtype of the inputs, eager experts loop. This is the CPU baseline that bench.py times. The
-    optional fp32 ``logit_bias`` [E] (routing-skew workload) is added to the logits before the
-    softmax."""
+    dtype of the inputs, with the eager experts loop (experts="eager", the module's own forward) or
+    the grouped_mm implementation the presets configure (experts="grouped_mm"). This is the CPU
+    baseline that bench.py times. The optional fp32 ``logit_bias`` [E] (routing-skew workload) is
+    added to the logits before the softmax."""
     logits = F.linear(x, params["gate.weight"])
     z = logits if logit_bias is None else logits.float() + logit_bias.float()
     probs = torch.softmax(z, dtype=torch.float, dim=-1)
@@ -243,7 +275,8 @@ def reference_block_forward(x, params, k, logit_bias=None):
     g = F.linear(x, params["shared_expert.gate_proj.weight"])
     u = F.linear(x, params["shared_expert.up_proj.weight"])
     sh = F.linear(F.silu(g) * u, params["shared_expert.down_proj.weight"])
-    routed = experts_eager(x, idx, w, params["experts.gate_up_proj"], params["experts.down_proj"])
+    run = experts_grouped_mm if experts == "grouped_mm" else experts_eager
+    routed = run(x, idx, w, params["experts.gate_up_proj"], params["experts.down_proj"])
     sh = torch.sigmoid(F.linear(x, params["shared_expert_gate.weight"])) * sh
     return routed + sh
 

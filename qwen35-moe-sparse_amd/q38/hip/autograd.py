@@ -19,7 +19,11 @@ the backward runs, with Y' = dout[t] * w[p] (the routed raw rows' gradient) in s
 Expert row ranges stay on the device (starts/counts of the permutation): the backward makes no
 host synchronisation.
 
-All tensors bf16 (the grads in the parameters' dtype), indices int32/int64 as in the forward.
+The kernels take bf16. Under bf16 autocast, parameters and activations of another dtype (the
+reference's training setup: fp32 parameters with torch.autocast, scripts/check_q38_kernels.py:19-26,
+whose padded path then runs its bmm in bf16) are cast to bf16 by differentiable .to() calls, and
+the output comes back in hidden_states' dtype, so their gradients arrive in their own dtype. Indices
+are int32/int64 as in the forward.
 """
 import torch
 
@@ -72,11 +76,21 @@ class HipExperts(torch.autograd.Function):
         return dx, None, dw, dgu_w, ddn_w
 
 
+def _bf16_autocast():
+    return torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
+
+
 def experts(x, topk_idx, topk_w, w_gate_up, w_down):
-    """Routed experts with autograd (ExpertsInterface contract): [T,h] bf16; gradients flow to x,
-    topk_w, w_gate_up and w_down."""
-    for t, n in ((x, "hidden_states"), (topk_w, "top_k_weights"), (w_gate_up, "gate_up_proj"), (w_down, "down_proj")):
+    """Routed experts with autograd (ExpertsInterface contract): [T,h] in x's dtype; gradients flow
+    to x, topk_w, w_gate_up and w_down. Tensors must be bf16, or any float dtype under bf16
+    autocast (cast to bf16 differentiably, as autocast casts the reference's bmm operands)."""
+    named = ((x, "hidden_states"), (topk_w, "top_k_weights"), (w_gate_up, "gate_up_proj"), (w_down, "down_proj"))
+    cast = False
+    for t, n in named:
         if t.dtype != torch.bfloat16:
-            raise TypeError(f"{n} must be bf16 for the HIP experts, got {t.dtype}")
-    return HipExperts.apply(x.contiguous(), topk_idx.contiguous(), topk_w.contiguous(), w_gate_up.contiguous(),
-                            w_down.contiguous())
+            if not (_bf16_autocast() and t.is_floating_point()):
+                raise TypeError(f"{n} must be bf16 for the HIP experts (or run under bf16 autocast), got {t.dtype}")
+            cast = True
+    args = [t.to(torch.bfloat16).contiguous() for t, _ in named]
+    out = HipExperts.apply(args[0], topk_idx.contiguous(), args[1], args[2], args[3])
+    return out.to(x.dtype) if cast else out

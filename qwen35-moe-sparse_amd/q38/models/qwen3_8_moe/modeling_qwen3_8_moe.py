@@ -10,7 +10,9 @@ of ``q38.prefill``; it is registered for the Auto classes like the reference (__
 ``save_pretrained`` exports this file and ``from_pretrained(..., trust_remote_code=True)`` runs the
 kernels again. The imports of the library are absolute because an export runs this file outside
 the package: the ``q38`` package must be importable where an export is loaded.
-Forward-only: every forward raises under autograd. Inputs and weights must be bf16 CUDA tensors;
+Under autograd the routed experts (``Qwen3_8MoeExperts``) are differentiable (the HIP backward:
+bf16 tensors, or fp32 parameters under bf16 autocast); the router, the shared MLP, the fused block
+and the causal LM are forward-only and raise under autograd. Inputs and weights are CUDA tensors;
 there is no CPU path.
 """
 import torch

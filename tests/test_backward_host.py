@@ -1,5 +1,5 @@
 """Host-side contracts of the differentiable HIP experts (q38.hip.autograd), no GPU needed: bf16
-only, and no CPU fallback (CPU tensors are refused before any kernel launch)."""
+only outside bf16 autocast, and no CPU fallback (CPU tensors are refused before any kernel launch)."""
 import pytest
 import torch
 
@@ -18,6 +18,8 @@ def test_experts_requires_bf16():
     from q38.hip import autograd
     with pytest.raises(TypeError, match="bf16"):
         autograd.experts(*_args(torch.float32))
+    with pytest.raises(TypeError, match="bf16"):
+        autograd.experts(*_args(torch.float16))
 
 
 def test_experts_refuses_cpu_tensors():

@@ -85,6 +85,42 @@ def test_experts_backward_partial_grads(gpu):
     assert _rel(wdg.grad, ref_g[3]) <= REL
 
 
+def test_experts_backward_fp32_params_under_autocast(gpu):
+    """fp32 leaves under bf16 autocast (the reference's training setup, scripts/check_q38_kernels.py:
+    19-26): the kernels run on bf16 casts, the output comes back in fp32 and every gradient arrives
+    in fp32, within the reference's bar of fp32 autograd; outside autocast fp32 is refused."""
+    from q38.hip import autograd
+    from q38.inference import hip_experts_forward
+    _, x, idx, w, wgu, wdn, dout = _inputs("c1", 411)
+    _, ref_g = _cpu_grads(x, idx, w, wgu, wdn, dout, torch.float32)
+    leaves = [t.float().to(gpu).requires_grad_(True) for t in (x, w, wgu, wdn)]
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = autograd.experts(leaves[0], idx.to(gpu), *leaves[1:])
+    assert out.dtype == torch.float32
+    out.backward(dout.float().to(gpu))
+    for nm, leaf, r in zip(("x", "top_k_weights", "gate_up_proj", "down_proj"), leaves, ref_g):
+        assert leaf.grad is not None and leaf.grad.dtype == torch.float32, nm
+        assert _rel(leaf.grad, r) <= REL, f"d{nm}: rel {_rel(leaf.grad, r):.3e}"
+    # The registered implementation with fp32 module parameters, as a model trains under autocast.
+
+    class Experts(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.gate_up_proj = torch.nn.Parameter(wgu.float().to(gpu))
+            self.down_proj = torch.nn.Parameter(wdn.float().to(gpu))
+
+    m = Experts()
+    xg = x.float().to(gpu).requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = hip_experts_forward(m, xg, idx.to(gpu), w.float().to(gpu))
+    out.backward(dout.float().to(gpu))
+    assert m.gate_up_proj.grad.dtype == torch.float32 and _rel(m.gate_up_proj.grad, ref_g[2]) <= REL
+    assert _rel(xg.grad, ref_g[0]) <= REL and _rel(m.down_proj.grad, ref_g[3]) <= REL
+    with pytest.raises(TypeError, match="autocast"):
+        autograd.experts(*[t.detach().requires_grad_(True) for t in (leaves[0],)], idx.to(gpu),
+                         *[t.detach().requires_grad_(True) for t in leaves[1:]])
+
+
 def test_registered_experts_train(gpu):
     """The registered ExpertsInterface implementation runs the differentiable path under autograd
     (module parameters with requires_grad) and the plain forward under inference_mode."""

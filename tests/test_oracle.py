@@ -245,3 +245,34 @@ def test_collision_rows_need_probabilities():
         _, on_p = orc.topk_cpu(p.numpy(), 5)
         _, on_z = orc.topk_cpu(z.numpy(), 5)
         assert (on_p != on_z).any(axis=1).mean() > 0.1
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_experts_grouped_mm_is_transformers(dtype):
+    """experts_grouped_mm (the presets' configured implementation, restated on F.grouped_mm) equals
+    the installed transformers grouped_mm_experts_forward bit for bit on the same module state,
+    dropped sentinel pairs included; and it agrees with the eager loop (fp32: to float rounding)."""
+    moe = pytest.importorskip("transformers.integrations.moe")
+    g = torch.Generator().manual_seed(9)
+    T, h, E, k, I = 93, 64, 8, 3, 32
+    x = torch.randn(T, h, generator=g).to(dtype)
+    idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)])
+    idx[5, 1] = E  # a sentinel pair (expert-parallel drop), contributes nothing
+    w = torch.rand(T, k, generator=g).to(dtype)
+    wgu = (torch.randn(E, 2 * I, h, generator=g) * 0.1).to(dtype)
+    wdn = (torch.randn(E, h, I, generator=g) * 0.1).to(dtype)
+
+    class Mod(torch.nn.Module):
+        num_experts, has_gate, has_bias, is_transposed = E, True, False, False
+        gate_up_proj, down_proj = wgu, wdn
+        act_fn = staticmethod(F.silu)
+
+        def _apply_gate(self, gu):
+            return moe._default_apply_gate(self, gu)
+
+    want = moe.grouped_mm_experts_forward(Mod(), x, idx, w)
+    got = orc.experts_grouped_mm(x, idx, w, wgu, wdn)
+    assert got.dtype == dtype and torch.equal(got, want)
+    if dtype == torch.float32:
+        eager = orc.experts_eager(x, idx, w, wgu, wdn)
+        assert torch.allclose(got, eager, rtol=1e-5, atol=1e-6)
