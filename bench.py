@@ -250,6 +250,21 @@ def hbm_traffic(workload, stage):
     return round(entry["FETCH_SIZE_KiB"] * f["fetch_factor"] * 1024 + entry["WRITE_SIZE_KiB"] * f["write_factor"] * 1024)
 
 
+MFMA_FILE = REPO / "profiles" / "mfma_busy.json"
+
+
+def mfma_busy(workload, stage):
+    """(MFMA busy %, engine clock GHz) of `stage` from the committed rocprofv3 PMC summary
+    (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE per XCD x 1024 SIMDs; clock = GRBM_GUI_ACTIVE per
+    XCD / dispatch duration), or None when no summary for this workload and stage exists."""
+    try:
+        entry = json.loads(MFMA_FILE.read_text())["workloads"][workload][stage]
+    except (OSError, ValueError, KeyError):
+        return None
+    return {"mfma_busy_pct": entry["mfma_busy_pct"], "clock_ghz": entry["clock_ghz"],
+            "source": "profiles/mfma_busy.json"}
+
+
 def copy_probe(mib):
     """One device-to-device copy of `mib` MiB: the known-size reference for the FETCH_SIZE and
     WRITE_SIZE counters in a PMC run of this script."""
@@ -521,6 +536,8 @@ def main():
         log(f"[bench] kernels: " + ", ".join(f"{n} {v['us']}us" for n, v in kernels.items()))
 
     fl = wl.flops()
+    for name in ("gate_up", "down"):
+        kernels[name]["mfma_counters"] = mfma_busy(wl.name, name)
     dom = max(kernels, key=lambda n: kernels[n]["us"])
     dk = kernels[dom]
     expert_us = kernels["gate_up"]["us"] + kernels["down"]["us"]
@@ -543,7 +560,7 @@ def main():
                    "shared_inter": wl.shared_inter, "routing_skew": wl.zipf_s, "parallelism": "single GPU"},
         "roofline": {"kernel": dom, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
                      "unit": dk["unit"], "frac": dk["frac"], "traffic": hbm_traffic(wl.name, dom),
-                     "work_per_launch": dk["work"]},
+                     "work_per_launch": dk["work"], "mfma_counters": mfma_busy(wl.name, dom)},
         # Routed + shared expert GEMM FLOPs over the two grouped launches that compute them.
         "mfma_frac_expert_gemms": round(expert_fl / (expert_us * 1e-6) / (PEAK_FP8 if fp8 else PEAK_BF16), 4),
         "mfma_frac_block": round(fl["block"] / (ms * 1e-3) / (PEAK_FP8 if fp8 else PEAK_BF16), 4),
