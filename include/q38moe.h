@@ -19,7 +19,15 @@
  *    thread-local, human-readable message. A launch failure reports the HIP error string.
  *  - Shapes: T tokens (T*k < 2^31), hidden h, E experts, top-k k, routed intermediate I, shared
  *    intermediate Is. Supported: 1 <= E <= 64, 1 <= k <= min(8, E), h % 64 == 0,
- *    I % 64 == 0, Is % 64 == 0; every pointer 16-byte aligned. dtype must be Q38MOE_BF16.
+ *    I % 64 == 0, Is % 64 == 0; every pointer 16-byte aligned.
+ *  - dtype: Q38MOE_BF16 (bf16 tensors, the reference's bf16 rounding sequence), or Q38MOE_FP32
+ *    for the forward entry points that take a dtype (route, route_from_logits, gate_up, down,
+ *    shared_expert, combine, experts_forward, block_forward[_noalloc]): fp32 tensors, fp32
+ *    products and sums with no intermediate roundings, as the reference computes fp32 models
+ *    (q38/inference.py:54-57, 172: Triton dots with input_precision="ieee"; the eager module in
+ *    the parameters' dtype). Every float tensor of a call has the call's dtype (routing weights,
+ *    logits and the shared gate logit included); indices stay int32/int64. The fp8 and backward
+ *    entry points are bf16 only.
  *  - Apart from the static scratch of q38moe_block_forward_noalloc, the library keeps no mutable
  *    global state, so calls on different streams may overlap as long as they use different
  *    workspaces and outputs.
@@ -34,7 +42,7 @@
 extern "C" {
 #endif
 
-#define Q38MOE_ABI_VERSION 8
+#define Q38MOE_ABI_VERSION 9
 
 #define Q38MOE_OK 0
 #define Q38MOE_EINVAL (-1)   /* bad shape, null pointer, misalignment, unsupported dtype */
@@ -42,6 +50,7 @@ extern "C" {
 #define Q38MOE_EHIP (-3)     /* a HIP runtime call or kernel launch failed */
 
 #define Q38MOE_BF16 1
+#define Q38MOE_FP32 2
 
 /* Library ABI version (Q38MOE_ABI_VERSION). */
 int q38moe_abi_version(void);
@@ -72,6 +81,9 @@ const char* q38moe_last_error(void);
  *   hist [ceil(T/64), E] int32 (NULL to skip): per-64-token-block expert counts, the input of
  *     q38moe_permute.
  * Outputs: topk_idx [T,k] int32, topk_w [T,k] bf16.
+ * Q38MOE_FP32: x, w_router, w_shared_gate fp32; logits = x . w_router^T in fp32 (no rounding) and
+ *   must not be NULL (the selection reads it back); topk_w and shared_gate_logit fp32 (the
+ *   probabilities, selection and renormalisation as above, no bf16 rounding of the weights).
  */
 int q38moe_route(const void* x, const void* w_router, const void* w_shared_gate,
                  const float* logit_bias, void* logits, int32_t* topk_idx, void* topk_w,
@@ -79,8 +91,9 @@ int q38moe_route(const void* x, const void* w_router, const void* w_shared_gate,
                  int32_t k, int32_t dtype, void* stream);
 
 /*
- * Router selection only (R2) from given bf16 logits [T,E]: modeling:808-812 with the logits of
- * :807 supplied by the caller. Same outputs and tie semantics as q38moe_route.
+ * Router selection only (R2) from given logits [T,E] (bf16, or fp32 with Q38MOE_FP32):
+ * modeling:808-812 with the logits of :807 supplied by the caller. Same outputs and tie semantics
+ * as q38moe_route (topk_w in the logits' dtype).
  */
 int q38moe_route_from_logits(const void* logits, const float* logit_bias, int32_t* topk_idx,
                              void* topk_w, int32_t* hist, int64_t T, int32_t E, int32_t k,
@@ -128,6 +141,7 @@ int32_t q38moe_gemm_block_m(void);
  * expert's gate_proj / up_proj weights (w_sh_gate, w_sh_up [I,h]; needed iff shared_rows > 0,
  * which also requires Is == I).
  * w_gate_up [E, 2I, h] bf16 (experts.gate_up_proj). H [T*k + shared_rows, I] bf16.
+ * Q38MOE_FP32: every tensor fp32 and H[r, n] = silu(g) * u in fp32 with no rounding.
  */
 int q38moe_gate_up(const void* x, const void* w_gate_up, const void* w_sh_gate,
                    const void* w_sh_up, const int32_t* perm, const int32_t* tiles,
@@ -139,7 +153,7 @@ int q38moe_gate_up(const void* x, const void* w_gate_up, const void* w_sh_gate,
  * same rounding): replaces _down_kernel (inference.py:99-130).
  *   Y[r, c] = bf16(H[r] . w_down[e, c, :]) for routed rows (expert e of the row's tile), and with
  *   w_sh_down [h, I] (shared_expert.down_proj) for shared rows. Y [T*k + shared_rows, h] bf16,
- *   expert-sorted row order.
+ *   expert-sorted row order. Q38MOE_FP32: fp32 tensors, Y unrounded.
  */
 int q38moe_down(const void* H, const void* w_down, const void* w_sh_down, const int32_t* tiles,
                 const int32_t* tile_count, int64_t shared_rows, void* Y, int64_t T, int32_t h,
@@ -149,6 +163,7 @@ int q38moe_down(const void* H, const void* w_down, const void* w_sh_down, const 
  * Shared expert alone, R9 (Qwen3_8MoeMLP.forward, modeling:751-753):
  *   out[t] = bf16(bf16(bf16(silu(bf16(x.Wg^T))) * bf16(x.Wu^T)) . Wd^T).
  * w_gate [Is,h], w_up [Is,h], w_down [h,Is] bf16; Hs workspace [T,Is] bf16; out [T,h] bf16.
+ * Q38MOE_FP32: fp32 tensors, no roundings.
  */
 int q38moe_shared_expert(const void* x, const void* w_gate, const void* w_up,
                          const void* w_down, void* Hs, void* out, int64_t T, int32_t h,
@@ -163,6 +178,8 @@ int q38moe_shared_expert(const void* x, const void* w_gate, const void* w_up,
  * topk_idx (NULL = all pairs valid; int32 or int64 per idx_is_int64): pairs whose index lies
  * outside [0,E) contribute nothing. shared_out may point into Y (rows T*k..) when the shared
  * expert ran inside the grouped GEMMs.
+ * Q38MOE_FP32: Y, topk_w, shared_out, shared_gate_logit and out fp32;
+ *   out = sum_j Y[inv[p]] * w[p] (+ sigmoid(gate_logit[t]) * shared_out[t]) with no roundings.
  */
 int q38moe_combine(const void* Y, const int32_t* inv, const void* topk_idx, int32_t idx_is_int64,
                    const void* topk_w, const void* shared_out, const void* shared_gate_logit,
@@ -174,9 +191,10 @@ int q38moe_combine(const void* Y, const int32_t* inv, const void* topk_idx, int3
  *   fn(self, hidden_states[T,h], top_k_index[T,k], top_k_weights[T,k]) -> [T,h]
  * (transformers integrations/moe.py:567-570; implementations inference.py:158-199 and
  * modeling:769-793). Runs histogram, permute, gate/up, down and combine. Requires
- * T*h < 2^31.
+ * T*h < 2^31. With Q38MOE_FP32 x, topk_w, the weights and out are fp32 (the workspace query takes
+ * the same dtype: the intermediates are twice as large).
  */
-int q38moe_experts_workspace_bytes(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
+int q38moe_experts_workspace_bytes(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int32_t dtype,
                                    size_t* bytes);
 int q38moe_experts_forward(const void* x, const void* topk_idx, int32_t idx_is_int64,
                            const void* topk_w, const void* w_gate_up, const void* w_down,
@@ -192,9 +210,11 @@ int q38moe_experts_forward(const void* x, const void* topk_idx, int32_t idx_is_i
  *   Optional router outputs (NULL to skip): logits [T,E] bf16, topk_idx [T,k] int32,
  *   topk_w [T,k] bf16.
  * With Is == I the shared expert runs inside the routed grouped GEMM launches.
+ * Q38MOE_FP32: every float tensor fp32 (logits and topk_w too); the router logits and the shared
+ *   gate logit are fp32 GEMMs, and nothing is rounded below fp32 (configuration 1 and fp32 models).
  */
 int q38moe_block_workspace_bytes(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
-                                 int32_t Is, size_t* bytes);
+                                 int32_t Is, int32_t dtype, size_t* bytes);
 int q38moe_block_forward(const void* x, const void* w_router, const void* w_gate_up,
                          const void* w_down, const void* w_sh_gate, const void* w_sh_up,
                          const void* w_sh_down, const void* w_sh_gate_proj,
@@ -210,7 +230,7 @@ int q38moe_block_forward(const void* x, const void* w_router, const void* w_gate
  * q38moe_block_forward, minus workspace / workspace_bytes; the scratch is a static device array of
  * Q38MOE_NOALLOC_SCRATCH_BYTES (32 MiB) per GPU, held until the process ends, whose address is
  * looked up on the first call on each device (which must be the current device, and the stream's).
- * Shapes whose block workspace (q38moe_block_workspace_bytes) exceeds it are rejected with
+ * Shapes whose block workspace (q38moe_block_workspace_bytes, same dtype) exceeds it are rejected with
  * Q38MOE_EWORKSPACE (at h = 1024, E = 64, k = 5, I = Is = 256 it holds T <= 2173). Every call on a
  * GPU shares that GPU's scratch: calls that overlap on one GPU (different streams, or threads)
  * race and must be serialised by the caller. Nothing carried over from a previous call is read.

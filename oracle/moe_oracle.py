@@ -136,14 +136,18 @@ def _f(t):
     return t.to(torch.float32)
 
 
-def router(x, w_router, k, logit_bias=None, logits=None):
-    """modeling:805-813. Returns (logits bf16 [T,E], probs fp32 [T,E], idx int64 [T,k], w bf16 [T,k]).
+def router(x, w_router, k, logit_bias=None, logits=None, dtype=torch.bfloat16):
+    """modeling:805-813. Returns (logits [T,E], probs fp32 [T,E], idx int64 [T,k], w [T,k]) with
+    logits and w in ``dtype``: bf16 (the logits one rounding of the fp32 product, as the bf16
+    F.linear; w rounded to bf16) or fp32 (nothing rounded: the fp32 model's router).
 
-    ``logits`` may be supplied (bf16) to run only the selection, as q38moe_route_from_logits does.
-    The optional fp32 ``logit_bias`` [E] is added before the softmax (routing-skew workload).
+    ``logits`` may be supplied to run only the selection, as q38moe_route_from_logits does; their
+    dtype then decides. The optional fp32 ``logit_bias`` [E] is added before the softmax
+    (routing-skew workload).
     """
     if logits is None:
-        logits = bf16(_f(x) @ _f(w_router).T)
+        logits = (_f(x) @ _f(w_router).T).to(dtype)
+    dtype = logits.dtype
     z = _f(logits)
     if logit_bias is not None:
         z = z + _f(logit_bias)
@@ -151,7 +155,7 @@ def router(x, w_router, k, logit_bias=None, logits=None):
     vals, idx = topk_cpu(probs.numpy(), k)
     vals = torch.from_numpy(vals)
     vals = vals / vals.sum(dim=-1, keepdim=True)
-    return logits, probs, torch.from_numpy(idx), bf16(vals)
+    return logits, probs, torch.from_numpy(idx), vals.to(dtype)
 
 
 def experts_grouped(x, idx, w, w_gate_up, w_down, return_sorted=False):
@@ -260,18 +264,22 @@ def block(x, params, k, logit_bias=None):
                      gate_logit=gate_logit)
 
 
-def reference_block_forward(x, params, k, logit_bias=None, experts="eager"):
+def reference_block_forward(x, params, k, logit_bias=None, experts="eager", routing=None):
     """The reference block's own op sequence (modeling:805-813, 769-793, 751-753, 824-835) in the
     dtype of the inputs, with the eager experts loop (experts="eager", the module's own forward) or
     the grouped_mm implementation the presets configure (experts="grouped_mm"). This is the CPU
     baseline that bench.py times. The optional fp32 ``logit_bias`` [E] (routing-skew workload) is
-    added to the logits before the softmax."""
-    logits = F.linear(x, params["gate.weight"])
-    z = logits if logit_bias is None else logits.float() + logit_bias.float()
-    probs = torch.softmax(z, dtype=torch.float, dim=-1)
-    top, idx = torch.topk(probs, k, dim=-1)
-    top /= top.sum(dim=-1, keepdim=True)
-    w = top.to(logits.dtype)
+    added to the logits before the softmax. ``routing`` = (idx [T,k], w [T,k]) replaces the router
+    (to compare a device's block on the device's own routing)."""
+    if routing is None:
+        logits = F.linear(x, params["gate.weight"])
+        z = logits if logit_bias is None else logits.float() + logit_bias.float()
+        probs = torch.softmax(z, dtype=torch.float, dim=-1)
+        top, idx = torch.topk(probs, k, dim=-1)
+        top /= top.sum(dim=-1, keepdim=True)
+        w = top.to(logits.dtype)
+    else:
+        idx, w = routing
     g = F.linear(x, params["shared_expert.gate_proj.weight"])
     u = F.linear(x, params["shared_expert.up_proj.weight"])
     sh = F.linear(F.silu(g) * u, params["shared_expert.down_proj.weight"])

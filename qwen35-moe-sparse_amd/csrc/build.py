@@ -15,7 +15,7 @@ PKG_ROOT = CSRC.parent
 REPO = PKG_ROOT.parent
 OUT = PKG_ROOT / "q38" / "hip" / "libq38moe.so"
 SOURCES = ["q38moe_route.hip", "q38moe_permute.hip", "q38moe_gemm.hip", "q38moe_combine.hip", "q38moe_quant.hip",
-           "q38moe_backward.hip", "q38moe_api.hip"]
+           "q38moe_backward.hip", "q38moe_fp32.hip", "q38moe_api.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",

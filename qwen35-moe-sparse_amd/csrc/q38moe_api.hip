@@ -44,9 +44,12 @@ int check_opt_ptr(const void* p, const char* name) {
 }
 
 int check_dtype(int32_t dtype) {
-  if (dtype != Q38MOE_BF16) return fail(Q38MOE_EINVAL, "unsupported dtype %d (only Q38MOE_BF16)", dtype);
+  if (dtype != Q38MOE_BF16 && dtype != Q38MOE_FP32)
+    return fail(Q38MOE_EINVAL, "unsupported dtype %d (Q38MOE_BF16 or Q38MOE_FP32)", dtype);
   return Q38MOE_OK;
 }
+
+size_t elem_size(int32_t dtype) { return dtype == Q38MOE_FP32 ? 4 : 2; }
 
 int check_routing(int64_t T, int32_t E, int32_t k) {
   if (T < 0) return fail(Q38MOE_EINVAL, "T must be >= 0 (got %lld)", (long long)T);
@@ -84,7 +87,8 @@ struct ExpertsWs {
   int64_t max_tiles;
 };
 
-ExpertsWs experts_layout(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int64_t shared_rows) {
+ExpertsWs experts_layout(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int64_t shared_rows,
+                         size_t esz = 2) {
   ExpertsWs w;
   const int64_t P = T * k;
   const int64_t rows = P + shared_rows;
@@ -97,8 +101,8 @@ ExpertsWs experts_layout(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, 
   w.inv = off; off = align_up(off + sizeof(int32_t) * P);
   w.tiles = off; off = align_up(off + 4 * sizeof(int32_t) * w.max_tiles);
   w.tile_count = off; off = align_up(off + sizeof(int32_t));
-  w.H = off; off = align_up(off + 2 * (size_t)rows * I);
-  w.Y = off; off = align_up(off + 2 * (size_t)rows * h);
+  w.H = off; off = align_up(off + esz * (size_t)rows * I);
+  w.Y = off; off = align_up(off + esz * (size_t)rows * h);
   w.end = off;
   return w;
 }
@@ -106,20 +110,23 @@ ExpertsWs experts_layout(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, 
 struct BlockWs {
   ExpertsWs ex;
   bool fused;  // shared expert inside the grouped GEMMs (Is == I)
-  size_t idx, w, gate, Hs, sh, end;
+  size_t idx, w, gate, Hs, sh, lg, end;
 };
 
-BlockWs block_layout(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int32_t Is) {
+// esz: bytes per activation element (2 = bf16, 4 = fp32). The fp32 block also keeps its router
+// logits here when the caller does not ask for them (the selection reads them back).
+BlockWs block_layout(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int32_t Is, size_t esz = 2) {
   BlockWs b;
   b.fused = Is == I;
-  b.ex = experts_layout(T, h, E, k, I, b.fused ? T : 0);
+  b.ex = experts_layout(T, h, E, k, I, b.fused ? T : 0, esz);
   size_t off = b.ex.end;
   const int64_t P = T * k;
   b.idx = off; off = align_up(off + sizeof(int32_t) * P);
-  b.w = off; off = align_up(off + 2 * (size_t)P);
-  b.gate = off; off = align_up(off + 2 * (size_t)T);
-  b.Hs = off; off = align_up(off + (b.fused ? 0 : 2 * (size_t)T * Is));
-  b.sh = off; off = align_up(off + (b.fused ? 0 : 2 * (size_t)T * h));
+  b.w = off; off = align_up(off + esz * (size_t)P);
+  b.gate = off; off = align_up(off + esz * (size_t)T);
+  b.Hs = off; off = align_up(off + (b.fused ? 0 : esz * (size_t)T * Is));
+  b.sh = off; off = align_up(off + (b.fused ? 0 : esz * (size_t)T * h));
+  b.lg = off; off = align_up(off + (esz == 4 ? sizeof(float) * (size_t)T * E : 0));
   b.end = off;
   return b;
 }
@@ -157,12 +164,12 @@ int check_rows(int64_t T, int32_t h, int32_t k) {
 
 // Routed experts (+ the shared expert when sh_* weights are given and fused) from routing
 // indices/weights in device memory: permute, gate/up, down, combine.
-int run_experts(const void* x, const void* idx, bool idx64, const uint16_t* topk_w,
-                const void* w_gate_up, const void* w_down, const uint16_t* sh_gate,
-                const uint16_t* sh_up, const uint16_t* sh_down, const uint16_t* shared_out,
-                const uint16_t* gate, void* out, int64_t T, int32_t h, int32_t E, int32_t k,
+int run_experts(const void* x, const void* idx, bool idx64, const void* topk_w,
+                const void* w_gate_up, const void* w_down, const void* sh_gate,
+                const void* sh_up, const void* sh_down, const void* shared_out,
+                const void* gate, void* out, int64_t T, int32_t h, int32_t E, int32_t k,
                 int32_t I, int64_t shared_rows, const int32_t* hist_ready, void* ws,
-                const ExpertsWs& L, hipStream_t st) {
+                const ExpertsWs& L, hipStream_t st, bool f32 = false) {
   const int bm = q38::gemm_block_m();
   int32_t* hist = at<int32_t>(ws, L.hist);
   int32_t* counts = at<int32_t>(ws, L.counts);
@@ -171,8 +178,6 @@ int run_experts(const void* x, const void* idx, bool idx64, const uint16_t* topk
   int32_t* inv = at<int32_t>(ws, L.inv);
   int4* tiles = at<int4>(ws, L.tiles);
   int32_t* tile_count = at<int32_t>(ws, L.tile_count);
-  uint16_t* H = at<uint16_t>(ws, L.H);
-  uint16_t* Y = at<uint16_t>(ws, L.Y);
   const int64_t P = T * k;
   if (hist_ready == nullptr) {
     Q38_HIP(q38::launch_histogram(idx, idx64, hist, T, E, k, st), "histogram launch");
@@ -181,16 +186,39 @@ int run_experts(const void* x, const void* idx, bool idx64, const uint16_t* topk
   Q38_HIP(q38::launch_permute(idx, idx64, hist_ready, counts, starts, perm, inv, tiles, tile_count,
                               bm, (int)L.max_tiles, (int)shared_rows, T, E, k, st),
           "permute launch");
+  if (f32) {
+    // fp32 path: the same permutation and tile table, fp32 GEMMs and combine.
+    float* H = at<float>(ws, L.H);
+    float* Y = at<float>(ws, L.Y);
+    Q38_HIP(q38::launch_gate_up_f32(static_cast<const float*>(x), perm, tiles, tile_count, (int)L.max_tiles, 0,
+                                    (int)P, static_cast<const float*>(w_gate_up), static_cast<const float*>(sh_gate),
+                                    static_cast<const float*>(sh_up), H, I, h, E, k, st),
+            "gate_up fp32 launch");
+    Q38_HIP(q38::launch_plain_f32(H, tiles, tile_count, (int)L.max_tiles, 0, static_cast<const float*>(w_down),
+                                  static_cast<const float*>(sh_down), Y, h, I, E, st),
+            "down fp32 launch");
+    const float* shared = shared_out != nullptr ? static_cast<const float*>(shared_out)
+                                                : (shared_rows > 0 ? Y + P * h : nullptr);
+    Q38_HIP(q38::launch_combine_f32(Y, inv, idx, idx64, static_cast<const float*>(topk_w), shared,
+                                    static_cast<const float*>(gate), static_cast<float*>(out), T, h, E, k, st),
+            "combine fp32 launch");
+    return Q38MOE_OK;
+  }
+  uint16_t* H = at<uint16_t>(ws, L.H);
+  uint16_t* Y = at<uint16_t>(ws, L.Y);
   Q38_HIP(q38::launch_gate_up(static_cast<const uint16_t*>(x), perm, tiles, tile_count,
                               (int)L.max_tiles, 0, (int)P, static_cast<const uint16_t*>(w_gate_up),
-                              sh_gate, sh_up, H, I, h, E, k, st),
+                              static_cast<const uint16_t*>(sh_gate), static_cast<const uint16_t*>(sh_up), H, I, h, E,
+                              k, st),
           "gate_up launch");
   Q38_HIP(q38::launch_down(H, tiles, tile_count, (int)L.max_tiles, 0,
-                           static_cast<const uint16_t*>(w_down), sh_down, Y, h, I, E, st),
+                           static_cast<const uint16_t*>(w_down), static_cast<const uint16_t*>(sh_down), Y, h, I, E,
+                           st),
           "down launch");
-  const uint16_t* shared = shared_out != nullptr ? shared_out : (shared_rows > 0 ? Y + P * h : nullptr);
-  Q38_HIP(q38::launch_combine(Y, inv, idx, idx64, topk_w, shared, gate, static_cast<uint16_t*>(out),
-                              T, h, E, k, st),
+  const uint16_t* shared = shared_out != nullptr ? static_cast<const uint16_t*>(shared_out)
+                                                 : (shared_rows > 0 ? Y + P * h : nullptr);
+  Q38_HIP(q38::launch_combine(Y, inv, idx, idx64, static_cast<const uint16_t*>(topk_w), shared,
+                              static_cast<const uint16_t*>(gate), static_cast<uint16_t*>(out), T, h, E, k, st),
           "combine launch");
   return Q38MOE_OK;
 }
@@ -222,11 +250,42 @@ int check_block_args(const void* x, const void* w_router, const void* w_gate_up,
 int run_block(const void* x, const void* w_router, const void* w_gate_up, const void* w_down, const void* w_sh_gate,
               const void* w_sh_up, const void* w_sh_down, const void* w_sh_gate_proj, const float* logit_bias,
               void* out, void* logits, int32_t* topk_idx, void* topk_w, int64_t T, int32_t h, int32_t E, int32_t k,
-              int32_t I, int32_t Is, void* workspace, const BlockWs& L, hipStream_t st) {
+              int32_t I, int32_t Is, void* workspace, const BlockWs& L, hipStream_t st, bool f32 = false) {
   int32_t* idx = topk_idx != nullptr ? topk_idx : at<int32_t>(workspace, L.idx);
+  int32_t* hist = at<int32_t>(workspace, L.ex.hist);
+  if (f32) {
+    // fp32 block: router logits and the shared gate logit as dense fp32 GEMMs (modeling:807, 831),
+    // selection on them, shared expert (separate when Is != I), routed experts, gated sum.
+    const float* xf = static_cast<const float*>(x);
+    float* w = topk_w != nullptr ? static_cast<float*>(topk_w) : at<float>(workspace, L.w);
+    float* gate = at<float>(workspace, L.gate);
+    float* lg = logits != nullptr ? static_cast<float*>(logits) : at<float>(workspace, L.lg);
+    const float* sh_out = nullptr;
+    if (!L.fused) {
+      float* Hs = at<float>(workspace, L.Hs);
+      float* sh = at<float>(workspace, L.sh);
+      Q38_HIP(q38::launch_gate_up_f32(xf, nullptr, nullptr, nullptr, 0, T, 0, nullptr,
+                                      static_cast<const float*>(w_sh_gate), static_cast<const float*>(w_sh_up), Hs, Is,
+                                      h, 0, 1, st),
+              "shared gate_up fp32 launch");
+      Q38_HIP(q38::launch_plain_f32(Hs, nullptr, nullptr, 0, T, nullptr, static_cast<const float*>(w_sh_down), sh, h,
+                                    Is, 0, st),
+              "shared down fp32 launch");
+      sh_out = sh;
+    }
+    Q38_HIP(q38::launch_plain_f32(xf, nullptr, nullptr, 0, T, nullptr, static_cast<const float*>(w_router), lg, E, h,
+                                  0, st),
+            "router logits fp32 launch");
+    Q38_HIP(q38::launch_plain_f32(xf, nullptr, nullptr, 0, T, nullptr, static_cast<const float*>(w_sh_gate_proj),
+                                  gate, 1, h, 0, st),
+            "shared gate logit fp32 launch");
+    Q38_HIP(q38::launch_route_from_f32_logits(lg, logit_bias, idx, w, hist, T, E, k, st), "route fp32 launch");
+    return run_experts(x, idx, false, w, w_gate_up, w_down, L.fused ? w_sh_gate : nullptr,
+                       L.fused ? w_sh_up : nullptr, L.fused ? w_sh_down : nullptr, sh_out, gate, out, T, h, E, k, I,
+                       L.fused ? T : 0, hist, workspace, L.ex, st, true);
+  }
   uint16_t* w = topk_w != nullptr ? static_cast<uint16_t*>(topk_w) : at<uint16_t>(workspace, L.w);
   uint16_t* gate = at<uint16_t>(workspace, L.gate);
-  int32_t* hist = at<int32_t>(workspace, L.ex.hist);
   const uint16_t* xb = static_cast<const uint16_t*>(x);
   const uint16_t* sh_out = nullptr;
   if (!L.fused) {
@@ -247,10 +306,8 @@ int run_block(const void* x, const void* w_router, const void* w_gate_up, const 
                             nullptr, logit_bias, static_cast<uint16_t*>(logits), idx, w, gate, hist, T, h, E, k, st),
           "route launch");
   // Routed experts (+ the shared expert inside the same GEMMs) and the gated sum (modeling:829-833).
-  return run_experts(x, idx, false, w, w_gate_up, w_down,
-                     L.fused ? static_cast<const uint16_t*>(w_sh_gate) : nullptr,
-                     L.fused ? static_cast<const uint16_t*>(w_sh_up) : nullptr,
-                     L.fused ? static_cast<const uint16_t*>(w_sh_down) : nullptr, sh_out, gate, out, T, h, E, k, I,
+  return run_experts(x, idx, false, w, w_gate_up, w_down, L.fused ? w_sh_gate : nullptr,
+                     L.fused ? w_sh_up : nullptr, L.fused ? w_sh_down : nullptr, sh_out, gate, out, T, h, E, k, I,
                      L.fused ? T : 0, hist, workspace, L.ex, st);
 }
 
@@ -318,6 +375,23 @@ int q38moe_route(const void* x, const void* w_router, const void* w_shared_gate,
   if (shared_gate_logit != nullptr && w_shared_gate == nullptr)
     return fail(Q38MOE_EINVAL, "shared_gate_logit requires w_shared_gate");
   (void)hipGetLastError();
+  if (dtype == Q38MOE_FP32) {
+    // fp32: logits as a dense fp32 GEMM into the caller's logits buffer, then the selection on them.
+    if (logits == nullptr) return fail(Q38MOE_EINVAL, "dtype FP32: logits must not be NULL (the selection reads them)");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    Q38_HIP(q38::launch_plain_f32(static_cast<const float*>(x), nullptr, nullptr, 0, T, nullptr,
+                                  static_cast<const float*>(w_router), static_cast<float*>(logits), E, h, 0, st),
+            "router logits fp32 launch");
+    if (shared_gate_logit != nullptr)
+      Q38_HIP(q38::launch_plain_f32(static_cast<const float*>(x), nullptr, nullptr, 0, T, nullptr,
+                                    static_cast<const float*>(w_shared_gate), static_cast<float*>(shared_gate_logit), 1,
+                                    h, 0, st),
+              "shared gate logit fp32 launch");
+    Q38_HIP(q38::launch_route_from_f32_logits(static_cast<const float*>(logits), logit_bias, topk_idx,
+                                              static_cast<float*>(topk_w), hist, T, E, k, st),
+            "route fp32 launch");
+    return Q38MOE_OK;
+  }
   Q38_HIP(q38::launch_route(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w_router),
                             static_cast<const uint16_t*>(w_shared_gate), nullptr, logit_bias,
                             static_cast<uint16_t*>(logits), topk_idx, static_cast<uint16_t*>(topk_w),
@@ -337,6 +411,13 @@ int q38moe_route_from_logits(const void* logits, const float* logit_bias, int32_
   if (logits == nullptr || topk_idx == nullptr || topk_w == nullptr)
     return fail(Q38MOE_EINVAL, "logits, topk_idx and topk_w must not be NULL");
   (void)hipGetLastError();
+  if (dtype == Q38MOE_FP32) {
+    Q38_HIP(q38::launch_route_from_f32_logits(static_cast<const float*>(logits), logit_bias, topk_idx,
+                                              static_cast<float*>(topk_w), hist, T, E, k,
+                                              static_cast<hipStream_t>(stream)),
+            "route_from_logits fp32 launch");
+    return Q38MOE_OK;
+  }
   Q38_HIP(q38::launch_route(nullptr, nullptr, nullptr, static_cast<const uint16_t*>(logits),
                             logit_bias, nullptr, topk_idx, static_cast<uint16_t*>(topk_w), nullptr,
                             hist, T, 64, E, k, static_cast<hipStream_t>(stream)),
@@ -399,6 +480,15 @@ int q38moe_gate_up(const void* x, const void* w_gate_up, const void* w_sh_gate,
     Q38_CHECK(check_ptr(w_sh_up, "w_sh_up"));
   }
   (void)hipGetLastError();
+  if (dtype == Q38MOE_FP32) {
+    Q38_HIP(q38::launch_gate_up_f32(static_cast<const float*>(x), perm, reinterpret_cast<const int4*>(tiles),
+                                    tile_count, (int)max_tiles_impl(T, E, k, shared_rows), 0, (int)(T * k),
+                                    static_cast<const float*>(w_gate_up), static_cast<const float*>(w_sh_gate),
+                                    static_cast<const float*>(w_sh_up), static_cast<float*>(H), I, h, E, k,
+                                    static_cast<hipStream_t>(stream)),
+            "gate_up fp32 launch");
+    return Q38MOE_OK;
+  }
   Q38_HIP(q38::launch_gate_up(static_cast<const uint16_t*>(x), perm, reinterpret_cast<const int4*>(tiles),
                               tile_count, (int)max_tiles_impl(T, E, k, shared_rows), 0, (int)(T * k),
                               static_cast<const uint16_t*>(w_gate_up), static_cast<const uint16_t*>(w_sh_gate),
@@ -426,6 +516,14 @@ int q38moe_down(const void* H, const void* w_down, const void* w_sh_down, const 
   if (shared_rows < 0 || shared_rows > T) return fail(Q38MOE_EINVAL, "shared_rows must be in [0, T]");
   if (shared_rows > 0) Q38_CHECK(check_ptr(w_sh_down, "w_sh_down"));
   (void)hipGetLastError();
+  if (dtype == Q38MOE_FP32) {
+    Q38_HIP(q38::launch_plain_f32(static_cast<const float*>(H), reinterpret_cast<const int4*>(tiles), tile_count,
+                                  (int)max_tiles_impl(T, E, k, shared_rows), 0, static_cast<const float*>(w_down),
+                                  static_cast<const float*>(w_sh_down), static_cast<float*>(Y), h, I, E,
+                                  static_cast<hipStream_t>(stream)),
+            "down fp32 launch");
+    return Q38MOE_OK;
+  }
   Q38_HIP(q38::launch_down(static_cast<const uint16_t*>(H), reinterpret_cast<const int4*>(tiles), tile_count,
                            (int)max_tiles_impl(T, E, k, shared_rows), 0, static_cast<const uint16_t*>(w_down),
                            static_cast<const uint16_t*>(w_sh_down), static_cast<uint16_t*>(Y), h, I, E,
@@ -575,6 +673,16 @@ int q38moe_shared_expert(const void* x, const void* w_gate, const void* w_up,
   Q38_CHECK(check_ptr(out, "out"));
   (void)hipGetLastError();
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == Q38MOE_FP32) {
+    Q38_HIP(q38::launch_gate_up_f32(static_cast<const float*>(x), nullptr, nullptr, nullptr, 0, T, 0, nullptr,
+                                    static_cast<const float*>(w_gate), static_cast<const float*>(w_up),
+                                    static_cast<float*>(Hs), Is, h, 0, 1, st),
+            "shared gate_up fp32 launch");
+    Q38_HIP(q38::launch_plain_f32(static_cast<const float*>(Hs), nullptr, nullptr, 0, T, nullptr,
+                                  static_cast<const float*>(w_down), static_cast<float*>(out), h, Is, 0, st),
+            "shared down fp32 launch");
+    return Q38MOE_OK;
+  }
   Q38_HIP(q38::launch_gate_up(static_cast<const uint16_t*>(x), nullptr, nullptr, nullptr, 0, T, 0, nullptr,
                               static_cast<const uint16_t*>(w_gate), static_cast<const uint16_t*>(w_up),
                               static_cast<uint16_t*>(Hs), Is, h, 0, 1, st),
@@ -602,6 +710,14 @@ int q38moe_combine(const void* Y, const int32_t* inv, const void* topk_idx, int3
   if (shared_out != nullptr && shared_gate_logit == nullptr)
     return fail(Q38MOE_EINVAL, "shared_out requires shared_gate_logit");
   (void)hipGetLastError();
+  if (dtype == Q38MOE_FP32) {
+    Q38_HIP(q38::launch_combine_f32(static_cast<const float*>(Y), inv, topk_idx, idx_is_int64 != 0,
+                                    static_cast<const float*>(topk_w), static_cast<const float*>(shared_out),
+                                    static_cast<const float*>(shared_gate_logit), static_cast<float*>(out), T, h, E,
+                                    k, static_cast<hipStream_t>(stream)),
+            "combine fp32 launch");
+    return Q38MOE_OK;
+  }
   Q38_HIP(q38::launch_combine(static_cast<const uint16_t*>(Y), inv, topk_idx, idx_is_int64 != 0,
                               static_cast<const uint16_t*>(topk_w), static_cast<const uint16_t*>(shared_out),
                               static_cast<const uint16_t*>(shared_gate_logit), static_cast<uint16_t*>(out), T, h,
@@ -610,14 +726,15 @@ int q38moe_combine(const void* Y, const int32_t* inv, const void* topk_idx, int3
   return Q38MOE_OK;
 }
 
-int q38moe_experts_workspace_bytes(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
+int q38moe_experts_workspace_bytes(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int32_t dtype,
                                    size_t* bytes) {
   g_err[0] = 0;
+  Q38_CHECK(check_dtype(dtype));
   Q38_CHECK(check_routing(T, E, k));
   Q38_CHECK(check_dim(h, "h"));
   Q38_CHECK(check_dim(I, "I"));
   if (bytes == nullptr) return fail(Q38MOE_EINVAL, "bytes must not be NULL");
-  *bytes = experts_layout(T, h, E, k, I, 0).end;
+  *bytes = experts_layout(T, h, E, k, I, 0, elem_size(dtype)).end;
   return Q38MOE_OK;
 }
 
@@ -637,26 +754,27 @@ int q38moe_experts_forward(const void* x, const void* topk_idx, int32_t idx_is_i
   Q38_CHECK(check_ptr(w_down, "w_down"));
   Q38_CHECK(check_ptr(out, "out"));
   if (topk_idx == nullptr || topk_w == nullptr) return fail(Q38MOE_EINVAL, "topk_idx and topk_w must not be NULL");
-  const ExpertsWs L = experts_layout(T, h, E, k, I, 0);
+  const ExpertsWs L = experts_layout(T, h, E, k, I, 0, elem_size(dtype));
   if (workspace == nullptr || workspace_bytes < L.end)
     return fail(Q38MOE_EWORKSPACE, "workspace needs %zu bytes (got %zu)", L.end, workspace_bytes);
   if (reinterpret_cast<uintptr_t>(workspace) % kAlign != 0)
     return fail(Q38MOE_EINVAL, "workspace must be 256-byte aligned");
   (void)hipGetLastError();
-  return run_experts(x, topk_idx, idx_is_int64 != 0, static_cast<const uint16_t*>(topk_w), w_gate_up, w_down,
-                     nullptr, nullptr, nullptr, nullptr, nullptr, out, T, h, E, k, I, 0, nullptr, workspace, L,
-                     static_cast<hipStream_t>(stream));
+  return run_experts(x, topk_idx, idx_is_int64 != 0, topk_w, w_gate_up, w_down, nullptr, nullptr, nullptr,
+                     nullptr, nullptr, out, T, h, E, k, I, 0, nullptr, workspace, L, static_cast<hipStream_t>(stream),
+                     dtype == Q38MOE_FP32);
 }
 
 int q38moe_block_workspace_bytes(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I,
-                                 int32_t Is, size_t* bytes) {
+                                 int32_t Is, int32_t dtype, size_t* bytes) {
   g_err[0] = 0;
+  Q38_CHECK(check_dtype(dtype));
   Q38_CHECK(check_routing(T, E, k));
   Q38_CHECK(check_dim(h, "h"));
   Q38_CHECK(check_dim(I, "I"));
   Q38_CHECK(check_dim(Is, "Is"));
   if (bytes == nullptr) return fail(Q38MOE_EINVAL, "bytes must not be NULL");
-  *bytes = block_layout(T, h, E, k, I, Is).end;
+  *bytes = block_layout(T, h, E, k, I, Is, elem_size(dtype)).end;
   return Q38MOE_OK;
 }
 
@@ -671,14 +789,15 @@ int q38moe_block_forward(const void* x, const void* w_router, const void* w_gate
   Q38_CHECK(check_block_args(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_sh_down, w_sh_gate_proj, out, T,
                              h, E, k, I, Is, dtype));
   if (T == 0) return Q38MOE_OK;
-  const BlockWs L = block_layout(T, h, E, k, I, Is);
+  const BlockWs L = block_layout(T, h, E, k, I, Is, elem_size(dtype));
   if (workspace == nullptr || workspace_bytes < L.end)
     return fail(Q38MOE_EWORKSPACE, "workspace needs %zu bytes (got %zu)", L.end, workspace_bytes);
   if (reinterpret_cast<uintptr_t>(workspace) % kAlign != 0)
     return fail(Q38MOE_EINVAL, "workspace must be 256-byte aligned");
   (void)hipGetLastError();
   return run_block(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_sh_down, w_sh_gate_proj, logit_bias, out,
-                   logits, topk_idx, topk_w, T, h, E, k, I, Is, workspace, L, static_cast<hipStream_t>(stream));
+                   logits, topk_idx, topk_w, T, h, E, k, I, Is, workspace, L, static_cast<hipStream_t>(stream),
+                   dtype == Q38MOE_FP32);
 }
 
 size_t q38moe_block_noalloc_scratch_bytes(void) { return kScratchBytes; }
@@ -693,7 +812,7 @@ int q38moe_block_forward_noalloc(const void* x, const void* w_router, const void
   Q38_CHECK(check_block_args(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_sh_down, w_sh_gate_proj, out, T,
                              h, E, k, I, Is, dtype));
   if (T == 0) return Q38MOE_OK;
-  const BlockWs L = block_layout(T, h, E, k, I, Is);
+  const BlockWs L = block_layout(T, h, E, k, I, Is, elem_size(dtype));
   if (L.end > kScratchBytes)
     return fail(Q38MOE_EWORKSPACE,
                 "q38moe_block_forward_noalloc: this shape needs %zu bytes of scratch, the static scratch holds %zu "
@@ -703,7 +822,8 @@ int q38moe_block_forward_noalloc(const void* x, const void* w_router, const void
   Q38_CHECK(scratch_for_current_device(static_cast<hipStream_t>(stream), &ws));
   (void)hipGetLastError();
   return run_block(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_sh_down, w_sh_gate_proj, logit_bias, out,
-                   logits, topk_idx, topk_w, T, h, E, k, I, Is, ws, L, static_cast<hipStream_t>(stream));
+                   logits, topk_idx, topk_w, T, h, E, k, I, Is, ws, L, static_cast<hipStream_t>(stream),
+                   dtype == Q38MOE_FP32);
 }
 
 // ---- fp8 expert path (R14) --------------------------------------------------------------------

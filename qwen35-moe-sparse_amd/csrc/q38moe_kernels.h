@@ -10,6 +10,23 @@ hipError_t launch_route(const uint16_t* x, const uint16_t* wr, const uint16_t* w
                         int32_t* idx_out, uint16_t* w_out, uint16_t* gate_out, int32_t* hist,
                         int64_t T, int h, int E, int k, hipStream_t stream);
 
+// Selection from fp32 logits (the fp32 path): fp32 renormalised weights out.
+hipError_t launch_route_from_f32_logits(const float* logits, const float* bias, int32_t* idx_out, float* w_out,
+                                        int32_t* hist, int64_t T, int E, int k, hipStream_t stream);
+
+// fp32 path (q38moe_fp32.hip): gate/up + SwiGLU and plain GEMMs (down, dense router logits) on fp32
+// MFMA over the same tile table (tiles != nullptr) or dense rows [0, M_dense) with the weights Ws
+// (Ws_a/Ws_b), and the fp32 combine.
+hipError_t launch_gate_up_f32(const float* x, const int32_t* perm, const int4* tiles, const int32_t* ntiles_dev,
+                              int max_mtiles, int64_t M_dense, int P, const float* w_gate_up, const float* ws_gate,
+                              const float* ws_up, float* H, int N, int K, int E, int topk, hipStream_t stream);
+hipError_t launch_plain_f32(const float* A, const int4* tiles, const int32_t* ntiles_dev, int max_mtiles,
+                            int64_t M_dense, const float* W, const float* Ws, float* C, int N, int K, int E,
+                            hipStream_t stream);
+hipError_t launch_combine_f32(const float* Y, const int32_t* inv, const void* idx, bool idx64, const float* w,
+                              const float* shared, const float* gate, float* out, int64_t T, int h, int E, int k,
+                              hipStream_t stream);
+
 hipError_t launch_histogram(const void* idx, bool idx64, int32_t* hist, int64_t T, int E, int k,
                             hipStream_t stream);
 

@@ -553,12 +553,15 @@ constexpr int ROUTE_THREADS = 512;  // 8 waves: 0-3 multiply, all select and rep
 
 // KT = k (1..KMAX) as a template parameter: each instantiation carries only its own selection
 // network, which keeps the kernel's code within the instruction cache.
-template <int KT>
+// F32IO: the fp32 path (fp32 models): logits come in as fp32 (logits_in, computed by the fp32
+// router GEMM) and the renormalised weights leave as fp32 (no bf16 rounding, modeling:812 with
+// the fp32 logits dtype); x is unused.
+template <int KT, bool F32IO>
 __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
-    const uint16_t* __restrict__ wsg, const uint16_t* __restrict__ logits_in,
+    const uint16_t* __restrict__ wsg, const void* __restrict__ logits_in,
     const float* __restrict__ bias, uint16_t* __restrict__ logits_out,
-    int32_t* __restrict__ idx_out, uint16_t* __restrict__ w_out,
+    int32_t* __restrict__ idx_out, void* __restrict__ w_out,
     uint16_t* __restrict__ gate_out, int32_t* __restrict__ hist, int64_t T, int h, int E, int k) {
   __shared__ __attribute__((aligned(16))) u32x4_t s_w[ROUTE_WROWS * (ROUTE_KCHUNK / 8)];
   // Row stride 72 (= 8 mod 64 banks): the selection's 8 lanes x 8 tokens per wave read 64
@@ -579,7 +582,7 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
   }
   if (tid == 0) s_nties = 0;
 
-  if (logits_in == nullptr) {
+  if (!F32IO && logits_in == nullptr) {
     const int ntile = (E + 15) >> 4;
     const bool gate_tile = wsg != nullptr;
     const int nrows_w = gate_tile ? ROUTE_WROWS : 64;
@@ -659,7 +662,10 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     for (int i = tid; i < ROUTE_TOKENS * E; i += ROUTE_THREADS) {
       const int tl = i / E, e = i - tl * E;
       const int64_t t = tb + tl;
-      s_logit[tl][e] = t < T ? bf16_to_f32(logits_in[t * E + e]) : 0.0f;
+      if (F32IO)
+        s_logit[tl][e] = t < T ? static_cast<const float*>(logits_in)[t * E + e] : 0.0f;
+      else
+        s_logit[tl][e] = t < T ? bf16_to_f32(static_cast<const uint16_t*>(logits_in)[t * E + e]) : 0.0f;
     }
   }
   __syncthreads();
@@ -689,7 +695,8 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
         if (ok) {
           for (int r = 0; r < k; ++r) {
             idx_out[t * k + r] = oi[r];
-            w_out[t * k + r] = (uint16_t)f32_to_bf16_rne(ow[r]);
+            if (F32IO) static_cast<float*>(w_out)[t * k + r] = ow[r];
+            else static_cast<uint16_t*>(w_out)[t * k + r] = (uint16_t)f32_to_bf16_rne(ow[r]);
             atomicAdd(&s_hist[oi[r]], 1);
           }
         } else {
@@ -711,7 +718,8 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     route_token<KT>(z, lane, E, oi, ow, s_sv[wave], s_si[wave]);
     if (lane < k) {
       idx_out[t * k + lane] = oi;
-      w_out[t * k + lane] = (uint16_t)f32_to_bf16_rne(ow);
+      if (F32IO) static_cast<float*>(w_out)[t * k + lane] = ow;
+      else static_cast<uint16_t*>(w_out)[t * k + lane] = (uint16_t)f32_to_bf16_rne(ow);
       atomicAdd(&s_hist[oi], 1);
     }
   }
@@ -725,10 +733,27 @@ hipError_t launch_route(const uint16_t* x, const uint16_t* wr, const uint16_t* w
                         int64_t T, int h, int E, int k, hipStream_t stream) {
   const int64_t nblk = (T + ROUTE_TOKENS - 1) / ROUTE_TOKENS;
   if (nblk == 0) return hipSuccess;
-#define Q38_ROUTE(KT)                                                                                  \
-  case KT:                                                                                             \
-    hipLaunchKernelGGL(route_kernel<KT>, dim3((unsigned)nblk), dim3(ROUTE_THREADS), 0, stream, x, wr, wsg, \
-                       logits_in, bias, logits_out, idx_out, w_out, gate_out, hist, T, h, E, k);         \
+#define Q38_ROUTE(KT)                                                                                         \
+  case KT:                                                                                                    \
+    hipLaunchKernelGGL((route_kernel<KT, false>), dim3((unsigned)nblk), dim3(ROUTE_THREADS), 0, stream, x, wr, \
+                       wsg, logits_in, bias, logits_out, idx_out, w_out, gate_out, hist, T, h, E, k);         \
+    break;
+  switch (k) {
+    Q38_ROUTE(1) Q38_ROUTE(2) Q38_ROUTE(3) Q38_ROUTE(4) Q38_ROUTE(5) Q38_ROUTE(6) Q38_ROUTE(7) Q38_ROUTE(8)
+    default: return hipErrorInvalidValue;
+  }
+#undef Q38_ROUTE
+  return hipGetLastError();
+}
+
+hipError_t launch_route_from_f32_logits(const float* logits, const float* bias, int32_t* idx_out, float* w_out,
+                                        int32_t* hist, int64_t T, int E, int k, hipStream_t stream) {
+  const int64_t nblk = (T + ROUTE_TOKENS - 1) / ROUTE_TOKENS;
+  if (nblk == 0) return hipSuccess;
+#define Q38_ROUTE(KT)                                                                                        \
+  case KT:                                                                                                   \
+    hipLaunchKernelGGL((route_kernel<KT, true>), dim3((unsigned)nblk), dim3(ROUTE_THREADS), 0, stream, nullptr, \
+                       nullptr, nullptr, logits, bias, nullptr, idx_out, w_out, nullptr, hist, T, 64, E, k);  \
     break;
   switch (k) {
     Q38_ROUTE(1) Q38_ROUTE(2) Q38_ROUTE(3) Q38_ROUTE(4) Q38_ROUTE(5) Q38_ROUTE(6) Q38_ROUTE(7) Q38_ROUTE(8)

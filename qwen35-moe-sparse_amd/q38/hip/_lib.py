@@ -12,8 +12,9 @@ import torch  # noqa: F401  (loads the HIP runtime first)
 
 LIB_PATH = Path(os.environ.get("Q38MOE_LIB", Path(__file__).resolve().parent / "libq38moe.so"))
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 BF16 = 1
+FP32 = 2
 
 _c_int, _c_i32, _c_i64, _c_size, _vp = ctypes.c_int, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
 
@@ -36,10 +37,11 @@ SIGNATURES = {
     "q38moe_shared_expert": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _c_i32, _vp]),
     "q38moe_combine": (_c_int, [_vp, _vp, _vp, _c_i32, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,
                                 _vp]),
-    "q38moe_experts_workspace_bytes": (_c_int, [_c_i64, _c_i32, _c_i32, _c_i32, _c_i32, ctypes.POINTER(_c_size)]),
+    "q38moe_experts_workspace_bytes": (_c_int, [_c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+                                                ctypes.POINTER(_c_size)]),
     "q38moe_experts_forward": (_c_int, [_vp, _vp, _c_i32, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _c_i32,
                                         _c_i32, _vp, _c_size, _c_i32, _vp]),
-    "q38moe_block_workspace_bytes": (_c_int, [_c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+    "q38moe_block_workspace_bytes": (_c_int, [_c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                                               ctypes.POINTER(_c_size)]),
     "q38moe_block_forward": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                       _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _vp, _c_size, _c_i32, _vp]),

@@ -1,15 +1,17 @@
 """Torch-tensor front end of the C ABI: shape/dtype checks, output allocation, stream passing.
 
 Every function launches HIP kernels on the current torch stream of the input's device and
-returns without synchronising. Inputs must be contiguous bf16 CUDA (HIP) tensors; weights use the
-reference parameter layouts (experts.gate_up_proj [E,2I,h], experts.down_proj [E,h,I],
-nn.Linear weights [out,in]).
+returns without synchronising. Inputs must be contiguous CUDA (HIP) tensors in bf16, or, for the
+forward path (router, permutation, grouped GEMMs, combine, experts, block), fp32 (the fp32 models
+of the reference, computed without intermediate roundings); the activations' dtype decides and the
+weights must share it. Weights use the reference parameter layouts (experts.gate_up_proj [E,2I,h],
+experts.down_proj [E,h,I], nn.Linear weights [out,in]).
 """
 import ctypes
 
 import torch
 
-from ._lib import BF16, check, lib
+from ._lib import BF16, FP32, check, lib
 
 _NULL = None
 
@@ -36,6 +38,16 @@ def _need(t, name, dtype=torch.bfloat16, ndim=None):
     return t
 
 
+_DTYPES = {torch.bfloat16: BF16, torch.float32: FP32}
+
+
+def _fdt(t, name):
+    """The float dtype of the forward path given by tensor t (bf16 or fp32)."""
+    if not isinstance(t, torch.Tensor) or t.dtype not in _DTYPES:
+        raise TypeError(f"{name} must be a bf16 or fp32 tensor, got {getattr(t, 'dtype', type(t))}")
+    return t.dtype
+
+
 def _idx_flag(idx):
     if idx.dtype == torch.int64:
         return 1
@@ -53,46 +65,50 @@ def max_tiles(T, E, k, shared_rows=0):
 
 
 def route(x, w_router, k, w_shared_gate=None, logit_bias=None, want_logits=False, want_hist=False):
-    """Router (modeling:805-813). Returns (logits|None, idx int32 [T,k], w bf16 [T,k],
-    shared_gate_logit bf16 [T]|None, hist int32 [ceil(T/64),E]|None)."""
-    _need(x, "x", ndim=2)
-    _need(w_router, "w_router", ndim=2)
+    """Router (modeling:805-813). Returns (logits|None, idx int32 [T,k], w [T,k],
+    shared_gate_logit [T]|None, hist int32 [ceil(T/64),E]|None); floats in x's dtype (bf16/fp32)."""
+    dt = _fdt(x, "x")
+    _need(x, "x", dtype=dt, ndim=2)
+    _need(w_router, "w_router", dtype=dt, ndim=2)
     T, h = x.shape
     E = w_router.shape[0]
     if w_router.shape[1] != h:
         raise ValueError(f"w_router {tuple(w_router.shape)} does not match hidden {h}")
     dev = x.device
     if w_shared_gate is not None:
-        _need(w_shared_gate, "w_shared_gate")
+        _need(w_shared_gate, "w_shared_gate", dtype=dt)
         if w_shared_gate.numel() != h:
             raise ValueError("w_shared_gate must hold h elements")
     if logit_bias is not None:
         _need(logit_bias, "logit_bias", dtype=torch.float32, ndim=1)
         if logit_bias.numel() != E:
             raise ValueError("logit_bias must hold E elements")
-    logits = torch.empty(T, E, dtype=torch.bfloat16, device=dev) if want_logits else None
+    # fp32: the selection reads the logits back, so they are always materialised.
+    logits = torch.empty(T, E, dtype=dt, device=dev) if want_logits or dt == torch.float32 else None
     idx = torch.empty(T, k, dtype=torch.int32, device=dev)
-    w = torch.empty(T, k, dtype=torch.bfloat16, device=dev)
-    gate = torch.empty(T, dtype=torch.bfloat16, device=dev) if w_shared_gate is not None else None
+    w = torch.empty(T, k, dtype=dt, device=dev)
+    gate = torch.empty(T, dtype=dt, device=dev) if w_shared_gate is not None else None
     hist = torch.empty((T + 63) // 64, E, dtype=torch.int32, device=dev) if want_hist else None
     check(lib.q38moe_route(_ptr(x), _ptr(w_router), _ptr(w_shared_gate), _ptr(logit_bias), _ptr(logits),
-                           _ptr(idx), _ptr(w), _ptr(gate), _ptr(hist), T, h, E, k, BF16, _stream(dev)),
+                           _ptr(idx), _ptr(w), _ptr(gate), _ptr(hist), T, h, E, k, _DTYPES[dt], _stream(dev)),
           "q38moe_route")
-    return logits, idx, w, gate, hist
+    return (logits if want_logits else None), idx, w, gate, hist
 
 
 def route_from_logits(logits, k, logit_bias=None, want_hist=False):
-    """Router selection (modeling:808-812) on given bf16 logits [T,E]: (idx int32, w bf16, hist)."""
-    _need(logits, "logits", ndim=2)
+    """Router selection (modeling:808-812) on given bf16 or fp32 logits [T,E]: (idx int32, w in the
+    logits' dtype, hist)."""
+    dt = _fdt(logits, "logits")
+    _need(logits, "logits", dtype=dt, ndim=2)
     T, E = logits.shape
     dev = logits.device
     if logit_bias is not None:
         _need(logit_bias, "logit_bias", dtype=torch.float32, ndim=1)
     idx = torch.empty(T, k, dtype=torch.int32, device=dev)
-    w = torch.empty(T, k, dtype=torch.bfloat16, device=dev)
+    w = torch.empty(T, k, dtype=dt, device=dev)
     hist = torch.empty((T + 63) // 64, E, dtype=torch.int32, device=dev) if want_hist else None
     check(lib.q38moe_route_from_logits(_ptr(logits), _ptr(logit_bias), _ptr(idx), _ptr(w), _ptr(hist),
-                                       T, E, k, BF16, _stream(dev)), "q38moe_route_from_logits")
+                                       T, E, k, _DTYPES[dt], _stream(dev)), "q38moe_route_from_logits")
     return idx, w, hist
 
 
@@ -130,9 +146,11 @@ def permute(idx, hist, E, shared_rows=0):
 
 def gate_up(x, w_gate_up, perm, tiles, tile_count, k, shared_weights=None, shared_rows=0):
     """Grouped gate/up GEMM + SwiGLU (inference.py:60-96): H [T*k + shared_rows, I] bf16, rows in
-    expert-sorted order then the shared-expert rows (shared_weights = (gate_proj.weight, up_proj.weight))."""
-    _need(x, "x", ndim=2)
-    _need(w_gate_up, "w_gate_up", ndim=3)
+    expert-sorted order then the shared-expert rows (shared_weights = (gate_proj.weight, up_proj.weight));
+    fp32 inputs give fp32 H (no roundings)."""
+    dt = _fdt(x, "x")
+    _need(x, "x", dtype=dt, ndim=2)
+    _need(w_gate_up, "w_gate_up", dtype=dt, ndim=3)
     _need(perm, "perm", dtype=torch.int32)
     _need(tiles, "tiles", dtype=torch.int32, ndim=2)
     T, h = x.shape
@@ -145,20 +163,22 @@ def gate_up(x, w_gate_up, perm, tiles, tile_count, k, shared_weights=None, share
     wg = wu = None
     if shared_rows:
         wg, wu = shared_weights
-        _need(wg, "shared gate_proj", ndim=2)
-        _need(wu, "shared up_proj", ndim=2)
+        _need(wg, "shared gate_proj", dtype=dt, ndim=2)
+        _need(wu, "shared up_proj", dtype=dt, ndim=2)
         if wg.shape != (I, h) or wu.shape != (I, h):
             raise ValueError("the shared expert runs inside the grouped GEMM only when its width equals I")
-    H = torch.empty(T * k + shared_rows, I, dtype=torch.bfloat16, device=x.device)
+    H = torch.empty(T * k + shared_rows, I, dtype=dt, device=x.device)
     check(lib.q38moe_gate_up(_ptr(x), _ptr(w_gate_up), _ptr(wg), _ptr(wu), _ptr(perm), _ptr(tiles), _ptr(tile_count),
-                             shared_rows, _ptr(H), T, h, E, k, I, BF16, _stream(x.device)), "q38moe_gate_up")
+                             shared_rows, _ptr(H), T, h, E, k, I, _DTYPES[dt], _stream(x.device)), "q38moe_gate_up")
     return H
 
 
 def down(H, w_down, tiles, tile_count, T, k, w_shared_down=None, shared_rows=0):
-    """Grouped down GEMM (inference.py:99-127, routing weight left to combine): Y [rows, h] bf16."""
-    _need(H, "H", ndim=2)
-    _need(w_down, "w_down", ndim=3)
+    """Grouped down GEMM (inference.py:99-127, routing weight left to combine): Y [rows, h] in H's
+    dtype (bf16 or fp32)."""
+    dt = _fdt(H, "H")
+    _need(H, "H", dtype=dt, ndim=2)
+    _need(w_down, "w_down", dtype=dt, ndim=3)
     _need(tiles, "tiles", dtype=torch.int32, ndim=2)
     E, h, I = w_down.shape
     if H.shape != (T * k + shared_rows, I):
@@ -166,35 +186,38 @@ def down(H, w_down, tiles, tile_count, T, k, w_shared_down=None, shared_rows=0):
     if tiles.shape[0] != max_tiles(T, E, k, shared_rows):
         raise ValueError("tiles was not built for this shape")
     if shared_rows:
-        _need(w_shared_down, "shared down_proj", ndim=2)
-    Y = torch.empty(T * k + shared_rows, h, dtype=torch.bfloat16, device=H.device)
+        _need(w_shared_down, "shared down_proj", dtype=dt, ndim=2)
+    Y = torch.empty(T * k + shared_rows, h, dtype=dt, device=H.device)
     check(lib.q38moe_down(_ptr(H), _ptr(w_down), _ptr(w_shared_down), _ptr(tiles), _ptr(tile_count), shared_rows,
-                          _ptr(Y), T, h, E, k, I, BF16, _stream(H.device)), "q38moe_down")
+                          _ptr(Y), T, h, E, k, I, _DTYPES[dt], _stream(H.device)), "q38moe_down")
     return Y
 
 
 def shared_expert(x, w_gate, w_up, w_down):
-    """Qwen3_8MoeMLP.forward (modeling:751-753) on x [T,h]: [T,h] bf16."""
-    _need(x, "x", ndim=2)
+    """Qwen3_8MoeMLP.forward (modeling:751-753) on x [T,h]: [T,h] in x's dtype (bf16 or fp32)."""
+    dt = _fdt(x, "x")
+    _need(x, "x", dtype=dt, ndim=2)
     for t, n in ((w_gate, "w_gate"), (w_up, "w_up"), (w_down, "w_down")):
-        _need(t, n, ndim=2)
+        _need(t, n, dtype=dt, ndim=2)
     T, h = x.shape
     Is = w_gate.shape[0]
     if w_gate.shape != (Is, h) or w_up.shape != (Is, h) or w_down.shape != (h, Is):
         raise ValueError("shared expert weights must be [Is,h], [Is,h], [h,Is]")
-    Hs = torch.empty(T, Is, dtype=torch.bfloat16, device=x.device)
-    out = torch.empty(T, h, dtype=torch.bfloat16, device=x.device)
+    Hs = torch.empty(T, Is, dtype=dt, device=x.device)
+    out = torch.empty(T, h, dtype=dt, device=x.device)
     check(lib.q38moe_shared_expert(_ptr(x), _ptr(w_gate), _ptr(w_up), _ptr(w_down), _ptr(Hs), _ptr(out), T, h,
-                                   Is, BF16, _stream(x.device)), "q38moe_shared_expert")
+                                   Is, _DTYPES[dt], _stream(x.device)), "q38moe_shared_expert")
     return out
 
 
 def combine(Y, inv, topk_w, E, idx=None, shared_out=None, shared_gate_logit=None):
     """out[t] = bf16(sum_j bf16(Y[inv[t*k+j]] * w[t,j])) (inference.py:128-130,199), optionally plus
-    the sigmoid-gated shared-expert row (modeling:831-833)."""
-    _need(Y, "Y", ndim=2)
+    the sigmoid-gated shared-expert row (modeling:831-833); fp32 Y gives the fp32 sum without
+    roundings."""
+    dt = _fdt(Y, "Y")
+    _need(Y, "Y", dtype=dt, ndim=2)
     _need(inv, "inv", dtype=torch.int32)
-    _need(topk_w, "topk_w", ndim=2)
+    _need(topk_w, "topk_w", dtype=dt, ndim=2)
     T, k = topk_w.shape
     h = Y.shape[1]
     flag = 0
@@ -202,11 +225,11 @@ def combine(Y, inv, topk_w, E, idx=None, shared_out=None, shared_gate_logit=None
         _need(idx, "topk_idx", dtype=None, ndim=2)
         flag = _idx_flag(idx)
     if shared_out is not None:
-        _need(shared_out, "shared_out", ndim=2)
-        _need(shared_gate_logit, "shared_gate_logit")
-    out = torch.empty(T, h, dtype=torch.bfloat16, device=Y.device)
+        _need(shared_out, "shared_out", dtype=dt, ndim=2)
+        _need(shared_gate_logit, "shared_gate_logit", dtype=dt)
+    out = torch.empty(T, h, dtype=dt, device=Y.device)
     check(lib.q38moe_combine(_ptr(Y), _ptr(inv), _ptr(idx), flag, _ptr(topk_w), _ptr(shared_out),
-                             _ptr(shared_gate_logit), _ptr(out), T, h, E, k, BF16, _stream(Y.device)),
+                             _ptr(shared_gate_logit), _ptr(out), T, h, E, k, _DTYPES[dt], _stream(Y.device)),
           "q38moe_combine")
     return out
 
@@ -315,52 +338,58 @@ def swiglu_backward(dH, GU):
     return dGU
 
 
-def experts_workspace_bytes(T, h, E, k, I):
+def experts_workspace_bytes(T, h, E, k, I, dtype=torch.bfloat16):
     n = ctypes.c_size_t()
-    check(lib.q38moe_experts_workspace_bytes(T, h, E, k, I, ctypes.byref(n)), "q38moe_experts_workspace_bytes")
+    check(lib.q38moe_experts_workspace_bytes(T, h, E, k, I, _DTYPES[dtype], ctypes.byref(n)),
+          "q38moe_experts_workspace_bytes")
     return n.value
 
 
 def experts_forward(x, topk_idx, topk_w, w_gate_up, w_down, workspace=None):
-    """Routed experts (ExpertsInterface contract, integrations/moe.py:567-570): [T,h] bf16."""
-    _need(x, "hidden_states", ndim=2)
+    """Routed experts (ExpertsInterface contract, integrations/moe.py:567-570): [T,h] in the
+    activations' dtype (bf16, or fp32 without intermediate roundings)."""
+    dt = _fdt(x, "hidden_states")
+    _need(x, "hidden_states", dtype=dt, ndim=2)
     _need(topk_idx, "top_k_index", dtype=None, ndim=2)
-    _need(topk_w, "top_k_weights", ndim=2)
-    _need(w_gate_up, "gate_up_proj", ndim=3)
-    _need(w_down, "down_proj", ndim=3)
+    _need(topk_w, "top_k_weights", dtype=dt, ndim=2)
+    _need(w_gate_up, "gate_up_proj", dtype=dt, ndim=3)
+    _need(w_down, "down_proj", dtype=dt, ndim=3)
     T, h = x.shape
     k = topk_idx.shape[1]
     E, twoI, _ = w_gate_up.shape
     I = twoI // 2
     if topk_w.shape != topk_idx.shape or topk_idx.shape[0] != T:
         raise ValueError("top_k_index/top_k_weights must both be [T,k]")
-    nbytes = experts_workspace_bytes(T, h, E, k, I)
-    if workspace is None:
+    nbytes = experts_workspace_bytes(T, h, E, k, I, dt)
+    if workspace is None or workspace.numel() < nbytes:
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
-    out = torch.empty(T, h, dtype=torch.bfloat16, device=x.device)
+    out = torch.empty(T, h, dtype=dt, device=x.device)
     check(lib.q38moe_experts_forward(_ptr(x), _ptr(topk_idx), _idx_flag(topk_idx), _ptr(topk_w), _ptr(w_gate_up),
                                      _ptr(w_down), _ptr(out), T, h, E, k, I, _ptr(workspace), workspace.numel(),
-                                     BF16, _stream(x.device)), "q38moe_experts_forward")
+                                     _DTYPES[dt], _stream(x.device)), "q38moe_experts_forward")
     return out
 
 
-def block_workspace_bytes(T, h, E, k, I, Is):
+def block_workspace_bytes(T, h, E, k, I, Is, dtype=torch.bfloat16):
     n = ctypes.c_size_t()
-    check(lib.q38moe_block_workspace_bytes(T, h, E, k, I, Is, ctypes.byref(n)), "q38moe_block_workspace_bytes")
+    check(lib.q38moe_block_workspace_bytes(T, h, E, k, I, Is, _DTYPES[dtype], ctypes.byref(n)),
+          "q38moe_block_workspace_bytes")
     return n.value
 
 
 def block_forward(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_sh_down, w_sh_gate_proj, k,
                   logit_bias=None, return_router=False, workspace=None, out=None):
-    """Qwen3_8MoeSparseMoeBlock.forward (modeling:824-835) on x [T,h]. Returns out [T,h] bf16, or
-    (out, logits [T,E], idx int32 [T,k], w bf16 [T,k]) with return_router."""
-    _need(x, "x", ndim=2)
+    """Qwen3_8MoeSparseMoeBlock.forward (modeling:824-835) on x [T,h]. Returns out [T,h], or
+    (out, logits [T,E], idx int32 [T,k], w [T,k]) with return_router; floats in x's dtype (bf16, or
+    fp32 computed without intermediate roundings)."""
+    dt = _fdt(x, "x")
+    _need(x, "x", dtype=dt, ndim=2)
     for t, n in ((w_router, "w_router"), (w_sh_gate, "w_sh_gate"), (w_sh_up, "w_sh_up"),
                  (w_sh_down, "w_sh_down")):
-        _need(t, n, ndim=2)
-    _need(w_gate_up, "w_gate_up", ndim=3)
-    _need(w_down, "w_down", ndim=3)
-    _need(w_sh_gate_proj, "w_sh_gate_proj")
+        _need(t, n, dtype=dt, ndim=2)
+    _need(w_gate_up, "w_gate_up", dtype=dt, ndim=3)
+    _need(w_down, "w_down", dtype=dt, ndim=3)
+    _need(w_sh_gate_proj, "w_sh_gate_proj", dtype=dt)
     T, h = x.shape
     E = w_router.shape[0]
     I = w_gate_up.shape[1] // 2
@@ -374,20 +403,20 @@ def block_forward(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_sh_down,
     if logit_bias is not None:
         _need(logit_bias, "logit_bias", dtype=torch.float32, ndim=1)
     dev = x.device
-    nbytes = block_workspace_bytes(T, h, E, k, I, Is)
+    nbytes = block_workspace_bytes(T, h, E, k, I, Is, dt)
     if workspace is None or workspace.numel() < nbytes:
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     if out is None:
-        out = torch.empty(T, h, dtype=torch.bfloat16, device=dev)
+        out = torch.empty(T, h, dtype=dt, device=dev)
     logits = idx = w = None
     if return_router:
-        logits = torch.empty(T, E, dtype=torch.bfloat16, device=dev)
+        logits = torch.empty(T, E, dtype=dt, device=dev)
         idx = torch.empty(T, k, dtype=torch.int32, device=dev)
-        w = torch.empty(T, k, dtype=torch.bfloat16, device=dev)
+        w = torch.empty(T, k, dtype=dt, device=dev)
     check(lib.q38moe_block_forward(_ptr(x), _ptr(w_router), _ptr(w_gate_up), _ptr(w_down), _ptr(w_sh_gate),
                                    _ptr(w_sh_up), _ptr(w_sh_down), _ptr(w_sh_gate_proj), _ptr(logit_bias), _ptr(out),
                                    _ptr(logits), _ptr(idx), _ptr(w), T, h, E, k, I, Is, _ptr(workspace),
-                                   workspace.numel(), BF16, _stream(dev)), "q38moe_block_forward")
+                                   workspace.numel(), _DTYPES[dt], _stream(dev)), "q38moe_block_forward")
     if return_router:
         return out, logits, idx, w
     return out
@@ -399,7 +428,8 @@ def block_forward_noalloc(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_
     instead of a workspace, no allocation inside the call. Outputs are the caller's (allocated
     here only when not given): out [T,h] bf16 and, optionally, logits [T,E] bf16, idx [T,k] int32,
     w [T,k] bf16. Raises RuntimeError when T exceeds what the scratch holds."""
-    _need(x, "x", ndim=2)
+    dt = _fdt(x, "x")
+    _need(x, "x", dtype=dt, ndim=2)
     T, h = x.shape
     E = w_router.shape[0]
     I = w_gate_up.shape[1] // 2
@@ -410,22 +440,22 @@ def block_forward_noalloc(x, w_router, w_gate_up, w_down, w_sh_gate, w_sh_up, w_
         raise ValueError("shared expert weights must be [Is,h], [Is,h], [h,Is]")
     for t, n in ((w_router, "w_router"), (w_gate_up, "w_gate_up"), (w_down, "w_down"), (w_sh_gate, "w_sh_gate"),
                  (w_sh_up, "w_sh_up"), (w_sh_down, "w_sh_down"), (w_sh_gate_proj, "w_sh_gate_proj")):
-        _need(t, n)
+        _need(t, n, dtype=dt)
     if logit_bias is not None:
         _need(logit_bias, "logit_bias", dtype=torch.float32, ndim=1)
     dev = x.device
     if out is None:
-        out = torch.empty(T, h, dtype=torch.bfloat16, device=dev)
-    for t, n, shape, dt in ((out, "out", (T, h), torch.bfloat16), (logits, "logits", (T, E), torch.bfloat16),
-                            (idx, "idx", (T, k), torch.int32), (w, "w", (T, k), torch.bfloat16)):
+        out = torch.empty(T, h, dtype=dt, device=dev)
+    for t, n, shape, tdt in ((out, "out", (T, h), dt), (logits, "logits", (T, E), dt),
+                             (idx, "idx", (T, k), torch.int32), (w, "w", (T, k), dt)):
         if t is not None:
-            _need(t, n, dtype=dt)
+            _need(t, n, dtype=tdt)
             if tuple(t.shape) != shape:
                 raise ValueError(f"{n} must be {shape}")
     check(lib.q38moe_block_forward_noalloc(_ptr(x), _ptr(w_router), _ptr(w_gate_up), _ptr(w_down), _ptr(w_sh_gate),
                                            _ptr(w_sh_up), _ptr(w_sh_down), _ptr(w_sh_gate_proj), _ptr(logit_bias),
-                                           _ptr(out), _ptr(logits), _ptr(idx), _ptr(w), T, h, E, k, I, Is, BF16,
-                                           _stream(dev)), "q38moe_block_forward_noalloc")
+                                           _ptr(out), _ptr(logits), _ptr(idx), _ptr(w), T, h, E, k, I, Is,
+                                           _DTYPES[dt], _stream(dev)), "q38moe_block_forward_noalloc")
     return out
 
 

@@ -81,7 +81,7 @@ def _fused_block(self, hidden_states, want_logits):
                             logit_bias=getattr(self, "routing_bias", None), return_router=want_logits,
                             workspace=_workspace(self, x.device, ops.block_workspace_bytes(
                                 x.shape[0], x.shape[1], weights[0].shape[0], k, weights[1].shape[1] // 2,
-                                weights[3].shape[0])))
+                                weights[3].shape[0], x.dtype)))
     if want_logits:
         return res[0].view(shape), res[1]
     return res.view(shape)

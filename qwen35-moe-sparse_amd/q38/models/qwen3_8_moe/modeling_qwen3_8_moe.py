@@ -130,11 +130,11 @@ class Qwen3_8MoeSparseMoeBlock(nn.Module):
         expert_output = self.experts(x, selected_experts, routing_weights)
         gate_logit = ops.route(x.contiguous(), self.gate.weight, self.gate.top_k,
                                w_shared_gate=self.shared_expert_gate.weight)[3]
-        # sigmoid(shared_expert_gate(x)) * shared + routed, in bf16 (modeling:831-833): the combine
-        # with one pair per token, weight 1 (exact in bf16) and the identity row map.
+        # sigmoid(shared_expert_gate(x)) * shared + routed, in x's dtype (modeling:831-833): the
+        # combine with one pair per token, weight 1 (exact) and the identity row map.
         T = x.shape[0]
         ident = torch.arange(T, dtype=torch.int32, device=x.device)
-        ones = torch.ones(T, 1, dtype=torch.bfloat16, device=x.device)
+        ones = torch.ones(T, 1, dtype=x.dtype, device=x.device)
         y = ops.combine(expert_output.contiguous(), ident, ones, self.gate.num_experts,
                         shared_out=shared_expert_output.contiguous(), shared_gate_logit=gate_logit)
         return y.reshape(batch_size, sequence_length, hidden_dim)

@@ -32,7 +32,7 @@ def test_header_symbols_exported():
 
 def test_abi_version():
     m = _lib()
-    assert m.lib.q38moe_abi_version() == m.ABI_VERSION == 8
+    assert m.lib.q38moe_abi_version() == m.ABI_VERSION == 9
 
 
 def test_max_tiles_and_block_m():
@@ -48,12 +48,17 @@ def test_max_tiles_and_block_m():
 def test_workspace_sizes():
     m = _lib()
     n = ctypes.c_size_t()
-    assert m.lib.q38moe_experts_workspace_bytes(16384, 1024, 64, 5, 256, ctypes.byref(n)) == 0
+    assert m.lib.q38moe_experts_workspace_bytes(16384, 1024, 64, 5, 256, m.BF16, ctypes.byref(n)) == 0
     P = 16384 * 5
     assert n.value >= P * 256 * 2 + P * 1024 * 2 + P * 4
     nb = ctypes.c_size_t()
-    assert m.lib.q38moe_block_workspace_bytes(16384, 1024, 64, 5, 256, 256, ctypes.byref(nb)) == 0
+    assert m.lib.q38moe_block_workspace_bytes(16384, 1024, 64, 5, 256, 256, m.BF16, ctypes.byref(nb)) == 0
     assert nb.value > n.value
+    # fp32 intermediates are twice as wide
+    n32 = ctypes.c_size_t()
+    assert m.lib.q38moe_experts_workspace_bytes(16384, 1024, 64, 5, 256, m.FP32, ctypes.byref(n32)) == 0
+    assert n32.value >= P * 256 * 4 + P * 1024 * 4 + P * 4 and n32.value > n.value
+    assert m.lib.q38moe_block_workspace_bytes(16384, 1024, 64, 5, 256, 256, 3, ctypes.byref(nb)) == -1
 
 
 @pytest.mark.parametrize("T,h,E,k,I,msg", [
@@ -68,7 +73,7 @@ def test_workspace_sizes():
 def test_invalid_shapes_rejected(T, h, E, k, I, msg):
     m = _lib()
     n = ctypes.c_size_t()
-    rc = m.lib.q38moe_experts_workspace_bytes(T, h, E, k, I, ctypes.byref(n))
+    rc = m.lib.q38moe_experts_workspace_bytes(T, h, E, k, I, m.BF16, ctypes.byref(n))
     assert rc == -1
     assert re.search(msg, m.lib.q38moe_last_error().decode())
 
