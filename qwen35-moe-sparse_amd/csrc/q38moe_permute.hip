@@ -206,11 +206,22 @@ __global__ __launch_bounds__(256) void permute_kernel(
     }
     s_rem[g] = rem;  // tid < 256 covers g <= E <= 64
     __syncthreads();
+    // Rank of this group's partial tile among all partial tiles: groups 0..63 are read once into
+    // the lanes of every wave and broadcast lane by lane (v_readlane, no LDS round trip per group);
+    // group 64 (the shared rows when E == 64) is one more LDS read.
+    const int rl = s_rem[lane];
+    const int r64 = E >= 64 ? s_rem[64] : 0;
     int rank = 0, npartial = 0;
-    for (int h = 0; h <= E; ++h) {
-      const int rh = s_rem[h];
-      npartial += rh > 0;
-      rank += rh > 0 && (rh > rem || (rh == rem && h < g));
+#pragma unroll 16
+    for (int h = 0; h < 64; ++h) {
+      const int rh = __builtin_amdgcn_readlane(rl, h);
+      const bool in = h <= E && rh > 0;
+      npartial += in;
+      rank += in && (rh > rem || (rh == rem && h < g));
+    }
+    if (E >= 64 && r64 > 0) {
+      npartial += 1;
+      rank += r64 > rem || (r64 == rem && 64 < g);
     }
     if (rem > 0) tiles[full + rank] = make_int4(g, row_start, rem, 0);
     if (tid == 0 && tile_count != nullptr) *tile_count = full + npartial;
