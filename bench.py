@@ -23,6 +23,7 @@ METRIC = "MoE-layer tokens/sec at 16K tokens bf16 (1 GPU) + % MFMA peak"
 PEAK_BF16 = 2.5e15   # dense bf16 MFMA, MI355X datasheet
 PEAK_FP8 = 5.0e15    # dense fp8 MFMA, MI355X datasheet
 PEAK_HBM = 8.0e12    # HBM3E bytes/s
+PEAK_FP32 = 157.3e12  # dense fp32 MFMA, MI355X datasheet
 
 
 def log(msg):
@@ -47,13 +48,21 @@ def time_stream(fn, iters, stream):
 
 
 def kernel_breakdown(wl, x, d, bias, iters, stream):
-    """Average duration of each stage kernel, launched alone back to back on `stream`."""
+    """Average duration of each stage kernel, launched alone back to back on `stream`. fp32
+    workloads: the route stage is the fp32 block's three launches (router logits GEMM, shared gate
+    logit GEMM, selection)."""
     import torch
     from q38.hip import ops
     T, h, E, k, I, Is = wl.tokens, wl.hidden, wl.experts, wl.topk, wl.inter, wl.shared_inter
     P = T * k
-    logits, idx, w, gate, hist = ops.route(x, d["gate.weight"], k, w_shared_gate=d["shared_expert_gate.weight"],
-                                           logit_bias=bias, want_hist=True)
+    f32 = x.dtype == torch.float32
+    esz = 4 if f32 else 2
+    peak_mfma = PEAK_FP32 if f32 else PEAK_BF16
+
+    def route_fn():
+        return ops.route(x, d["gate.weight"], k, w_shared_gate=d["shared_expert_gate.weight"], logit_bias=bias,
+                         want_hist=True)
+    logits, idx, w, gate, hist = route_fn()
     fused = I == Is
     srows = T if fused else 0
     counts, starts, perm, inv, tiles, tcount = ops.permute(idx, hist, E, shared_rows=srows)
@@ -65,21 +74,29 @@ def kernel_breakdown(wl, x, d, bias, iters, stream):
     torch.cuda.synchronize()
     fl = wl.flops()
     sh_fl = fl["shared"] if fused else 0
+    # The small-tile GEMMs (few rows per expert) stream each routed expert's weights once: their
+    # bound is HBM, the algorithmic bytes those weights plus the rows read and written.
+    small = not f32 and ops.gemm_tiling(T, h, E, k, I, srows) == "small"
+    used = int((counts > 0).sum())
+    rows = P + srows
+    gu_bound, gu_work = ("hbm", (used * 2 * I * h + (2 * I * h if fused else 0) + rows * (h + I)) * esz) \
+        if small else ("mfma", fl["gate_up"] + sh_fl * 2 // 3)
+    dn_bound, dn_work = ("hbm", (used * h * I + (h * I if fused else 0) + rows * (I + h)) * esz) \
+        if small else ("mfma", fl["down"] + sh_fl // 3)
     stages = {
-        "route": (lambda: ops.route(x, d["gate.weight"], k, w_shared_gate=d["shared_expert_gate.weight"],
-                                    logit_bias=bias, want_hist=True), "hbm",
+        "route": (route_fn, "hbm",
                   # x read + router weights + idx/w/gate/hist written
-                  T * h * 2 + (E + 1) * h * 2 + P * 6 + T * 2),
+                  (T * h + (E + 1) * h + T) * esz + P * (4 + esz)),
         "permute": (lambda: ops.permute(idx, hist, E, shared_rows=srows), "hbm", P * 4 * 3),
         # gate/up: routed pairs (+ the shared expert's gate/up when it runs in the same launch)
         "gate_up": (lambda: ops.gate_up(x, d["experts.gate_up_proj"], perm, tiles, tcount, k, shared_weights=sh_w,
-                                        shared_rows=srows), "mfma", fl["gate_up"] + sh_fl * 2 // 3),
+                                        shared_rows=srows), gu_bound, gu_work),
         "down": (lambda: ops.down(H, d["experts.down_proj"], tiles, tcount, T, k,
-                                  w_shared_down=d["shared_expert.down_proj.weight"], shared_rows=srows), "mfma",
-                 fl["down"] + sh_fl // 3),
+                                  w_shared_down=d["shared_expert.down_proj.weight"], shared_rows=srows), dn_bound,
+                 dn_work),
         # combine reads k bf16 rows + the shared row, writes one row per token
         "combine": (lambda: ops.combine(Y, inv, w, E, shared_out=sh, shared_gate_logit=gate), "hbm",
-                    T * h * 2 * (k + 2)),
+                    T * h * esz * (k + 2)),
     }
     if not fused:
         stages["shared_expert"] = (lambda: ops.shared_expert(x, *sh_w, d["shared_expert.down_proj.weight"]), "mfma",
@@ -89,11 +106,13 @@ def kernel_breakdown(wl, x, d, bias, iters, stream):
         fn()
         dt = time_stream(fn, iters, stream)
         if bound == "mfma":
-            achieved, peak, unit = work / dt / 1e12, PEAK_BF16 / 1e12, "TFLOP/s"
+            achieved, peak, unit = work / dt / 1e12, peak_mfma / 1e12, "TFLOP/s"
         else:
             achieved, peak, unit = work / dt / 1e9, PEAK_HBM / 1e9, "GB/s"
         out[name] = dict(us=round(dt * 1e6, 2), bound=bound, work=work, achieved=round(achieved, 2),
                          peak=peak, unit=unit, frac=round(achieved / peak, 4))
+    for name in ("gate_up", "down"):
+        out[name]["tiling"] = "fp32" if f32 else ("small" if small else "persistent")
     return out
 
 
@@ -361,9 +380,11 @@ def backward_bench(args):
     from q38 import workloads
     from q38.hip import autograd, ops
 
-    wl = workloads.get(args.workload)
+    wl = workloads.get(args.workload, batch=1, seq=args.tokens) if args.tokens else workloads.get(args.workload)
     dev = torch.device("cuda:0")
-    x, params, bias = workloads.make(wl, device="cpu")
+    f32 = wl.dtype == "fp32"
+    dt = torch.float32 if f32 else torch.bfloat16
+    x, params, bias = workloads.make(wl, device="cpu", dtype=dt)
     x = x.to(dev)
     d = {n: p.to(dev).contiguous() for n, p in params.items()}
     T, h, E, k, I = wl.tokens, wl.hidden, wl.experts, wl.topk, wl.inter
@@ -464,6 +485,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2")
+    ap.add_argument("--tokens", type=int, default=0,
+                    help="run the workload's shapes on this many tokens (one sequence) instead of its own "
+                         "batch x seq: decode and short-chunk sizes, where the small-tile GEMMs run")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=20)
     ap.add_argument("--backward", action="store_true",
@@ -486,20 +510,22 @@ def main():
     from q38 import workloads
     from q38.hip import ops
 
-    wl = workloads.get(args.workload)
+    wl = workloads.get(args.workload, batch=1, seq=args.tokens) if args.tokens else workloads.get(args.workload)
     dev = torch.device("cuda:0")
     log(f"[bench] workload {wl.name}: T={wl.tokens} h={wl.hidden} E={wl.experts} k={wl.topk} I={wl.inter} "
         f"Is={wl.shared_inter}")
-    x, params, bias = workloads.make(wl, device="cpu")
+    f32 = wl.dtype == "fp32"
+    dt = torch.float32 if f32 else torch.bfloat16
+    x, params, bias = workloads.make(wl, device="cpu", dtype=dt)
     x = x.to(dev)
     d = {n: p.to(dev).contiguous() for n, p in params.items()}
     if bias is not None:
         bias = bias.to(dev)
     T, h = x.shape
     k = wl.topk
-    ws = torch.empty(ops.block_workspace_bytes(T, h, wl.experts, k, wl.inter, wl.shared_inter), dtype=torch.uint8,
-                     device=dev)
-    out = torch.empty(T, h, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(ops.block_workspace_bytes(T, h, wl.experts, k, wl.inter, wl.shared_inter, dtype=dt),
+                     dtype=torch.uint8, device=dev)
+    out = torch.empty(T, h, dtype=dt, device=dev)
     weights = [d[n] for n in workloads.PARAM_ORDER]
     stream = torch.cuda.current_stream(dev)
     fp8 = wl.dtype == "fp8"
@@ -536,12 +562,17 @@ def main():
         log(f"[bench] kernels: " + ", ".join(f"{n} {v['us']}us" for n, v in kernels.items()))
 
     fl = wl.flops()
+    peak_mfma = PEAK_FP8 if fp8 else (PEAK_FP32 if f32 else PEAK_BF16)
+    # MFMA counters were collected at the workloads' own sizes only.
+    counters = (lambda n: None) if args.tokens else (lambda n: mfma_busy(wl.name, n))
     for name in ("gate_up", "down"):
-        kernels[name]["mfma_counters"] = mfma_busy(wl.name, name)
+        kernels[name]["mfma_counters"] = counters(name)
     dom = max(kernels, key=lambda n: kernels[n]["us"])
     dk = kernels[dom]
     expert_us = kernels["gate_up"]["us"] + kernels["down"]["us"]
-    expert_fl = kernels["gate_up"]["work"] + kernels["down"]["work"]
+    # routed + shared expert FLOPs of the two grouped launches (the shared expert runs inside them
+    # when its width equals the routed experts')
+    expert_fl = fl["experts"] + (fl["shared"] if fp8 or wl.inter == wl.shared_inter else 0)
     res = {
         "metric": METRIC,
         "value": round(T / (ms * 1e-3), 1),
@@ -553,17 +584,19 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8 e4m3 experts (fp32 accumulate), bf16 router/activations" if fp8 else "bf16",
+        "dtype": "fp8 e4m3 experts (fp32 accumulate), bf16 router/activations" if fp8 else ("fp32" if f32 else "bf16"),
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights; no checkpoint)",
         "config": {"workload": f"{wl.name}: one Q38 MoE block forward, {wl.batch}x{wl.seq} packed tokens",
                    "tokens": T, "hidden": h, "experts": wl.experts, "top_k": k, "expert_inter": wl.inter,
-                   "shared_inter": wl.shared_inter, "routing_skew": wl.zipf_s, "parallelism": "single GPU"},
+                   "shared_inter": wl.shared_inter, "routing_skew": wl.zipf_s, "parallelism": "single GPU",
+                   "gemm_tiling": kernels["gate_up"].get("tiling", "persistent")},
         "roofline": {"kernel": dom, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
-                     "unit": dk["unit"], "frac": dk["frac"], "traffic": hbm_traffic(wl.name, dom),
-                     "work_per_launch": dk["work"], "mfma_counters": mfma_busy(wl.name, dom)},
+                     "unit": dk["unit"], "frac": dk["frac"],
+                     "traffic": None if args.tokens else hbm_traffic(wl.name, dom),
+                     "work_per_launch": dk["work"], "mfma_counters": counters(dom)},
         # Routed + shared expert GEMM FLOPs over the two grouped launches that compute them.
-        "mfma_frac_expert_gemms": round(expert_fl / (expert_us * 1e-6) / (PEAK_FP8 if fp8 else PEAK_BF16), 4),
-        "mfma_frac_block": round(fl["block"] / (ms * 1e-3) / (PEAK_FP8 if fp8 else PEAK_BF16), 4),
+        "mfma_frac_expert_gemms": round(expert_fl / (expert_us * 1e-6) / peak_mfma, 4),
+        "mfma_frac_block": round(fl["block"] / (ms * 1e-3) / peak_mfma, 4),
         "kernels": kernels,
     }
     if not args.no_cpu_baseline:

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define Q38MOE_ABI_VERSION 9
+#define Q38MOE_ABI_VERSION 10
 
 #define Q38MOE_OK 0
 #define Q38MOE_EINVAL (-1)   /* bad shape, null pointer, misalignment, unsupported dtype */
@@ -131,6 +131,22 @@ int64_t q38moe_max_tiles(int64_t T, int32_t E, int32_t k, int64_t shared_rows);
 
 /* Rows per grouped-GEMM tile of this build. */
 int32_t q38moe_gemm_block_m(void);
+
+/* Which grouped-GEMM kernels the bf16 gate/up and down entry points (and the forward entry points
+ * built on them) run for a shape (T tokens, hidden h, E experts, top-k k, intermediate I,
+ * shared_rows fused shared-expert rows): Q38MOE_TILING_PERSISTENT (a persistent grid, one
+ * 256-row x 256-column tile per CU at a time) or Q38MOE_TILING_SMALL (16 weight rows x up to 64
+ * rows per workgroup with K split over its waves, for few rows per expert). Both compute the same
+ * roundings. Rule: small tiles when h and I are in {128, 256, 512, 1024, 2048} and
+ * T*k + shared_rows <= 32 * (E + (shared_rows > 0)), i.e. at most 32 rows per group on average
+ * (the measured crossover at the benchmark's shapes); the environment variable
+ * Q38MOE_GEMM_TILING=small|persistent, read once, overrides the row condition. The reference picks
+ * its Triton tiles per shape by timing candidates on the first call (inference.py:133-155, 181-183);
+ * this is the build's fixed, shape-keyed counterpart, and the query lets callers and tests see
+ * which kernels a shape runs. */
+#define Q38MOE_TILING_PERSISTENT 1
+#define Q38MOE_TILING_SMALL 2
+int32_t q38moe_gemm_tiling(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int64_t shared_rows);
 
 /*
  * Grouped gate/up GEMM with fused SwiGLU, R5-R6 (+R9 first half): replaces _gate_up_kernel

@@ -14,7 +14,7 @@ CSRC = Path(__file__).resolve().parent
 PKG_ROOT = CSRC.parent
 REPO = PKG_ROOT.parent
 OUT = PKG_ROOT / "q38" / "hip" / "libq38moe.so"
-SOURCES = ["q38moe_route.hip", "q38moe_permute.hip", "q38moe_gemm.hip", "q38moe_combine.hip", "q38moe_quant.hip",
+SOURCES = ["q38moe_route.hip", "q38moe_permute.hip", "q38moe_gemm.hip", "q38moe_gemm_small.hip", "q38moe_combine.hip", "q38moe_quant.hip",
            "q38moe_backward.hip", "q38moe_fp32.hip", "q38moe_api.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -2,6 +2,7 @@
 // Declarations and the reference function each entry point replaces: include/q38moe.h.
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 
@@ -74,6 +75,53 @@ constexpr size_t kAlign = 256;
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 int64_t hist_blocks(int64_t T) { return (T + 63) / 64; }
+
+// GEMM tiling by shape. The persistent kernels (q38moe_gemm.hip) hand each CU whole (256-row tile,
+// 256 weight rows) units: with few rows per expert those units are few, each streams 512 KiB of one
+// expert's weights through one CU, and the kernel's time stays near 20-30 us (configuration 2's
+// shapes) from T = 1 up to T ~ 1000. The small-tile kernels (q38moe_gemm_small.hip: 16 weight rows
+// per workgroup, K split over its waves, every weight block in flight at once) take 6 us (gate/up)
+// and 4 us (down) at T = 1 but grow with the rows per expert, since each workgroup walks its rows in
+// 16-row blocks. Measured on MI355X at configuration 2's shapes (E = 64, k = 5, fused shared rows)
+// the two meet near T = 350, i.e. about 32 rows per group (E experts + the shared group): the rule
+// takes the small tiles up to that average. Q38MOE_GEMM_TILING=small|persistent (read once)
+// overrides the rule, to time one tiling against the other on the same shapes.
+constexpr int64_t kSmallRowsPerGroup = 32;
+int tiling_override() {
+  static const int v = [] {
+    const char* e = std::getenv("Q38MOE_GEMM_TILING");
+    if (e == nullptr) return 0;
+    if (std::strcmp(e, "small") == 0) return Q38MOE_TILING_SMALL;
+    if (std::strcmp(e, "persistent") == 0) return Q38MOE_TILING_PERSISTENT;
+    return 0;
+  }();
+  return v;
+}
+bool small_tiles(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int64_t shared_rows) {
+  if (!q38::small_gemm_supported(h) || !q38::small_gemm_supported(I)) return false;
+  if (tiling_override() != 0) return tiling_override() == Q38MOE_TILING_SMALL;
+  return T * k + shared_rows <= kSmallRowsPerGroup * (E + (shared_rows > 0 ? 1 : 0));
+}
+
+hipError_t gate_up_bf16(const uint16_t* x, const int32_t* perm, const int4* tiles, const int32_t* tile_count,
+                        int max_tiles, int64_t T, int32_t k, int64_t shared_rows, const uint16_t* w_gate_up,
+                        const uint16_t* sh_gate, const uint16_t* sh_up, uint16_t* H, int32_t I, int32_t h, int32_t E,
+                        hipStream_t st) {
+  if (small_tiles(T, h, E, k, I, shared_rows))
+    return q38::launch_gate_up_small(x, perm, tiles, tile_count, max_tiles, (int)(T * k), (int)shared_rows, w_gate_up,
+                                     sh_gate, sh_up, H, I, h, E, k, st);
+  return q38::launch_gate_up(x, perm, tiles, tile_count, max_tiles, 0, (int)(T * k), w_gate_up, sh_gate, sh_up, H, I,
+                             h, E, k, st);
+}
+
+hipError_t down_bf16(const uint16_t* H, const int4* tiles, const int32_t* tile_count, int max_tiles, int64_t T,
+                     int32_t k, int64_t shared_rows, const uint16_t* w_down, const uint16_t* sh_down, uint16_t* Y,
+                     int32_t I, int32_t h, int32_t E, hipStream_t st) {
+  if (small_tiles(T, h, E, k, I, shared_rows))
+    return q38::launch_down_small(H, tiles, tile_count, max_tiles, (int)(T * k), (int)shared_rows, w_down, sh_down, Y,
+                                  h, I, E, st);
+  return q38::launch_down(H, tiles, tile_count, max_tiles, 0, w_down, sh_down, Y, h, I, E, st);
+}
 
 int64_t max_tiles_impl(int64_t T, int32_t E, int32_t k, int64_t shared_rows) {
   const int64_t bm = q38::gemm_block_m();
@@ -206,14 +254,12 @@ int run_experts(const void* x, const void* idx, bool idx64, const void* topk_w,
   }
   uint16_t* H = at<uint16_t>(ws, L.H);
   uint16_t* Y = at<uint16_t>(ws, L.Y);
-  Q38_HIP(q38::launch_gate_up(static_cast<const uint16_t*>(x), perm, tiles, tile_count,
-                              (int)L.max_tiles, 0, (int)P, static_cast<const uint16_t*>(w_gate_up),
-                              static_cast<const uint16_t*>(sh_gate), static_cast<const uint16_t*>(sh_up), H, I, h, E,
-                              k, st),
+  Q38_HIP(gate_up_bf16(static_cast<const uint16_t*>(x), perm, tiles, tile_count, (int)L.max_tiles, T, k, shared_rows,
+                       static_cast<const uint16_t*>(w_gate_up), static_cast<const uint16_t*>(sh_gate),
+                       static_cast<const uint16_t*>(sh_up), H, I, h, E, st),
           "gate_up launch");
-  Q38_HIP(q38::launch_down(H, tiles, tile_count, (int)L.max_tiles, 0,
-                           static_cast<const uint16_t*>(w_down), static_cast<const uint16_t*>(sh_down), Y, h, I, E,
-                           st),
+  Q38_HIP(down_bf16(H, tiles, tile_count, (int)L.max_tiles, T, k, shared_rows, static_cast<const uint16_t*>(w_down),
+                    static_cast<const uint16_t*>(sh_down), Y, I, h, E, st),
           "down launch");
   const uint16_t* shared = shared_out != nullptr ? static_cast<const uint16_t*>(shared_out)
                                                  : (shared_rows > 0 ? Y + P * h : nullptr);
@@ -359,6 +405,10 @@ int64_t q38moe_max_tiles(int64_t T, int32_t E, int32_t k, int64_t shared_rows) {
 
 int32_t q38moe_gemm_block_m(void) { return q38::gemm_block_m(); }
 
+int32_t q38moe_gemm_tiling(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int64_t shared_rows) {
+  return small_tiles(T, h, E, k, I, shared_rows) ? Q38MOE_TILING_SMALL : Q38MOE_TILING_PERSISTENT;
+}
+
 int q38moe_route(const void* x, const void* w_router, const void* w_shared_gate,
                  const float* logit_bias, void* logits, int32_t* topk_idx, void* topk_w,
                  void* shared_gate_logit, int32_t* hist, int64_t T, int32_t h, int32_t E,
@@ -489,11 +539,11 @@ int q38moe_gate_up(const void* x, const void* w_gate_up, const void* w_sh_gate,
             "gate_up fp32 launch");
     return Q38MOE_OK;
   }
-  Q38_HIP(q38::launch_gate_up(static_cast<const uint16_t*>(x), perm, reinterpret_cast<const int4*>(tiles),
-                              tile_count, (int)max_tiles_impl(T, E, k, shared_rows), 0, (int)(T * k),
-                              static_cast<const uint16_t*>(w_gate_up), static_cast<const uint16_t*>(w_sh_gate),
-                              static_cast<const uint16_t*>(w_sh_up), static_cast<uint16_t*>(H), I, h, E, k,
-                              static_cast<hipStream_t>(stream)),
+  Q38_HIP(gate_up_bf16(static_cast<const uint16_t*>(x), perm, reinterpret_cast<const int4*>(tiles), tile_count,
+                       (int)max_tiles_impl(T, E, k, shared_rows), T, k, shared_rows,
+                       static_cast<const uint16_t*>(w_gate_up), static_cast<const uint16_t*>(w_sh_gate),
+                       static_cast<const uint16_t*>(w_sh_up), static_cast<uint16_t*>(H), I, h, E,
+                       static_cast<hipStream_t>(stream)),
           "gate_up launch");
   return Q38MOE_OK;
 }
@@ -524,10 +574,10 @@ int q38moe_down(const void* H, const void* w_down, const void* w_sh_down, const 
             "down fp32 launch");
     return Q38MOE_OK;
   }
-  Q38_HIP(q38::launch_down(static_cast<const uint16_t*>(H), reinterpret_cast<const int4*>(tiles), tile_count,
-                           (int)max_tiles_impl(T, E, k, shared_rows), 0, static_cast<const uint16_t*>(w_down),
-                           static_cast<const uint16_t*>(w_sh_down), static_cast<uint16_t*>(Y), h, I, E,
-                           static_cast<hipStream_t>(stream)),
+  Q38_HIP(down_bf16(static_cast<const uint16_t*>(H), reinterpret_cast<const int4*>(tiles), tile_count,
+                    (int)max_tiles_impl(T, E, k, shared_rows), T, k, shared_rows,
+                    static_cast<const uint16_t*>(w_down), static_cast<const uint16_t*>(w_sh_down),
+                    static_cast<uint16_t*>(Y), I, h, E, static_cast<hipStream_t>(stream)),
           "down launch");
   return Q38MOE_OK;
 }

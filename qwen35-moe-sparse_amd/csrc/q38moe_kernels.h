@@ -54,6 +54,18 @@ hipError_t launch_down(const uint16_t* H, const int4* tiles, const int32_t* ntil
                        const uint16_t* ws_down, uint16_t* Y, int N, int K, int E,
                        hipStream_t stream);
 
+// The same two GEMMs (tile tables only, bf16) decomposed for few rows per expert: 16 weight rows x
+// up to 64 activation rows per workgroup, K split over its waves (q38moe_gemm_small.hip), for K in
+// {128, 256, 512, 1024, 2048} (small_gemm_supported); P = T * k routed rows, shared_rows after them.
+bool small_gemm_supported(int K);
+hipError_t launch_gate_up_small(const uint16_t* x, const int32_t* perm, const int4* tiles, const int32_t* ntiles_dev,
+                                int max_mtiles, int P, int shared_rows, const uint16_t* w_gate_up,
+                                const uint16_t* ws_gate, const uint16_t* ws_up, uint16_t* H, int N, int K, int E,
+                                int topk, hipStream_t stream);
+hipError_t launch_down_small(const uint16_t* H, const int4* tiles, const int32_t* ntiles_dev, int max_mtiles, int P,
+                             int shared_rows, const uint16_t* w_down, const uint16_t* ws_down, uint16_t* Y, int N,
+                             int K, int E, hipStream_t stream);
+
 // Grouped GEMM with gathered activation rows and plain weight rows: C[r] = bf16(A[perm[r] / topk] .
 // W[e]^T) for the routed rows of a tile table without shared-expert rows; W [E, N, K].
 hipError_t launch_gather_gemm(const uint16_t* A, const int32_t* perm, const int4* tiles,

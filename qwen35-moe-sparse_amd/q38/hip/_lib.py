@@ -12,9 +12,11 @@ import torch  # noqa: F401  (loads the HIP runtime first)
 
 LIB_PATH = Path(os.environ.get("Q38MOE_LIB", Path(__file__).resolve().parent / "libq38moe.so"))
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 BF16 = 1
 FP32 = 2
+TILING_PERSISTENT = 1
+TILING_SMALL = 2
 
 _c_int, _c_i32, _c_i64, _c_size, _vp = ctypes.c_int, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
 
@@ -30,6 +32,7 @@ SIGNATURES = {
                                 _vp]),
     "q38moe_max_tiles": (_c_i64, [_c_i64, _c_i32, _c_i32, _c_i64]),
     "q38moe_gemm_block_m": (_c_i32, []),
+    "q38moe_gemm_tiling": (_c_i32, [_c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64]),
     "q38moe_gate_up": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i64, _c_i32, _c_i32, _c_i32,
                                 _c_i32, _c_i32, _vp]),
     "q38moe_down": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,

@@ -11,7 +11,7 @@ import ctypes
 
 import torch
 
-from ._lib import BF16, FP32, check, lib
+from ._lib import BF16, FP32, TILING_PERSISTENT, TILING_SMALL, check, lib
 
 _NULL = None
 
@@ -62,6 +62,12 @@ def gemm_block_m():
 
 def max_tiles(T, E, k, shared_rows=0):
     return int(lib.q38moe_max_tiles(T, E, k, shared_rows))
+
+
+def gemm_tiling(T, h, E, k, I, shared_rows=0):
+    """"small" or "persistent": the grouped-GEMM kernels bf16 calls of this shape run."""
+    v = int(lib.q38moe_gemm_tiling(T, h, E, k, I, shared_rows))
+    return {TILING_SMALL: "small", TILING_PERSISTENT: "persistent"}[v]
 
 
 def route(x, w_router, k, w_shared_gate=None, logit_bias=None, want_logits=False, want_hist=False):

@@ -1,6 +1,9 @@
 """The C ABI library: loads, exports every entry point of include/q38moe.h, validates arguments on
 the host. CPU only: no call here reaches a kernel launch."""
 import ctypes
+import os
+import subprocess
+import sys
 import re
 from pathlib import Path
 
@@ -32,7 +35,7 @@ def test_header_symbols_exported():
 
 def test_abi_version():
     m = _lib()
-    assert m.lib.q38moe_abi_version() == m.ABI_VERSION == 9
+    assert m.lib.q38moe_abi_version() == m.ABI_VERSION == 10
 
 
 def test_max_tiles_and_block_m():
@@ -43,6 +46,40 @@ def test_max_tiles_and_block_m():
     assert m.lib.q38moe_max_tiles(16384, 64, 5, 0) == cd(16384 * 5, bm) + 64
     assert m.lib.q38moe_max_tiles(16384, 64, 5, 16384) == cd(16384 * 5, bm) + 64 + cd(16384, bm)
     assert m.lib.q38moe_max_tiles(-1, 64, 5, 0) == -1
+
+
+def test_gemm_tiling_rule():
+    """Small tiles up to 32 pair rows per group on average (E experts, plus the shared group when its
+    rows are fused), for K in {128, ..., 2048} only; monotone in T; the environment override
+    switches the row condition in a fresh process (the variable is read once)."""
+    m = _lib()
+    tiling = lambda T, sh, h=1024, E=64, k=5, I=256: m.lib.q38moe_gemm_tiling(T, h, E, k, I, sh)  # noqa: E731
+    assert tiling(1, 1) == m.TILING_SMALL
+    assert tiling(346, 346) == m.TILING_SMALL       # 346 * 6 = 2076 <= 32 * 65
+    assert tiling(347, 347) == m.TILING_PERSISTENT
+    assert tiling(409, 0) == m.TILING_SMALL         # 409 * 5 = 2045 <= 32 * 64
+    assert tiling(410, 0) == m.TILING_PERSISTENT
+    assert tiling(16384, 16384) == m.TILING_PERSISTENT
+    assert tiling(1, 1, h=4096) == m.TILING_PERSISTENT
+    assert tiling(1, 1, I=192) == m.TILING_PERSISTENT
+    assert tiling(1, 1, h=2048, I=512) == m.TILING_SMALL
+    assert tiling(40, 40, E=8, k=2) == m.TILING_SMALL    # 120 <= 32 * 9
+    assert tiling(100, 100, E=8, k=2) == m.TILING_PERSISTENT
+    kinds = [tiling(T, T) for T in range(1, 5000, 7)]
+    first_big = kinds.index(m.TILING_PERSISTENT)
+    assert all(v == m.TILING_SMALL for v in kinds[:first_big])
+    assert all(v == m.TILING_PERSISTENT for v in kinds[first_big:])
+    code = ("import ctypes, sys; lib = ctypes.CDLL(sys.argv[1]); "
+            "f = lib.q38moe_gemm_tiling; f.restype = ctypes.c_int32; "
+            "f.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64]; "
+            "print(f(16384, 1024, 64, 5, 256, 16384), f(1, 1024, 64, 5, 256, 1), f(1, 4096, 64, 5, 256, 1))")
+    for value, want in (("small", (m.TILING_SMALL, m.TILING_SMALL, m.TILING_PERSISTENT)),
+                        ("persistent", (m.TILING_PERSISTENT,) * 3)):
+        env = dict(os.environ, Q38MOE_GEMM_TILING=value)
+        r = subprocess.run([sys.executable, "-c", code, str(m.LIB_PATH)], env=env, capture_output=True, text=True,
+                           timeout=60)
+        assert r.returncode == 0, r.stderr
+        assert tuple(int(v) for v in r.stdout.split()) == want
 
 
 def test_workspace_sizes():

@@ -1,0 +1,120 @@
+"""GPU parity of the small-tile grouped GEMMs (16 weight rows x up to 64 rows per workgroup, K split
+over its waves), which the bf16 gate/up and down calls run when a shape has few pair rows per
+expert (q38moe_gemm_tiling). Same products and
+rounding points as the persistent kernels (inference.py:90-96, 122-127), so the same bars: H and Y
+in bf16 results of identical roundings (fp32 accumulation order aside: at most 1 ulp off in fewer
+than 1e-3 of the elements when fed the oracle's inputs), block outputs within the bf16 tolerance
+of tests/_util.py.
+
+Shapes cover a single token, experts with no rows, an expert with more than one 256-row tile (all
+four 64-row quarters of a tile in use), configuration 3's skew, the fused shared rows, the separate
+shared expert (Is != I), 17 experts with k = 8, and both sides of the tiling rule.
+"""
+import pytest
+import torch
+
+from _util import assert_bf16_close, bf16_ulp_diff
+from oracle import moe_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(name, T, **over):
+    from q38 import workloads
+    wl = workloads.get(name, **over) if over else workloads.get(name)
+    x, params, bias = workloads.make(wl, tokens=T)
+    return wl, x, params, bias
+
+
+def _block_args(d, wl):
+    return (d["gate.weight"], d["experts.gate_up_proj"], d["experts.down_proj"], d["shared_expert.gate_proj.weight"],
+            d["shared_expert.up_proj.weight"], d["shared_expert.down_proj.weight"], d["shared_expert_gate.weight"],
+            wl.topk)
+
+
+@pytest.mark.parametrize("name,T,hot", [("c2", 1, False), ("c2", 13, False), ("c2", 300, False), ("c3", 340, True)])
+def test_small_tile_stages(gpu, name, T, hot):
+    """gate/up (+ fused shared rows) and down on small tiles against the oracle on the same routing.
+    hot: expert 0 is in every token's top-k (the rest drawn without repeats), so it has T > 256
+    rows: two tiles, every 64-row quarter and 16-row block of the first one in use."""
+    from q38.hip import ops
+    wl, x, p, bias = _setup(name, T)
+    k, E = wl.topk, wl.experts
+    assert ops.gemm_tiling(T, wl.hidden, E, k, wl.inter, T) == "small"
+    _, _, ridx, rw = orc.router(x, p["gate.weight"], k, logit_bias=bias)
+    if hot:
+        g = torch.Generator().manual_seed(T)
+        ridx = torch.stack([torch.cat([torch.zeros(1, dtype=torch.long), 1 + torch.randperm(E - 1, generator=g)[:k - 1]])
+                            for _ in range(T)])
+    _, _, ref_H, ref_Y = orc.experts_grouped(x, ridx, rw, p["experts.gate_up_proj"], p["experts.down_proj"],
+                                             return_sorted=True)
+    d = {n: t.to(gpu) for n, t in p.items()}
+    hist = ops.histogram(ridx.to(gpu), E)
+    counts, starts, perm, inv, tiles, tc = ops.permute(ridx.to(gpu), hist, E, shared_rows=T)
+    if hot:
+        assert int(counts[0]) == T > 256
+    sh = (d["shared_expert.gate_proj.weight"], d["shared_expert.up_proj.weight"])
+    H = ops.gate_up(x.to(gpu), d["experts.gate_up_proj"], perm, tiles, tc, k, shared_weights=sh, shared_rows=T)
+    torch.cuda.synchronize()
+    P = T * k
+    Hc = H.cpu()
+    assert_bf16_close(Hc[:P], ref_H, what="H routed rows")
+    assert float((bf16_ulp_diff(Hc[:P], ref_H) > 1).float().mean()) < 1e-3
+    # shared rows: the shared expert's bf16 SwiGLU on every token
+    xf = orc._f(x)
+    g = orc._f(orc.bf16(xf @ orc._f(p["shared_expert.gate_proj.weight"]).T))
+    u = orc._f(orc.bf16(xf @ orc._f(p["shared_expert.up_proj.weight"]).T))
+    ref_Hs = orc.bf16(orc._f(orc.bf16(torch.nn.functional.silu(g))) * u)
+    assert float((bf16_ulp_diff(Hc[P:], ref_Hs) > 1).float().mean()) < 1e-3
+    # down on the oracle's H (routed) and the GPU's shared rows: isolates the down GEMM
+    Hin = torch.cat([ref_H, Hc[P:]]).to(gpu)
+    Y = ops.down(Hin, d["experts.down_proj"], tiles, tc, T, k, w_shared_down=d["shared_expert.down_proj.weight"],
+                 shared_rows=T)
+    torch.cuda.synchronize()
+    Yc = Y.cpu()
+    assert float((bf16_ulp_diff(Yc[:P], ref_Y) > 1).float().mean()) < 1e-3
+    ref_Ys = orc.bf16(orc._f(Hc[P:]) @ orc._f(p["shared_expert.down_proj.weight"]).T)
+    assert float((bf16_ulp_diff(Yc[P:], ref_Ys) > 1).float().mean()) < 1e-3
+
+
+@pytest.mark.parametrize("name,T,over", [
+    ("c2", 1, {}),
+    ("c2", 2, {}),
+    ("c2", 64, {}),
+    ("c2", 346, {}),      # last T on the small side: 346 * 6 pair + shared rows <= 32 * 65
+    ("c2", 347, {}),      # first T on the persistent side
+    ("c3", 300, {}),
+    ("c2", 200, {"shared_inter": 128}),  # separate shared expert: shared rows not in the tile table
+    ("c2", 60, {"experts": 17, "topk": 8, "hidden": 512, "inter": 128, "shared_inter": 128}),
+])
+def test_small_tile_block(gpu, name, T, over):
+    """Whole block through the tiling rule: routing bit-exact on the GPU's logits, output within the
+    bf16 tolerance of the oracle's block on that routing."""
+    from q38.hip import ops
+    wl, x, p, bias = _setup(name, T, **over)
+    fused = wl.shared_inter == wl.inter
+    kind = ops.gemm_tiling(T, wl.hidden, wl.experts, wl.topk, wl.inter, T if fused else 0)
+    assert kind == ("persistent" if T == 347 else "small")
+    d = {n: t.to(gpu) for n, t in p.items()}
+    out, logits, idx, w = ops.block_forward(x.to(gpu), *_block_args(d, wl), return_router=True,
+                                            logit_bias=None if bias is None else bias.to(gpu))
+    torch.cuda.synchronize()
+    _, _, sidx, srw = orc.router(None, None, wl.topk, logit_bias=bias, logits=logits.cpu())
+    assert torch.equal(idx.cpu().long(), sidx)
+    assert torch.equal(w.cpu(), srw)
+    ref = orc.reference_block_forward(x, p, wl.topk, routing=(sidx, srw))
+    mx, r = assert_bf16_close(out.cpu(), ref, what=f"{name} T={T} {over} block ({kind} tiles)")
+    print(f"{name} T={T} {over} {kind}: max-abs {mx:.3e} rel {r:.3e}")
+
+
+def test_small_tile_experts_deterministic(gpu):
+    """Small tiles keep the run-to-run bit-exactness of the block (no atomics, fixed K order)."""
+    from q38.hip import ops
+    wl, x, p, bias = _setup("c3", 300)
+    assert ops.gemm_tiling(300, wl.hidden, wl.experts, wl.topk, wl.inter, 300) == "small"
+    d = {n: t.to(gpu) for n, t in p.items()}
+    args = (x.to(gpu), *_block_args(d, wl))
+    a = ops.block_forward(*args, logit_bias=bias.to(gpu))
+    b = ops.block_forward(*args, logit_bias=bias.to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
