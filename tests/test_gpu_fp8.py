@@ -11,6 +11,7 @@ e4m3 code of the second quantisation by one step, 1/8 relative, so the bf16 max-
 widened). Against the bf16 block the fp8 block is reported, with relative L2 <= 8e-2 for the e4m3
 quantisation error itself.
 """
+import numpy as np
 import pytest
 import torch
 
@@ -158,3 +159,33 @@ def test_block_forward_fp8_edge_shapes(gpu, shape):
     gate_logit = orc.bf16(orc._f(x) @ orc._f(params["shared_expert_gate.weight"]).reshape(-1))
     ref_out, _ = orc.experts_fp8(x, idx.cpu().long(), w.cpu(), orc.quant_weights_fp8(params), wl.topk, gate_logit)
     assert_bf16_close(out.cpu(), ref_out, max_abs=5e-2, what=f"fp8 edge block {shape}")
+
+
+def test_block_forward_fp8_full_c4(gpu):
+    """Configuration 4 at its full size (T = 32768, h = 2048, I = 512): routing bit-exact against the
+    CPU oracle on the GPU's logits for every token; outputs finite and bit-identical on a second
+    forward; and, since tokens are independent through the block (per-token x scales, per-row H
+    scales, per-token k-sum), the fake-quant oracle run on a seeded sample of 256 tokens with their
+    GPU routing reproduces those tokens' outputs within the bar of the smaller fp8 block tests."""
+    ops = _ops()
+    wl, x, params, _ = _setup("c4", None)
+    T = wl.tokens
+    assert T == 32768 and x.shape == (T, 2048)
+    d = {n: p.to(gpu) for n, p in params.items()}
+    wq = ops.quantize_weights_fp8(d)
+    xd = x.to(gpu)
+    args = (xd, d["gate.weight"], wq, d["shared_expert_gate.weight"], wl.topk)
+    out, logits, idx, w = ops.block_forward_fp8(*args, return_router=True)
+    out2 = ops.block_forward_fp8(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2), "fp8 block not deterministic at full size"
+    assert bool(torch.isfinite(out).all())
+    _, _, sidx, sw = orc.router(None, None, wl.topk, logits=logits.cpu())
+    assert torch.equal(idx.cpu().long(), sidx)
+    assert torch.equal(w.cpu(), sw)
+    sel = torch.from_numpy(np.sort(np.random.RandomState(4).choice(T, 256, replace=False)))
+    xs = x[sel]
+    gate_logit = orc.bf16(orc._f(xs) @ orc._f(params["shared_expert_gate.weight"]).reshape(-1))
+    ref, _ = orc.experts_fp8(xs, sidx[sel], sw[sel], orc.quant_weights_fp8(params), wl.topk, gate_logit)
+    mx, r = assert_bf16_close(out.cpu()[sel], ref, max_abs=5e-2, what="c4 T=32768 fp8 block, 256 sampled tokens")
+    print(f"c4 T={T}: sampled tokens vs fake-quant max-abs {mx:.3e} rel {r:.3e}")
