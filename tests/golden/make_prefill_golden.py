@@ -12,6 +12,8 @@ model with ``.to(torch.bfloat16)`` and then puts the rotary inverse-frequency bu
 as a model loaded with ``from_pretrained(dtype=bf16)`` (q38/evaluate.py:185) keeps them.
 
 Usage: python tests/golden/make_prefill_golden.py [--batch 2 --seq 1024] [--debug /tmp/dump.pt]
+       python tests/golden/make_prefill_golden.py --batch 4 --seq 4096 --eos-every 1000 --full-rows \
+           --out tests/golden/prefill_c5_full.npz      (the configuration-5 input itself)
 """
 import argparse
 import importlib.util
@@ -30,6 +32,8 @@ from q38 import prefill as P  # noqa: E402
 OUT = Path(__file__).resolve().parent / "prefill_c5.npz"
 # (batch row, position) pairs whose full logit rows are stored.
 ROWS = ((0, 0), (0, 301), (0, 1023), (1, 64), (1, 640), (1, 1000))
+# For the full configuration-5 input (4 x 4096): rows in every sequence, late positions included.
+ROWS_FULL = ((0, 0), (0, 1023), (1, 2047), (2, 3000), (3, 4000), (3, 4095))
 
 
 def reference_package():
@@ -97,7 +101,11 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--ids-seed", type=int, default=1234)
     ap.add_argument("--debug", default=None, help="also save per-layer stream sums here (torch.save)")
+    ap.add_argument("--out", default=str(OUT))
+    ap.add_argument("--full-rows", action="store_true", help="store the ROWS_FULL logit rows (4 x 4096 input)")
     args = ap.parse_args()
+    rows = ROWS_FULL if args.full_rows else ROWS
+    out_path = Path(args.out)
     torch.manual_seed(0)
     c = P.c5_config()
     params = P.init_params(c, args.seed)
@@ -106,7 +114,7 @@ def main():
     model = mod.Qwen3_8MoeForCausalLM(reference_config(mod, c)).eval()
     model.load_state_dict(params, strict=True)
     out = dict(batch=args.batch, seq=args.seq, eos_every=args.eos_every, seed=args.seed,
-               ids_seed=args.ids_seed, ids=ids.numpy().astype(np.int32), rows=np.array(ROWS, dtype=np.int32))
+               ids_seed=args.ids_seed, ids=ids.numpy().astype(np.int32), rows=np.array(rows, dtype=np.int32))
     dumps = {}
     print("reference fp32", flush=True)
     logits, aux, layers = run(model, ids, args.debug)
@@ -114,7 +122,7 @@ def main():
     out["aux_loss_fp32"] = np.float64(aux)
     out["lse_fp32"] = torch.logsumexp(lf, -1).numpy()
     out["argmax_fp32"] = lf.argmax(-1).numpy().astype(np.int32)
-    out["logits_fp32"] = np.stack([lf[b, s].numpy() for b, s in ROWS])
+    out["logits_fp32"] = np.stack([lf[b, s].numpy() for b, s in rows])
     dumps["fp32"] = layers
     print("reference bf16", flush=True)
     model = model.to(torch.bfloat16)
@@ -126,10 +134,10 @@ def main():
     out["aux_loss_bf16"] = np.float64(aux)
     out["lse_bf16"] = torch.logsumexp(lf, -1).numpy()
     out["argmax_bf16"] = lf.argmax(-1).numpy().astype(np.int32)
-    out["logits_bf16"] = np.stack([bf16_bits(logits[b, s]) for b, s in ROWS])
+    out["logits_bf16"] = np.stack([bf16_bits(logits[b, s]) for b, s in rows])
     dumps["bf16"] = layers
-    np.savez_compressed(OUT, **out)
-    print("wrote", OUT, OUT.stat().st_size, "bytes")
+    np.savez_compressed(out_path, **out)
+    print("wrote", out_path, out_path.stat().st_size, "bytes")
     if args.debug:
         torch.save(dumps, args.debug)
 
