@@ -1,5 +1,6 @@
 """Packed prefill (benchmark config 5) on the GPU: the restated Q38 trunk with the fused HIP MoE block
-in every layer, against the reference model's forward (tests/golden/prefill_c5.npz).
+in every layer, against the reference model's forward (tests/golden/prefill_c5.npz on 2 x 1024
+tokens, tests/golden/prefill_c5_full.npz on the config-5 input itself, 4 x 4096).
 
 Tolerances. The fp32 check runs the trunk on the GPU with the CPU oracle in place of the MoE
 kernels, so it pins the GPU execution of every trunk op: logsumexp within 1e-4, stored logit rows
@@ -89,12 +90,79 @@ def test_prefill_bf16_hip_within_reference_bf16_spread(gpu, golden, params):
     assert _rel(ours, ref16) <= spread
 
 
-def test_prefill_full_config5_input(gpu, params):
-    """The config-5 input itself: 4 x 4096 packed tokens, EOS about every 1000."""
+GOLDEN_FULL = Path(__file__).resolve().parent / "golden" / "prefill_c5_full.npz"
+
+
+@pytest.fixture(scope="module")
+def golden_full():
+    return np.load(GOLDEN_FULL)
+
+
+def test_prefill_full_config5_fp32_trunk(gpu, golden_full, params):
+    """The config-5 input itself (4 x 4096 packed tokens, EOS about every 1000) against the
+    reference's fp32 forward on it, with the trunk on the GPU and the CPU oracle for the MoE blocks.
+
+    Bar. On this input a few tokens sit on a near-tie between their 5th and 6th expert, and two fp32
+    evaluation orders of the same forward choose differently there; the changed expert output then
+    moves the rest of that packed segment a little. The restated trunk run on the CPU already does
+    this against the reference's CPU forward (0.24 % of tokens beyond 1e-4 in logsumexp, in bursts
+    inside segments; everything else within 1e-5), so the bar is on the bulk: the 99th percentile of
+    the logsumexp difference below 1e-4, under 1 % of tokens beyond 1e-4, none beyond 1e-2, argmax
+    agreement above 99 %, and the stored logit rows within 1e-3 relative L2."""
+    g = golden_full
+    assert g["ids"].shape == (4, 4096)
+    ids = P.make_ids(4, 4096, P.c5_config())
+    assert np.array_equal(ids.numpy(), g["ids"].astype(np.int64)), "golden made from another input"
+
+    def oracle_moe(block, x):
+        w = {n: p.cpu() for n, p in block.named_parameters()}
+        B, S, h = x.shape
+        return O.reference_block_forward(x.reshape(-1, h).cpu(), w, block.gate.top_k).view(B, S, h).to(x.device)
+
+    model = P.Q38Prefill(P.c5_config(), moe_forward=oracle_moe).load_params(params).to(gpu)
+    with torch.inference_mode():
+        logits = model(ids.to(gpu))
+    lse = torch.logsumexp(logits, -1).cpu().numpy()
+    d = np.abs(lse - g["lse_fp32"])
+    print(f"full fp32 trunk: lse diff p50 {np.percentile(d, 50):.1e} p99 {np.percentile(d, 99):.1e} max "
+          f"{d.max():.1e}, beyond 1e-4: {(d > 1e-4).mean():.4f}")
+    assert np.percentile(d, 99) < 1e-4
+    assert (d > 1e-4).mean() < 0.01
+    assert d.max() < 1e-2
+    assert (logits.argmax(-1).cpu().numpy() == g["argmax_fp32"]).mean() > 0.99
+    assert _rel(_rows(logits, g), g["logits_fp32"]) < 1e-3
+
+
+def test_prefill_full_config5_bf16_hip(gpu, golden_full, params):
+    """The product path on the config-5 input itself (4 x 4096 packed tokens, the fused HIP MoE block
+    in all 12 layers): finite, deterministic, and within the reference's own bf16 spread of its fp32
+    forward on this input (the bars of the 2 x 1024 check)."""
+    g = golden_full
     cfg = P.c5_config()
     model = P.Q38Prefill(cfg).load_params(params).to(device=gpu, dtype=torch.bfloat16)
-    ids = P.make_ids(4, 4096, cfg).to(gpu)
+    ids = torch.from_numpy(g["ids"].astype(np.int64)).to(gpu)
     with torch.inference_mode():
-        logits = model(ids)
+        out = model(ids, output_router_logits=True)
+        again = model(ids)
+    logits = out.logits
     assert logits.shape == (4, 4096, cfg.vocab)
     assert torch.isfinite(logits).all()
+    assert torch.equal(logits, again), "the HIP prefill must be deterministic"
+    k = cfg.topk
+    spread_aux = abs(float(g["aux_loss_bf16"]) - float(g["aux_loss_fp32"]))
+    aux_ref = float(g["aux_loss_fp32"])
+    assert abs(float(out.aux_loss) - aux_ref) <= max(2 * spread_aux, 0.1 * abs(aux_ref - k))
+    ref32, ref16 = g["logits_fp32"], _bf16_rows(g["logits_bf16"])
+    spread = _rel(ref16, ref32)
+    spread_lse = np.abs(g["lse_bf16"] - g["lse_fp32"]).max()
+    spread_am = (g["argmax_bf16"] == g["argmax_fp32"]).mean()
+    ours = _rows(logits, g)
+    lse = torch.logsumexp(logits.float(), -1).cpu().numpy()
+    am = logits.float().argmax(-1).cpu().numpy()
+    print(f"full bf16: rows rel {_rel(ours, ref32):.3f} (reference bf16 {spread:.3f}), lse max diff "
+          f"{np.abs(lse - g['lse_fp32']).max():.3f} (reference bf16 {spread_lse:.3f}), argmax agreement "
+          f"{(am == g['argmax_fp32']).mean():.3f} (reference bf16 {spread_am:.3f})")
+    assert _rel(ours, ref32) <= 1.25 * spread
+    assert np.abs(lse - g["lse_fp32"]).max() <= 1.5 * spread_lse
+    assert (am == g["argmax_fp32"]).mean() >= spread_am - 0.1
+    assert _rel(ours, ref16) <= spread
