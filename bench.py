@@ -485,6 +485,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2")
+    ap.add_argument("--graph", action="store_true",
+                    help="time replays of the block captured as one HIP graph (q38.hip.graph.BlockGraph) "
+                         "instead of eager calls")
     ap.add_argument("--tokens", type=int, default=0,
                     help="run the workload's shapes on this many tokens (one sequence) instead of its own "
                          "batch x seq: decode and short-chunk sizes, where the small-tile GEMMs run")
@@ -535,8 +538,16 @@ def main():
         ws = torch.empty(ops.block_fp8_workspace_bytes(T, h, wl.experts, k, wl.inter), dtype=torch.uint8,
                          device=dev)
 
+    graph = None
+    if args.graph and not fp8:
+        from q38.hip.graph import BlockGraph
+        graph = BlockGraph(weights, k, T, logit_bias=bias)
+        graph.x.copy_(x)
+
     def step():
-        if fp8:
+        if graph is not None:
+            graph.replay()
+        elif fp8:
             ops.block_forward_fp8(x, d["gate.weight"], wq, d["shared_expert_gate.weight"], k, logit_bias=bias,
                                   workspace=ws, out=out)
         else:
@@ -589,7 +600,8 @@ def main():
         "config": {"workload": f"{wl.name}: one Q38 MoE block forward, {wl.batch}x{wl.seq} packed tokens",
                    "tokens": T, "hidden": h, "experts": wl.experts, "top_k": k, "expert_inter": wl.inter,
                    "shared_inter": wl.shared_inter, "routing_skew": wl.zipf_s, "parallelism": "single GPU",
-                   "gemm_tiling": kernels["gate_up"].get("tiling", "persistent")},
+                   "gemm_tiling": kernels["gate_up"].get("tiling", "persistent"),
+                   "launch": "hip_graph" if graph is not None else "eager"},
         "roofline": {"kernel": dom, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
                      "unit": dk["unit"], "frac": dk["frac"],
                      "traffic": None if args.tokens else hbm_traffic(wl.name, dom),
