@@ -48,11 +48,24 @@ __global__ __launch_bounds__(256) void permute_kernel(
   __shared__ int s_tile0[64];
   __shared__ int s_ntile[64];
   __shared__ int s_ccnt[NCHUNK][64];  // pairs per expert in each chunk, then the chunk's offsets
-  __shared__ int s_rem[256];
   const int tid = threadIdx.x, e = tid & 63, part = tid >> 6;
   const int lane = e, wave = part;
   const int b = blockIdx.x;
   for (int i = tid; i < NCHUNK * 64; i += 256) (&s_ccnt[0][0])[i] = 0;
+
+  // This block's pairs p0 + i, i = 64 c + lane for chunks c = wave, wave + 4: loaded first, so that
+  // their round trip overlaps the histogram scan's (they do not depend on it).
+  const int64_t t0 = (int64_t)b * PERM_TOKENS;
+  const int64_t t1 = min(t0 + PERM_TOKENS, T);
+  const int np = (int)((t1 - t0) * k);
+  const int64_t p0 = t0 * k;
+  const int nchunk = (np + 63) / 64;
+  int64_t vload[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int i = 64 * (wave + 4 * j) + lane;
+    vload[j] = i < np ? (int64_t)idx[p0 + i] : (int64_t)-1;
+  }
 
   // Expert totals over all blocks and the counts of the blocks before this one. Thread `tid`
   // sums column e over rows part, part + 4, ...; up to 64 independent loads are in flight per
@@ -94,11 +107,6 @@ __global__ __launch_bounds__(256) void permute_kernel(
   // rank among the earlier pairs of its chunk with the same expert is a popcount of the lanes
   // below it in the mask of equal ids, built from one ballot per id bit (ids 0..63, 64 = dropped:
   // out of range or past the block's pairs, like transformers' grouped_mm, moe.py:405-420).
-  const int64_t t0 = (int64_t)b * PERM_TOKENS;
-  const int64_t t1 = min(t0 + PERM_TOKENS, T);
-  const int np = (int)((t1 - t0) * k);
-  const int64_t p0 = t0 * k;
-  const int nchunk = (np + 63) / 64;
   int cv[2], crank[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -106,11 +114,8 @@ __global__ __launch_bounds__(256) void permute_kernel(
     cv[j] = 64;
     crank[j] = 0;
     if (c < nchunk) {  // wave-uniform
-      const int i = 64 * c + lane;
-      if (i < np) {
-        const int64_t v = (int64_t)idx[p0 + i];
-        if (v >= 0 && v < E) cv[j] = (int)v;
-      }
+      const int64_t v = vload[j];  // -1 past the block's pairs
+      if (v >= 0 && v < E) cv[j] = (int)v;
       uint64_t same = ~0ull;
 #pragma unroll
       for (int bit = 0; bit < 7; ++bit) {
@@ -184,55 +189,42 @@ __global__ __launch_bounds__(256) void permute_kernel(
   if (row_scale_out != nullptr && tid < t1 - t0 && t0 + tid < shared_rows)
     row_scale_out[cap + t0 + tid] = row_scale_in[t0 + tid];
 
-  if (b == 0 && tiles != nullptr) {
+  if (tiles != nullptr) {
     // Tile table, in the order the persistent grouped GEMM walks it: every full tile (block_m
     // rows) by expert, then the shared-expert rows [P, P + shared_rows) (group id E), then one
     // partial tile per group with a remainder, by falling row count (ties: lower group first),
     // then unused entries {-1, 0, 0, 0}. Cost falls along the list, so round-robin assignment
-    // balances the workgroups.
+    // balances the workgroups. Every block knows every group's totals, so the table is built in
+    // parallel: block b writes the entries of groups b, b + grid, ... (group E = the shared rows),
+    // block 0 the count and the unused entries.
     const int routed_full = s_tile0[63] + s_ntile[63];
     const int shared_full = shared_rows / block_m;
     const int full = routed_full + shared_full;
     const int64_t P = T * k;
-    // Partial tiles: group g < E from the routed counts, g == E the shared rows.
-    const int g = tid;
-    int rem = 0, row_start = 0;
-    if (g < E) {
-      rem = s_total[g] % block_m;
-      row_start = s_start[g] + s_ntile[g] * block_m;
-    } else if (g == E) {
-      rem = shared_rows % block_m;
-      row_start = (int)P + shared_full * block_m;
+    // Remainder (partial-tile rows) of group `tid`, for the ranks below.
+    const int h = tid;
+    const int rem_h = h < E ? s_total[h] % block_m : (h == E ? shared_rows % block_m : 0);
+    const int npartial = __syncthreads_count(h <= E && rem_h > 0);
+    for (int g = b; g <= E; g += (int)gridDim.x) {  // block-uniform
+      const int rem = g < E ? s_total[g] % block_m : shared_rows % block_m;
+      // Rank of group g's partial tile among all partial tiles.
+      const int rank = __syncthreads_count(h <= E && rem_h > 0 && (rem_h > rem || (rem_h == rem && h < g)));
+      if (tid == 0 && rem > 0) {
+        const int row_start = g < E ? s_start[g] + s_ntile[g] * block_m : (int)P + shared_full * block_m;
+        tiles[full + rank] = make_int4(g, row_start, rem, 0);
+      }
+      if (g < E) {
+        for (int j = tid; j < s_ntile[g]; j += 256)
+          tiles[s_tile0[g] + j] = make_int4(g, s_start[g] + j * block_m, block_m, 0);
+      } else {
+        for (int j = tid; j < shared_full; j += 256)
+          tiles[routed_full + j] = make_int4(E, (int)P + j * block_m, block_m, 0);
+      }
     }
-    s_rem[g] = rem;  // tid < 256 covers g <= E <= 64
-    __syncthreads();
-    // Rank of this group's partial tile among all partial tiles: groups 0..63 are read once into
-    // the lanes of every wave and broadcast lane by lane (v_readlane, no LDS round trip per group);
-    // group 64 (the shared rows when E == 64) is one more LDS read.
-    const int rl = s_rem[lane];
-    const int r64 = E >= 64 ? s_rem[64] : 0;
-    int rank = 0, npartial = 0;
-#pragma unroll 16
-    for (int h = 0; h < 64; ++h) {
-      const int rh = __builtin_amdgcn_readlane(rl, h);
-      const bool in = h <= E && rh > 0;
-      npartial += in;
-      rank += in && (rh > rem || (rh == rem && h < g));
+    if (b == 0) {
+      if (tid == 0 && tile_count != nullptr) *tile_count = full + npartial;
+      for (int i = full + npartial + tid; i < max_tiles; i += 256) tiles[i] = make_int4(-1, 0, 0, 0);
     }
-    if (E >= 64 && r64 > 0) {
-      npartial += 1;
-      rank += r64 > rem || (r64 == rem && 64 < g);
-    }
-    if (rem > 0) tiles[full + rank] = make_int4(g, row_start, rem, 0);
-    if (tid == 0 && tile_count != nullptr) *tile_count = full + npartial;
-    // Expert g's full tiles.
-    if (g < E) {
-      for (int j = 0; j < s_ntile[g]; ++j)
-        tiles[s_tile0[g] + j] = make_int4(g, s_start[g] + j * block_m, block_m, 0);
-    }
-    for (int i = routed_full + tid; i < full; i += 256)
-      tiles[i] = make_int4(E, (int)P + (i - routed_full) * block_m, block_m, 0);
-    for (int i = full + npartial + tid; i < max_tiles; i += 256) tiles[i] = make_int4(-1, 0, 0, 0);
   }
 }
 
