@@ -75,8 +75,13 @@ __device__ __forceinline__ float torch_topk_sum(const float* v) {
   return t;
 }
 
+// The selection's comparator (torch's topk on the CPU: NaN above every number). NANS = false is the
+// same order for rows without NaN, whose probabilities are all numbers (finite, or -inf in the
+// unused slots past E): the replay of such rows, nearly all of them, skips the NaN tests.
+template <bool NANS = true>
 __device__ __forceinline__ bool cmp_gt(float a, float b) {
-  return (__builtin_isnan(a) && !__builtin_isnan(b)) || (a > b);
+  if constexpr (NANS) return (__builtin_isnan(a) && !__builtin_isnan(b)) || (a > b);
+  else return a > b;
 }
 
 // Whole-wave reductions without LDS traffic: DPP within rows of 16 lanes (xor 1, xor 2, half-row
@@ -149,6 +154,7 @@ __device__ __forceinline__ void swap_slots(float& qv, int& qi, int lane, int a, 
 // moves to lo + (the number of slots in [lo, hi) holding a cmp-greater value, plus those before p
 // holding an equivalent one). Every lane computes that rank against the n values (read as
 // scalars) and one forward permute places the elements; lanes outside [lo, hi) keep theirs.
+template <bool NANS>
 __device__ void insertion_sort_slots(float& qv, int& qi, int lane, int lo, int hi) {
   const int n = hi - lo;
   if (n <= 1) return;
@@ -157,8 +163,8 @@ __device__ void insertion_sort_slots(float& qv, int& qi, int lane, int lo, int h
   for (int j = 0; j < KMAX; ++j) {
     if (j < n) {  // wave-uniform
       const float vj = lane_f(qv, lo + j);
-      const bool gt = cmp_gt(vj, qv);
-      const bool equiv = !gt && !cmp_gt(qv, vj);
+      const bool gt = cmp_gt<NANS>(vj, qv);
+      const bool equiv = !gt && !cmp_gt<NANS>(qv, vj);
       rank += (gt || (equiv && lo + j < lane)) ? 1 : 0;
     }
   }
@@ -168,12 +174,13 @@ __device__ void insertion_sort_slots(float& qv, int& qi, int lane, int lo, int h
 }
 
 // libstdc++ __adjust_heap + __push_heap on LDS arrays based at `first` (single lane).
+template <bool NANS>
 __device__ void heap_adjust(float* v, int* id, int first, int hole, int len, float val, int vid) {
   const int top = hole;
   int second = hole;
   while (second < (len - 1) / 2) {
     second = 2 * (second + 1);
-    if (cmp_gt(v[first + second], v[first + second - 1])) second--;
+    if (cmp_gt<NANS>(v[first + second], v[first + second - 1])) second--;
     v[first + hole] = v[first + second];
     id[first + hole] = id[first + second];
     hole = second;
@@ -185,7 +192,7 @@ __device__ void heap_adjust(float* v, int* id, int first, int hole, int len, flo
     hole = second - 1;
   }
   int parent = (hole - 1) / 2;
-  while (hole > top && cmp_gt(v[first + parent], val)) {
+  while (hole > top && cmp_gt<NANS>(v[first + parent], val)) {
     v[first + hole] = v[first + parent];
     id[first + hole] = id[first + parent];
     hole = parent;
@@ -197,6 +204,7 @@ __device__ void heap_adjust(float* v, int* id, int first, int hole, int len, flo
 
 // libstdc++ __heap_select(first, middle, last) followed by iter_swap(first, nth): the
 // depth-limit exit of __introselect. Runs on one lane over an LDS copy of the queue.
+template <bool NANS>
 __device__ void heap_select_slots(float& qv, int& qi, int lane, int first, int middle, int last,
                                   int nth, float* sv, int* si) {
   sv[lane] = qv;
@@ -209,18 +217,18 @@ __device__ void heap_select_slots(float& qv, int& qi, int lane, int first, int m
     if (len >= 2) {
       int parent = (len - 2) / 2;
       while (true) {
-        heap_adjust(sv, si, first, parent, len, sv[first + parent], si[first + parent]);
+        heap_adjust<NANS>(sv, si, first, parent, len, sv[first + parent], si[first + parent]);
         if (parent == 0) break;
         parent--;
       }
     }
     for (int i = middle; i < last; ++i) {
-      if (cmp_gt(sv[i], sv[first])) {
+      if (cmp_gt<NANS>(sv[i], sv[first])) {
         const float val = sv[i];
         const int vid = si[i];
         sv[i] = sv[first];
         si[i] = si[first];
-        heap_adjust(sv, si, first, 0, len, val, vid);
+        heap_adjust<NANS>(sv, si, first, 0, len, val, vid);
       }
     }
     const float tv = sv[first];
@@ -238,6 +246,7 @@ __device__ void heap_select_slots(float& qv, int& qi, int lane, int first, int m
 }
 
 // std::nth_element(q, q+k-1, q+n, cmp) then std::sort(q, q+k-1, cmp), with queue slot = lane.
+template <bool NANS>
 __device__ void nth_element_then_sort(float& qv, int& qi, int lane, int n, int k, float* sv,
                                       int* si) {
   const int nth = k - 1;
@@ -246,7 +255,7 @@ __device__ void nth_element_then_sort(float& qv, int& qi, int lane, int n, int k
   bool sorted_tail = true;
   while (last - first > 3) {
     if (depth == 0) {
-      heap_select_slots(qv, qi, lane, first, nth + 1, last, nth, sv, si);
+      heap_select_slots<NANS>(qv, qi, lane, first, nth + 1, last, nth, sv, si);
       sorted_tail = false;
       break;
     }
@@ -255,13 +264,13 @@ __device__ void nth_element_then_sort(float& qv, int& qi, int lane, int n, int k
     const int mid = first + (last - first) / 2;
     const float a = lane_f(qv, first + 1), b = lane_f(qv, mid), c = lane_f(qv, last - 1);
     int s;
-    if (cmp_gt(a, b)) {
-      if (cmp_gt(b, c)) s = mid;
-      else if (cmp_gt(a, c)) s = last - 1;
+    if (cmp_gt<NANS>(a, b)) {
+      if (cmp_gt<NANS>(b, c)) s = mid;
+      else if (cmp_gt<NANS>(a, c)) s = last - 1;
       else s = first + 1;
-    } else if (cmp_gt(a, c)) {
+    } else if (cmp_gt<NANS>(a, c)) {
       s = first + 1;
-    } else if (cmp_gt(b, c)) {
+    } else if (cmp_gt<NANS>(b, c)) {
       s = last - 1;
     } else {
       s = mid;
@@ -274,8 +283,8 @@ __device__ void nth_element_then_sort(float& qv, int& qi, int lane, int n, int k
     // li = the i-th left stop and ri = the i-th right stop counted from the right by a forward
     // permute (each stop sends its position to the lane of its rank; lane 63 is never a rank a
     // left stop or a partial right-stop set reaches, so the other lanes send there).
-    const bool isl = lane > first && lane < last && !cmp_gt(qv, pv);
-    const bool isg = lane >= first && lane < last && !cmp_gt(pv, qv);
+    const bool isl = lane > first && lane < last && !cmp_gt<NANS>(qv, pv);
+    const bool isg = lane >= first && lane < last && !cmp_gt<NANS>(pv, qv);
     const uint64_t le = ballot64(isl);
     const uint64_t ge = ballot64(isg);
     const int nl = __popcll(le), nr = __popcll(ge);
@@ -305,15 +314,48 @@ __device__ void nth_element_then_sort(float& qv, int& qi, int lane, int n, int k
     if (cut <= nth) first = cut;
     else last = cut;
   }
-  if (sorted_tail) insertion_sort_slots(qv, qi, lane, first, last);
+  if (sorted_tail) insertion_sort_slots<NANS>(qv, qi, lane, first, last);
   // std::sort on k-1 <= 16 elements is __insertion_sort.
-  insertion_sort_slots(qv, qi, lane, 0, k - 1);
+  insertion_sort_slots<NANS>(qv, qi, lane, 0, k - 1);
+}
+
+// Selection and renormalisation for one token held by the calling wave, from its fp32
+// probabilities: p of expert `lane` (lanes >= E ignored); all_nan when the row's softmax is NaN
+// everywhere. The selection replays libstdc++ on them. Lane r < K receives the r-th selected expert
+// and its renormalised weight.
+template <int K>
+__device__ void select_token(float p, bool all_nan, int lane, int E, int& out_idx, float& out_w, float* sv,
+                             int* si) {
+  const bool valid = lane < E;
+  float qv = valid ? p : -INFINITY;
+  int qi = lane;
+
+  if (K * 64 <= E) {
+    // std::partial_sort path (K == 1, E == 64): first slot whose value is cmp-greater than all
+    // before it = lowest-index maximum (slot 0 when every value is NaN).
+    int best = 0;
+    if (!all_nan) {
+      const uint64_t key = valid ? ((uint64_t)order_key(qv) << 32) | (uint32_t)(63 - lane) : 0ull;
+      best = 63 - (int)(uint32_t)wave_max_u64(key);
+    }
+    qi = best;
+  } else if (all_nan) {
+    nth_element_then_sort<true>(qv, qi, lane, E, K, sv, si);
+  } else {
+    nth_element_then_sort<false>(qv, qi, lane, E, K, sv, si);
+  }
+  // Renormalise over the selected probabilities with torch's row-sum order, then divide.
+  const float pr = __shfl(p, qi & 63);
+  float v[K];
+#pragma unroll
+  for (int r = 0; r < K; ++r) v[r] = lane_f(pr, r);
+  out_idx = qi;
+  out_w = pr / torch_topk_sum<K>(v);
 }
 
 // Route one token held by the calling wave. z: selection input of expert `lane` (bf16 logit plus
 // the optional bias; lanes >= E ignored). The fp32 probabilities follow torch's CPU softmax bit
-// for bit, and the selection replays libstdc++ on them. Lane r < K receives the r-th selected
-// expert and its renormalised weight.
+// for bit; then select_token.
 template <int K>
 __device__ void route_token(float z, int lane, int E, int& out_idx, float& out_w, float* sv, int* si) {
   const bool valid = lane < E;
@@ -345,28 +387,7 @@ __device__ void route_token(float z, int lane, int E, int& out_idx, float& out_w
     }
     p = ex * (1.0f / sum);
   }
-  float qv = valid ? p : -INFINITY;
-  int qi = lane;
-
-  if (K * 64 <= E) {
-    // std::partial_sort path (K == 1, E == 64): first slot whose value is cmp-greater than all
-    // before it = lowest-index maximum (slot 0 when every value is NaN).
-    int best = 0;
-    if (!all_nan) {
-      const uint64_t key = valid ? ((uint64_t)order_key(qv) << 32) | (uint32_t)(63 - lane) : 0ull;
-      best = 63 - (int)(uint32_t)wave_max_u64(key);
-    }
-    qi = best;
-  } else {
-    nth_element_then_sort(qv, qi, lane, E, K, sv, si);
-  }
-  // Renormalise over the selected probabilities with torch's row-sum order, then divide.
-  const float pr = __shfl(p, qi & 63);
-  float v[K];
-#pragma unroll
-  for (int r = 0; r < K; ++r) v[r] = lane_f(pr, r);
-  out_idx = qi;
-  out_w = pr / torch_topk_sum<K>(v);
+  select_token<K>(p, all_nan, lane, E, out_idx, out_w, sv, si);
 }
 
 constexpr int ROUTE_TOKENS = 64;   // per block: 4 MFMA waves x 16 tokens
@@ -378,6 +399,9 @@ constexpr int ROUTE_WROWS = 65;    // 64 expert rows + the shared-expert gate ro
 __device__ __forceinline__ int wr_slot(int n, int c) { return n * (ROUTE_KCHUNK / 8) + (c ^ (n & 15)); }
 
 constexpr int SEL_LANES = 8;  // lanes per token in the selection fast path
+// Outcomes of group_select: selected; tie (the row's probabilities are left in LDS for the
+// replay); NaN or a non-finite maximum (the replay starts from the logits).
+enum { SEL_DONE = 0, SEL_REPLAY_PROBS = 1, SEL_REPLAY_LOGITS = 2 };
 
 // Value of lane (lane ^ O) for O in {1, 2, 4}, by DPP (no LDS round trip): quad permutes for 1 and
 // 2; for 4, the half-row mirror (lane i of each 8 takes 7 - i) followed by the quad reverse (i takes
@@ -456,8 +480,8 @@ __device__ __forceinline__ void merge_round(float (&v)[NP], int (&id)[NP], int& 
 // largest probabilities are not all distinct (or the row has a NaN / non-finite max); such tokens
 // need the libstdc++ replay. Every lane of the group returns the same answer.
 template <int KP1>
-__device__ __forceinline__ bool group_select(const float* row, const float* bias, int E, int s,
-                                             int* out_idx, float* out_w) {
+__device__ __forceinline__ int group_select(float* row, const float* bias, int E, int s,
+                                            int* out_idx, float* out_w) {
   constexpr int K = KP1 - 1;
   constexpr int PER = 64 / SEL_LANES;  // 8 values per lane
   constexpr int NP = KP1 <= 8 ? 8 : 16;
@@ -481,7 +505,7 @@ __device__ __forceinline__ bool group_select(const float* row, const float* bias
   nan |= xor_lanes<1>(nan);
   nan |= xor_lanes<2>(nan);
   nan |= xor_lanes<4>(nan);
-  if (nan || !__builtin_isfinite(mx)) return false;
+  if (nan || !__builtin_isfinite(mx)) return SEL_REPLAY_LOGITS;
   float ex[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) ex[j] = s + SEL_LANES * j < E ? torch_cpu_expf(z[j] - mx) : 0.0f;
@@ -528,10 +552,19 @@ __device__ __forceinline__ bool group_select(const float* row, const float* bias
   merge_round<2>(v, id, dummy);
   merge_round<4>(v, id, dummy);
   const int lim = min(K, E - 1);
+  bool tie = false;
 #pragma unroll
   for (int r = 0; r < KP1 - 1; ++r) {
-    if (r < lim && v[r] == v[r + 1]) return false;
-    if (r == K - 1 && v[r] == -INFINITY) return false;  // fewer than k experts: replay
+    if (r < lim && v[r] == v[r + 1]) tie = true;
+    if (r == K - 1 && v[r] == -INFINITY) tie = true;  // fewer than k experts: replay
+  }
+  if (tie) {
+    // The replay starts from these probabilities: they replace the row's logits in LDS (read by
+    // nothing else from here on).
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (s + SEL_LANES * j < E) row[s + SEL_LANES * j] = ex[j] * rs;
+    return SEL_REPLAY_PROBS;
   }
   const float tot = torch_topk_sum<K>(v);
 #pragma unroll
@@ -539,7 +572,7 @@ __device__ __forceinline__ bool group_select(const float* row, const float* bias
     out_idx[r] = id[r];
     out_w[r] = v[r] / tot;
   }
-  return true;
+  return SEL_DONE;
 }
 
 
@@ -689,10 +722,10 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     if (t < T) {  // uniform over the token's lanes
       int oi[KMAX];
       float ow[KMAX];
-      const bool ok = group_select<KT + 1>(s_logit[tl], bias != nullptr ? s_bias : nullptr, E,
+      const int sel = group_select<KT + 1>(s_logit[tl], bias != nullptr ? s_bias : nullptr, E,
                                            lane % SEL_LANES, oi, ow);
       if (lane % SEL_LANES == 0) {
-        if (ok) {
+        if (sel == SEL_DONE) {
           for (int r = 0; r < k; ++r) {
             idx_out[t * k + r] = oi[r];
             if (F32IO) static_cast<float*>(w_out)[t * k + r] = ow[r];
@@ -700,7 +733,7 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
             atomicAdd(&s_hist[oi[r]], 1);
           }
         } else {
-          s_ties[atomicAdd(&s_nties, 1)] = tl;
+          s_ties[atomicAdd(&s_nties, 1)] = tl | (sel == SEL_REPLAY_PROBS ? 0x100 : 0);
         }
       }
     }
@@ -710,12 +743,17 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
   // Phase 4: tied tokens, one wave each.
   const int nties = s_nties;
   for (int q = wave; q < nties; q += ROUTE_THREADS / 64) {
-    const int tl = s_ties[q];
+    const int tl = s_ties[q] & 0xff;
+    const bool probs = (s_ties[q] & 0x100) != 0;  // wave-uniform
     const int64_t t = tb + tl;
-    const float z = lane < E ? s_logit[tl][lane] + s_bias[lane] : -INFINITY;
     int oi;
     float ow;
-    route_token<KT>(z, lane, E, oi, ow, s_sv[wave], s_si[wave]);
+    if (probs) {
+      select_token<KT>(lane < E ? s_logit[tl][lane] : 0.0f, false, lane, E, oi, ow, s_sv[wave], s_si[wave]);
+    } else {
+      const float z = lane < E ? s_logit[tl][lane] + s_bias[lane] : -INFINITY;
+      route_token<KT>(z, lane, E, oi, ow, s_sv[wave], s_si[wave]);
+    }
     if (lane < k) {
       idx_out[t * k + lane] = oi;
       if (F32IO) static_cast<float*>(w_out)[t * k + lane] = ow;
