@@ -86,6 +86,8 @@ def test_small_tile_stages(gpu, name, T, hot):
     ("c3", 300, {}),
     ("c2", 200, {"shared_inter": 128}),  # separate shared expert: shared rows not in the tile table
     ("c2", 60, {"experts": 17, "topk": 8, "hidden": 512, "inter": 128, "shared_inter": 128}),
+    ("c2", 40, {"hidden": 2048, "inter": 512, "shared_inter": 512}),  # K = 2048 (gate/up), 512 (down)
+    ("c2", 25, {"experts": 1, "topk": 1, "hidden": 128, "inter": 128, "shared_inter": 128}),  # K = 128
 ])
 def test_small_tile_block(gpu, name, T, over):
     """Whole block through the tiling rule: routing bit-exact on the GPU's logits, output within the
