@@ -2,8 +2,9 @@
 against q38moe_block_forward (caller workspace), through the C ABI: the same kernels on the same
 inputs, so outputs, logits, routing indices and weights are bit-identical. Two calls in a row, the
 second smaller and on other tokens, so that anything read from the previous call's scratch would
-show; the fused shared expert (Is == I), the separate one (Is != I) and the skew bias; shapes beyond
-the scratch are refused with the library's message."""
+show; the fused shared expert (Is == I), the separate one (Is != I), the skew bias and token counts
+on the small-tile side of the GEMM tiling rule; shapes beyond the scratch are refused with the
+library's message."""
 import pytest
 import torch
 
@@ -19,17 +20,27 @@ def _weights(wl, gpu):
     return x.to(gpu), [params[n].to(gpu) for n in NAMES], (None if bias is None else bias.to(gpu))
 
 
-@pytest.mark.parametrize("name,Is", [("c2", None), ("c3", None), ("c2", 128)])
-def test_noalloc_matches_block_forward(gpu, name, Is):
+LARGE = ((0, 2048, "persistent"), (1200, 1900, "persistent"))
+
+
+@pytest.mark.parametrize("name,Is,spans", [
+    ("c2", None, LARGE),
+    ("c3", None, LARGE),
+    ("c2", 128, LARGE),
+    ("c2", None, ((0, 300, "small"), (500, 517, "small"))),
+])
+def test_noalloc_matches_block_forward(gpu, name, Is, spans):
     from q38 import workloads
     from q38.hip import ops
     wl = workloads.get(name) if Is is None else workloads.get(name, shared_inter=Is)
     x, W, bias = _weights(wl, gpu)
     k = wl.topk
-    for lo, hi in ((0, 2048), (1200, 1900)):  # second call: fewer tokens, other tokens
+    for lo, hi, want_kind in spans:  # second call: fewer tokens, other tokens
         xs = x[lo:hi].contiguous()
         T = xs.shape[0]
-        print(f"noalloc {name} Is={wl.shared_inter} T={T}", flush=True)
+        kind = ops.gemm_tiling(T, wl.hidden, wl.experts, k, wl.inter, T if wl.shared_inter == wl.inter else 0)
+        print(f"noalloc {name} Is={wl.shared_inter} T={T} {kind} tiles", flush=True)
+        assert kind == want_kind
         ref = ops.block_forward(xs, *W, k, logit_bias=bias, return_router=True)
         E = W[0].shape[0]
         logits = torch.empty(T, E, dtype=torch.bfloat16, device=gpu)
