@@ -21,8 +21,9 @@
 // tile's row count skip their MFMAs; rows are paired across SIMDs (waves 0-3 hold rows 0-127), so
 // a tile of <= 128 rows costs half a full one.
 //
-// The kernel is persistent: workgroup b walks tiles slot(b), slot(b) + G, ... (G = grid size) of a
-// list the permutation orders full tiles first and partial tiles by falling row count. Its async
+// The kernel is persistent: workgroup b walks tiles slot(b), slot(b) + G, ... (G = grid size; for
+// down, half of the workgroups walk theirs backwards) of a list the permutation orders full tiles
+// first and partial tiles by falling row count. Its async
 // copy streams (global_load_lds_dwordx4 into LDS rings: activation rows 3 slices ahead in a
 // 4-slot ring, copied by waves 0-3; weight rows 2 slices ahead in a 3-slot ring, waves 4-7) run
 // on across tile boundaries, so the next tile's first slices load during this tile's epilogue. The
@@ -255,6 +256,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
   const int used = used_m * p.ntiles_n;
   int L = slot;
   if (L >= used) return;
+  // Down: every other group of ntiles_n consecutive slots (one row tile's column tiles; each XCD
+  // holds a contiguous run of slots, so every XCD has both kinds) walks its units last to first.
+  // The same units per workgroup, in another order: the XCD's epilogues, which write 128 KiB of
+  // Y each, no longer fall at the same moments across all of its CUs (down 77-78 -> 73-74 us at
+  // configuration 2; gate/up, whose outputs are a quarter the size, gains nothing from it).
+  const bool reverse = MODE == MODE_DOWN && ((slot / p.ntiles_n) & 1) != 0;
+  const int step = reverse ? -G : G;
+  if (reverse) L = slot + ((used - 1 - slot) / G) * G;
   const int nk = p.K / BK;
   // This wave's copy distance and ring: activation rows (gathered, farther away in the memory
   // hierarchy) run NA - 1 = 3 slices ahead, weight rows (shared by the concurrent tiles of an
@@ -280,8 +289,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
   auto rot_of = [&](int4 t_, int u) { return (t_.x < p.E ? 2 * t_.x : 2 * (u / p.ntiles_n)) % nk; };
   int4 ti = tile_entry(p, L / p.ntiles_n);
   int rot = rot_of(ti, L);
-  int Ln = L + G;
-  int4 tin = Ln < used ? tile_entry(p, Ln / p.ntiles_n) : make_int4(0, 0, 0, 0);
+  int Ln = L + step;
+  int4 tin = (Ln >= 0 && Ln < used) ? tile_entry(p, Ln / p.ntiles_n) : make_int4(0, 0, 0, 0);
   int rows[NCOPY], rows_n[NCOPY];
   const uint16_t* src[NCOPY];
   const uint16_t* src_n[NCOPY];
@@ -334,8 +343,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
       for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[t][mi][i] = 0.0f;
-    const bool has_next = Ln < used;
-    const int Lnn = Ln + G;
+    const bool has_next = Ln >= 0 && Ln < used;
+    const int Lnn = Ln + step;
     int4 tinn = make_int4(0, 0, 0, 0);
     const bool active = 64 * wm < ti.z;
     const bool next_async = has_next && async_rows && gathered<MODE>(p, tin);
@@ -346,7 +355,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
         const int r = 64 * wave + lane;
         dma4(p.perm + tin.y + (r < tin.z ? r : 0), lds_addr(next_rows + 64 * wave));
       }
-      if (Lnn < used) tinn = tile_entry(p, Lnn / p.ntiles_n);
+      if (Lnn >= 0 && Lnn < used) tinn = tile_entry(p, Lnn / p.ntiles_n);
     }
 
     // Step: wait until at most N of this wave's vector-memory operations are outstanding, which
