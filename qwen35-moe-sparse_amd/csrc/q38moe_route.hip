@@ -724,17 +724,27 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
       float ow[KMAX];
       const int sel = group_select<KT + 1>(s_logit[tl], bias != nullptr ? s_bias : nullptr, E,
                                            lane % SEL_LANES, oi, ow);
-      if (lane % SEL_LANES == 0) {
-        if (sel == SEL_DONE) {
-          for (int r = 0; r < k; ++r) {
-            idx_out[t * k + r] = oi[r];
-            if (F32IO) static_cast<float*>(w_out)[t * k + r] = ow[r];
-            else static_cast<uint16_t*>(w_out)[t * k + r] = (uint16_t)f32_to_bf16_rne(ow[r]);
-            atomicAdd(&s_hist[oi[r]], 1);
+      const int s = lane % SEL_LANES;
+      if (sel == SEL_DONE) {
+        // Every lane of the group holds the answer; lane s < k writes pair s (index, weight and
+        // histogram count), so the k outputs of a token leave in one store each.
+        if (s < KT) {
+          int my_i = oi[0];
+          float my_w = ow[0];
+#pragma unroll
+          for (int r = 1; r < KT; ++r) {
+            if (s == r) {
+              my_i = oi[r];
+              my_w = ow[r];
+            }
           }
-        } else {
-          s_ties[atomicAdd(&s_nties, 1)] = tl | (sel == SEL_REPLAY_PROBS ? 0x100 : 0);
+          idx_out[t * KT + s] = my_i;
+          if (F32IO) static_cast<float*>(w_out)[t * KT + s] = my_w;
+          else static_cast<uint16_t*>(w_out)[t * KT + s] = (uint16_t)f32_to_bf16_rne(my_w);
+          atomicAdd(&s_hist[my_i], 1);
         }
+      } else if (s == 0) {
+        s_ties[atomicAdd(&s_nties, 1)] = tl | (sel == SEL_REPLAY_PROBS ? 0x100 : 0);
       }
     }
   }
