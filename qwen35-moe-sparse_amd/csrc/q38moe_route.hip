@@ -8,7 +8,7 @@
 // (std::partial_sort when k*64 <= n). The selection here replays libstdc++'s introselect step by
 // step, with each Hoare partition evaluated wave-parallel (one lane per queue slot), so indices
 // match the CPU library bit for bit. Rows whose k+1 largest values are all distinct have a unique
-// answer and take a fast path (k+1 wave arg-max rounds).
+// answer and take a fast path (k rounds of a group-wide maximum over 8 lanes per token).
 //
 // Selection compares the fp32 probabilities themselves, computed bit for bit as torch's CPU
 // softmax computes them (torch_softmax_* below), so rows whose distinct logits collapse to equal
@@ -417,75 +417,22 @@ template <int O>
 __device__ __forceinline__ float xor_lanes_f(float v) { return __int_as_float(xor_lanes<O>(__float_as_int(v))); }
 
 
-// Compare-exchange for a descending list: afterwards v[i] >= v[j] (unless one is NaN; rows with a
-// NaN take the replay path, so their order here does not matter).
-__device__ __forceinline__ void cas_desc(float& vi, int& ii, float& vj, int& ij) {
-  const bool sw = vj > vi;
-  const float tv = sw ? vj : vi, bv = sw ? vi : vj;
-  const int ti = sw ? ij : ii, bi = sw ? ii : ij;
-  vi = tv; ii = ti; vj = bv; ij = bi;
-}
-
-// Sorts a bitonic list of NP (a power of two) into descending order: log2(NP) half-cleaner stages.
-template <int NP>
-__device__ __forceinline__ void bitonic_merge_desc(float (&v)[NP], int (&id)[NP]) {
-#pragma unroll
-  for (int d = NP / 2; d > 0; d >>= 1)
-#pragma unroll
-    for (int i = 0; i < NP; ++i)
-      if ((i & d) == 0) cas_desc(v[i], id[i], v[i + d], id[i + d]);
-}
-
-// Descending sort of 8 values (Batcher's odd-even merge sort network, 19 compare-exchanges).
-__device__ __forceinline__ void sort8_desc(float (&v)[8], int (&id)[8]) {
-#define Q38_CE(A, B) cas_desc(v[A], id[A], v[B], id[B])
-  Q38_CE(0, 1); Q38_CE(2, 3); Q38_CE(4, 5); Q38_CE(6, 7);
-  Q38_CE(0, 2); Q38_CE(1, 3); Q38_CE(4, 6); Q38_CE(5, 7);
-  Q38_CE(1, 2); Q38_CE(5, 6);
-  Q38_CE(0, 4); Q38_CE(1, 5); Q38_CE(2, 6); Q38_CE(3, 7);
-  Q38_CE(2, 4); Q38_CE(3, 5);
-  Q38_CE(1, 2); Q38_CE(3, 4); Q38_CE(5, 6);
-#undef Q38_CE
-}
-
-// One merge round of group_select (partner = lane ^ O): keeps the NP largest of the two sorted
-// lists (elementwise max of one list and the other reversed is bitonic) and re-sorts them.
-template <int O, int NP>
-__device__ __forceinline__ void merge_round(float (&v)[NP], int (&id)[NP], int& nan) {
-  float ov[NP];
-  int oid[NP];
-#pragma unroll
-  for (int r = 0; r < NP; ++r) {
-    ov[r] = xor_lanes_f<O>(v[NP - 1 - r]);
-    oid[r] = xor_lanes<O>(id[NP - 1 - r]);
-  }
-  nan |= xor_lanes<O>(nan);
-#pragma unroll
-  for (int r = 0; r < NP; ++r) {
-    const bool take = ov[r] > v[r];
-    v[r] = take ? ov[r] : v[r];
-    id[r] = take ? oid[r] : id[r];
-  }
-  bitonic_merge_desc<NP>(v, id);
-}
-
 // Per-token selection by a group of SEL_LANES lanes (lane s of the group holds experts s,
 // s + SEL_LANES, ...). The group computes the row's fp32 probabilities as torch's CPU softmax does
 // (the 16 partial sums of its vector reduction are lanes s and s + 8 of the two interleaved
-// halves of each lane's experts, folded l ^ 8 locally, then across lanes ^ 4, ^ 2, ^ 1). Each lane
-// sorts its 8 probabilities; the groups' sorted lists of NP >= KP1 are merged by xor-shuffle rounds,
-// each keeping the NP largest of two lists (elementwise max of one list and the other reversed is a
-// bitonic sequence holding them) and re-sorting them with a bitonic merge. Equal values are kept as
-// often as they occur, so duplicates among the k+1 largest are seen. Returns false when the k+1
-// largest probabilities are not all distinct (or the row has a NaN / non-finite max); such tokens
-// need the libstdc++ replay. Every lane of the group returns the same answer.
+// halves of each lane's experts, folded l ^ 8 locally, then across lanes ^ 4, ^ 2, ^ 1). Then k
+// rounds of a group-wide maximum: each round takes the largest remaining probability (a local max
+// over the lane's 8, then three lane exchanges), counts how often it occurs in the row and removes
+// every occurrence. A count above one among the first k rounds means the k+1 largest values are
+// not all distinct. Returns SEL_DONE with the k largest in descending order when they are; else
+// (or when the row has a NaN / non-finite max, or fewer than k experts) the token needs the
+// libstdc++ replay. Every lane of the group returns the same answer.
 template <int KP1>
 __device__ __forceinline__ int group_select(float* row, const float* bias, int E, int s,
                                             int* out_idx, float* out_w) {
   constexpr int K = KP1 - 1;
   constexpr int PER = 64 / SEL_LANES;  // 8 values per lane
-  constexpr int NP = KP1 <= 8 ? 8 : 16;
-  static_assert(SEL_LANES == 8, "the reduction and merge rounds below are for 8 lanes per token");
+  static_assert(SEL_LANES == 8, "the reductions below are for 8 lanes per token");
   float z[PER];
   int nan = 0;
   float mx = -INFINITY;
@@ -530,33 +477,39 @@ __device__ __forceinline__ int group_select(float* row, const float* bias, int E
     }
   }
   const float rs = 1.0f / sum;
-  float v[NP];
-  int id[NP];
-  {
-    float lv[8];
-    int li[8];
+  float lv[PER];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      lv[j] = s + SEL_LANES * j < E ? ex[j] * rs : -INFINITY;
-      li[j] = s + SEL_LANES * j;
-    }
-    sort8_desc(lv, li);
-#pragma unroll
-    for (int r = 0; r < NP; ++r) {
-      v[r] = r < 8 ? lv[r & 7] : -INFINITY;
-      id[r] = r < 8 ? li[r & 7] : -1;
-    }
-  }
-  int dummy = 0;
-  merge_round<1>(v, id, dummy);
-  merge_round<2>(v, id, dummy);
-  merge_round<4>(v, id, dummy);
+  for (int j = 0; j < PER; ++j) lv[j] = s + SEL_LANES * j < E ? ex[j] * rs : -INFINITY;
   const int lim = min(K, E - 1);
   bool tie = false;
+  float v[K];
+  int id[K];
 #pragma unroll
-  for (int r = 0; r < KP1 - 1; ++r) {
-    if (r < lim && v[r] == v[r + 1]) tie = true;
-    if (r == K - 1 && v[r] == -INFINITY) tie = true;  // fewer than k experts: replay
+  for (int r = 0; r < K; ++r) {
+    float m = lv[0];
+#pragma unroll
+    for (int j = 1; j < PER; ++j) m = fmaxf(m, lv[j]);
+    m = fmaxf(m, xor_lanes_f<1>(m));
+    m = fmaxf(m, xor_lanes_f<2>(m));
+    m = fmaxf(m, xor_lanes_f<4>(m));
+    int c = 0, ix = 64;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const bool eq = lv[j] == m;
+      c += eq ? 1 : 0;
+      ix = eq ? min(ix, s + SEL_LANES * j) : ix;
+      lv[j] = eq ? -INFINITY : lv[j];
+    }
+    c += xor_lanes<1>(c);
+    c += xor_lanes<2>(c);
+    c += xor_lanes<4>(c);
+    ix = min(ix, xor_lanes<1>(ix));
+    ix = min(ix, xor_lanes<2>(ix));
+    ix = min(ix, xor_lanes<4>(ix));
+    if (r < lim && c > 1) tie = true;            // v[r] == v[r + 1]
+    if (r == K - 1 && m == -INFINITY) tie = true;  // fewer than k experts: replay
+    v[r] = m;
+    id[r] = ix;
   }
   if (tie) {
     // The replay starts from these probabilities: they replace the row's logits in LDS (read by
