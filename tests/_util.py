@@ -19,6 +19,27 @@ def assert_bf16_close(actual, expected, max_abs=BF16_MAX_ABS, rel=BF16_REL, what
     return mx, r
 
 
+# fp32 path: the reference's fp32 experts bar (scripts/check_q38_kernels.py:26).
+FP32_RTOL, FP32_ATOL = 1e-4, 2e-8
+
+
+def assert_fp32_close(actual, expected, what, allowance=None):
+    """torch.allclose(actual, expected, rtol=1e-4, atol=2e-8) elementwise, optionally widened by an
+    fp32 accumulation allowance (for intermediates whose sums cancel)."""
+    a = actual.detach().cpu()
+    b = expected.detach().cpu()
+    assert a.dtype == torch.float32 and a.shape == b.shape, what
+    err = (a - b).abs()
+    bound = FP32_ATOL + FP32_RTOL * b.abs()
+    if allowance is not None:
+        bound = bound + allowance
+    bad = err > bound
+    worst = float((err / bound).max()) if err.numel() else 0.0
+    print(f"{what}: max-abs {float(err.max()):.3e}, worst err/bound {worst:.3f}")
+    assert not bool(bad.any()), \
+        f"{what}: {int(bad.sum())} of {bad.numel()} outside rtol {FP32_RTOL}, atol {FP32_ATOL}"
+
+
 def bf16_ulp_diff(a, b):
     """|ordinal(a) - ordinal(b)| of bf16 values, elementwise (0 = identical bits)."""
     def ordinal(t):

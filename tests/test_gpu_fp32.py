@@ -14,27 +14,10 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from _util import assert_fp32_close as _assert_fp32_close
 from oracle import moe_oracle as orc
 
 pytestmark = pytest.mark.gpu
-
-RTOL, ATOL = 1e-4, 2e-8
-
-
-def _assert_fp32_close(actual, expected, what, allowance=None):
-    """torch.allclose(actual, expected, rtol=1e-4, atol=2e-8) elementwise, optionally widened by an
-    fp32 accumulation allowance (for intermediates whose sums cancel)."""
-    a = actual.detach().cpu()
-    b = expected.detach().cpu()
-    assert a.dtype == torch.float32 and a.shape == b.shape, what
-    err = (a - b).abs()
-    bound = ATOL + RTOL * b.abs()
-    if allowance is not None:
-        bound = bound + allowance
-    bad = err > bound
-    worst = float((err / bound).max()) if err.numel() else 0.0
-    print(f"{what}: max-abs {float(err.max()):.3e}, worst err/bound {worst:.3f}")
-    assert not bool(bad.any()), f"{what}: {int(bad.sum())} of {bad.numel()} outside rtol {RTOL}, atol {ATOL}"
 
 
 def _c1(T, seed_x=1234, **over):
