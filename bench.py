@@ -424,11 +424,10 @@ def backward_bench(args):
         H = ops.gate_up(xb, wgu, perm, tiles, tcount, k)
         Y = ops.down(H, wdn, tiles, tcount, T, k)
         d_raw = ops.gather_rows(dout, perm, starts, counts, k, w=wb)
-        wdn_t, wgu_t = ops.transpose_experts(wdn), ops.transpose_experts(wgu)
-        dH = ops.down(d_raw, wdn_t, tiles, tcount, T, k)
+        dH = ops.down_kn(d_raw, wdn, tiles, tcount, T, k)
         GU = ops.gather_gemm(xb, perm, wgu, tiles, tcount, k)
         dGU = ops.swiglu_backward(dH, GU)
-        dxp = ops.down(dGU, wgu_t, tiles, tcount, T, k)
+        dxp = ops.down_kn(dGU, wgu, tiles, tcount, T, k)
         ones = torch.ones_like(wb)
         xs = ops.gather_rows(xb, perm, starts, counts, k)
         it = args.kernel_iters
@@ -436,12 +435,10 @@ def backward_bench(args):
         by = lambda n: {"work": n, "unit": "GB/s", "peak": PEAK_HBM / 1e9, "bound": "hbm"}
         stages = {
             "pair_dots_rows": (lambda: ops.pair_dots(dout, Y, inv, idx, E, w=wb), by(2 * (T * h + 2 * P * h) + 4 * P)),
-            "transpose_down_proj": (lambda: ops.transpose_experts(wdn), by(2 * 2 * E * h * I)),
-            "dH_down_t": (lambda: ops.down(d_raw, wdn_t, tiles, tcount, T, k), fl(2 * P * h * I)),
+            "dH_down_kn": (lambda: ops.down_kn(d_raw, wdn, tiles, tcount, T, k), fl(2 * P * h * I)),
             "gate_up_recompute": (lambda: ops.gather_gemm(xb, perm, wgu, tiles, tcount, k), fl(2 * P * h * 2 * I)),
             "swiglu_backward": (lambda: ops.swiglu_backward(dH, GU), by(2 * (P * I + 2 * P * 2 * I))),
-            "transpose_gate_up_proj": (lambda: ops.transpose_experts(wgu), by(2 * 2 * E * 2 * I * h)),
-            "dx_down_t": (lambda: ops.down(dGU, wgu_t, tiles, tcount, T, k), fl(2 * P * 2 * I * h)),
+            "dx_down_kn": (lambda: ops.down_kn(dGU, wgu, tiles, tcount, T, k), fl(2 * P * 2 * I * h)),
             "dx_combine": (lambda: ops.combine(dxp, inv, ones, E, idx=idx), by(2 * (P * h + T * h))),
             "wgrad_gate_up": (lambda: ops.expert_wgrad(dGU, xb, starts, counts, k, perm=perm), fl(2 * P * 2 * I * h)),
             "wgrad_gate_up_presorted": (lambda: ops.expert_wgrad(dGU, xs, starts, counts, k), fl(2 * P * 2 * I * h)),

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define Q38MOE_ABI_VERSION 10
+#define Q38MOE_ABI_VERSION 11
 
 #define Q38MOE_OK 0
 #define Q38MOE_EINVAL (-1)   /* bad shape, null pointer, misalignment, unsupported dtype */
@@ -322,8 +322,8 @@ int q38moe_block_forward_fp8(const void* x, const void* w_router, const void* wq
 /*
  * Experts backward (the differentiable experts path, inference.py:358-384, whose gradients of x,
  * top_k_weights, gate_up_proj and down_proj scripts/check_q38_kernels.py:19-27 checks). The Python
- * layer chains these with q38moe_down (transposed weights) and q38moe_combine (unit weights) on the
- * permutation and tile table of the forward, built without shared-expert rows.
+ * layer chains these with q38moe_down_kn (the weights untransposed) and q38moe_combine (unit
+ * weights) on the permutation and tile table of the forward, built without shared-expert rows.
  *
  * Gathered grouped GEMM: C[r] = bf16(x[perm[r] / k] . w[e]^T) for the T*k sorted rows of the tile
  * table (e = the row's expert); w [E,N,K], x [T,K], C [T*k,N] bf16; K, N multiples of 64. Used to
@@ -332,6 +332,19 @@ int q38moe_block_forward_fp8(const void* x, const void* w_router, const void* wq
 int q38moe_gather_gemm(const void* x, const int32_t* perm, const void* w, const int32_t* tiles,
                        const int32_t* tile_count, void* C, int64_t T, int32_t K, int32_t N, int32_t E,
                        int32_t k, void* stream);
+
+/*
+ * Grouped product with K-major expert weights, for the input-gradient products of the padded
+ * path's bmm backward (inference.py:374-380), which multiply by the expert weights themselves:
+ *   Y[r, n] = bf16(sum_j A[r, j] * w_kn[e, j, n])   for the T*k sorted rows of the tile table
+ * (e = the row's expert; tables built without shared-expert rows). A [T*k,K], w_kn [E,K,N],
+ * Y [T*k,N] bf16; K, N multiples of 64. The same products, K order and rounding as q38moe_down
+ * on the per-expert transposes of w_kn (bit-identical results), without the transposes:
+ *   dH rows:       A = routed rows' gradient (K = h), w_kn = down_proj [E,h,I]     -> N = I
+ *   dx rows:       A = [d_g | d_u] (K = 2I),          w_kn = gate_up_proj [E,2I,h] -> N = h
+ */
+int q38moe_down_kn(const void* A, const void* w_kn, const int32_t* tiles, const int32_t* tile_count, void* Y,
+                   int64_t T, int32_t K, int32_t N, int32_t E, int32_t k, void* stream);
 
 /*
  * Routing-weight gradient (routed = raw * top_k_weights, inference.py:381):
@@ -358,6 +371,14 @@ int q38moe_gather_rows(const void* src, const int32_t* perm, const void* w, cons
                        void* stream);
 
 /*
+ * Per-expert transpose dst[e] = src[e]^T, bf16 [E,R,C] -> [E,C,R], R and C multiples of 64 (the
+ * transposes inside the padded path's bmm backward, inference.py:374-380): down_proj [E,h,I] ->
+ * [E,I,h], gate_up_proj [E,2I,h] -> [E,h,2I], the operands of q38moe_down for the input-gradient
+ * products (q38moe_down_kn takes the weights untransposed). src and dst must not overlap.
+ */
+int q38moe_transpose_experts(const void* src, void* dst, int32_t E, int32_t R, int32_t C, void* stream);
+
+/*
  * Expert weight gradients (the per-expert weight products of the padded path's bmm backward,
  * inference.py:374-380): dW[e][m][n] = bf16(sum over expert e's sorted rows r of G[r][m] * X[s(r)][n])
  * with the rows of e = [starts[e], starts[e] + counts[e]) and s(r) = perm[r] / k (X = the tokens
@@ -367,14 +388,6 @@ int q38moe_gather_rows(const void* src, const int32_t* perm, const void* w, cons
  *   gate_up_proj's gradient: G = [d_g | d_u] (M = 2I), X = x, perm given      -> [E, 2I, h]
  *   down_proj's gradient:    G = routed rows' gradient (M = h), X = H, no perm -> [E, h, I]
  */
-/*
- * Per-expert transpose dst[e] = src[e]^T, bf16 [E,R,C] -> [E,C,R], R and C multiples of 64: the
- * expert weights as the operand of the input-gradient products (the transposes inside the
- * padded path's bmm backward, inference.py:374-380): down_proj [E,h,I] -> [E,I,h] for dH,
- * gate_up_proj [E,2I,h] -> [E,h,2I] for the input rows' gradient. src and dst must not overlap.
- */
-int q38moe_transpose_experts(const void* src, void* dst, int32_t E, int32_t R, int32_t C, void* stream);
-
 int q38moe_expert_wgrad(const void* G, const void* X, const int32_t* perm, const int32_t* starts,
                         const int32_t* counts, void* dW, int64_t T, int32_t M, int32_t N, int32_t E,
                         int32_t k, void* stream);

@@ -605,6 +605,28 @@ int q38moe_gather_gemm(const void* x, const int32_t* perm, const void* w, const 
   return Q38MOE_OK;
 }
 
+int q38moe_down_kn(const void* A, const void* w_kn, const int32_t* tiles, const int32_t* tile_count, void* Y,
+                   int64_t T, int32_t K, int32_t N, int32_t E, int32_t k, void* stream) {
+  g_err[0] = 0;
+  Q38_CHECK(check_routing(T, E, k));
+  Q38_CHECK(check_dim(K, "K"));
+  Q38_CHECK(check_dim(N, "N"));
+  if (T == 0) return Q38MOE_OK;
+  Q38_CHECK(check_rows(T, K, k));
+  Q38_CHECK(check_rows(T, N, k));
+  Q38_CHECK(check_ptr(A, "A"));
+  Q38_CHECK(check_ptr(w_kn, "w_kn"));
+  Q38_CHECK(check_ptr(Y, "Y"));
+  Q38_CHECK(check_ptr(tiles, "tiles"));
+  if (tile_count == nullptr) return fail(Q38MOE_EINVAL, "tile_count must not be NULL");
+  (void)hipGetLastError();
+  Q38_HIP(q38::launch_down_kn(static_cast<const uint16_t*>(A), reinterpret_cast<const int4*>(tiles), tile_count,
+                              (int)max_tiles_impl(T, E, k, 0), static_cast<const uint16_t*>(w_kn),
+                              static_cast<uint16_t*>(Y), N, K, E, static_cast<hipStream_t>(stream)),
+          "down_kn launch");
+  return Q38MOE_OK;
+}
+
 int q38moe_pair_dots(const void* dout, const void* Y, const int32_t* inv, const void* topk_idx,
                      int32_t idx_is_int64, const void* topk_w, void* dw, void* d_raw, int64_t T, int32_t h,
                      int32_t E, int32_t k, void* stream) {

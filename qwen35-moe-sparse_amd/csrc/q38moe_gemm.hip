@@ -12,7 +12,9 @@
 // tokens; outputs are stored row-contiguous in that order (no scatter).
 //
 // Weights are [N, K] row-major (experts.gate_up_proj[e], experts.down_proj[e], nn.Linear), so
-// both MFMA operands are K-contiguous. A tile is 256 activation rows x 256 weight rows; K runs in
+// both MFMA operands are K-contiguous. One down instantiation (WKN) takes them K-major, [K, N]: the
+// experts backward multiplies by gate_up_proj[e] and down_proj[e] themselves (dx rows, dH), and
+// reads them as stored through the transposing LDS read instead of transposing them first. A tile is 256 activation rows x 256 weight rows; K runs in
 // 32-wide slices. One 512-thread workgroup per CU (8 waves, two per SIMD); wave w owns activation
 // rows 64*(w/2).. and weight rows 128*(w%2).., i.e. 2x4 blocks of mfma_f32_32x32x16_bf16 with the
 // weight fragment as the first operand, so lane = activation row and each lane holds runs of 4
@@ -79,6 +81,35 @@ struct GemmParams {
 
 __device__ __forceinline__ int swz(int r, int c) { return r * BK + ((c ^ ((r >> 2) & 3)) << 3); }
 
+// A weight fragment of mfma_f32_32x32x16_bf16 from a ring slot: output row n0 + lane % 32, the 8
+// K elements of 16-byte chunk kc + lane / 32 (kc = 0: the slice's first 16, 2: its second 16).
+// Row-major weight slots ([256 rows][32 K], swizzled as swz) are read directly. K-major slots (WKN:
+// [32 K rows][256 columns], 512 bytes per K row, 16-byte chunk c of K row r at c ^ 4 (r % 4)) are
+// read with the gfx950 transposing LDS read ds_read_b64_tr_b16: within each 16-lane group, component
+// j of lane i is element i % 4 of the 8 bytes that lane 4j + i / 4 addresses, so lane s addressing
+// K row k0 + s / 4, columns c0 + 4 (s % 4) .. + 3 receives K rows k0 .. k0 + 3 of column c0 + s;
+// two such reads (k0 and k0 + 4) are the fragment. A half-wave's reads cover 4 K rows x 64 bytes,
+// which the swizzle spreads over all 64 banks.
+typedef short q38_i16x4_t __attribute__((ext_vector_type(4)));
+template <bool WKN>
+__device__ __forceinline__ u32x4_t w_frag(const uint16_t* slot, int n0, int kc, int lane) {
+  if constexpr (!WKN) {
+    return ld16(slot + swz(n0 + (lane & 31), kc + (lane >> 5)));
+  } else {
+    const int s = lane & 15;
+    const int col = n0 + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
+    const int k0 = 8 * (kc + (lane >> 5)) + (s >> 2);
+    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)slot;
+    auto off = [&](int kr) { return kr * 512 + 16 * ((col >> 3) ^ (4 * (kr & 3))) + 2 * (col & 7); };
+    const q38_i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) q38_i16x4_t*)(uintptr_t)(base + off(k0)));
+    const q38_i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) q38_i16x4_t*)(uintptr_t)(base + off(k0 + 4)));
+    const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
+    return u32x4_t{a.x, a.y, b.x, b.y};
+  }
+}
+
 // Tile-table entry as scalar loads (x2 + x1: there is no 3-dword scalar load, and a 3-dword vector
 // load would join the copy queue).
 __device__ __forceinline__ int4 tile_entry(const GemmParams& p, int mt) {
@@ -121,7 +152,12 @@ __device__ __forceinline__ void gather_rows(const GemmParams& p, int4 ti, int wa
 // Global source of each of this lane's copies for tile `ti`, output-column tile `nt`. Copy q of
 // wave w fills slice rows 64w + 16q + lane/4 (rows < 256: activations, else weights); lane l
 // lands in 16-byte slot l % 4 of its row, which holds chunk (l % 4) ^ ((row >> 2) & 3).
-template <int MODE>
+// WKN (down only): the weights are [E, K, N] (each expert's matrix stored K-major, as the
+// experts' backward multiplies by gate_up_proj and down_proj themselves). A weight slot then holds
+// the slice's 32 K rows of the tile's 256 output columns, 512 bytes per K row: copy q of weight
+// wave w fills K row 8 (w - 4) + 2q + lane/32, 16-byte slot lane % 32, which holds column chunk
+// (lane % 32) ^ 4 (K row % 4). The slice's K offset is then a multiple of N (see Q38_ISSUE).
+template <int MODE, bool WKN = false>
 __device__ __forceinline__ void copy_sources(const GemmParams& p, int4 ti, int nt, int wave,
                                              int lane, const int (&rows)[NCOPY],
                                              const uint16_t* (&src)[NCOPY]) {
@@ -131,7 +167,12 @@ __device__ __forceinline__ void copy_sources(const GemmParams& p, int4 ti, int n
   for (int q = 0; q < NCOPY; ++q) {
     const int r = 64 * wave + 16 * q + (lane >> 2);
     const int c = (lane & 3) ^ ((r >> 2) & 3);
-    if (wave < 4) {
+    if (WKN && wave >= 4) {
+      const int kr = 8 * (wave - 4) + 2 * q + (lane >> 5);
+      const int col = nt * BW + 8 * ((lane & 31) ^ (4 * (kr & 3)));
+      // Tile tables of this form hold experts only; another group reads expert 0 (in bounds).
+      src[q] = p.W + (int64_t)(ti.x < p.E ? ti.x : 0) * K * N + (int64_t)kr * N + (col < N ? col : 0);
+    } else if (wave < 4) {
       int64_t arow = rows[q];
       if (MODE != MODE_DOWN) arow = shared_grp ? (int64_t)(rows[q] - p.P) : (int64_t)(rows[q] / p.topk);
       src[q] = p.A + arow * K + c * 8;
@@ -228,8 +269,9 @@ __device__ __forceinline__ void wait_vmcnt_barrier(int n) {
 #undef Q38_W
 }
 
-template <int MODE, bool ASYNC_ROWS, bool FP8>
+template <int MODE, bool ASYNC_ROWS, bool FP8, bool WKN = false>
 __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p) {
+  static_assert(!WKN || (MODE == MODE_DOWN && !FP8), "K-major weights: bf16 down only");
   // 16-byte stores per wave and tile: 2 per 32x32 output block, 2 x 2 (gate/up) or 2 x 4 blocks.
   constexpr int EPI_STORES = MODE == MODE_GATE_UP ? 8 : 16;
   constexpr int NT_OUT = MODE == MODE_GATE_UP ? 2 : 4;  // 32-column output blocks per wave
@@ -310,7 +352,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
   // Retire these loads on every path (waves >= 4 never read them); a load left pending in the
   // compiler's bookkeeping makes it wait for all copies wherever its register is reused.
   wait_vmcnt0();
-  copy_sources<MODE>(p, ti, L % p.ntiles_n, wave, lane, rows, src);
+  copy_sources<MODE, WKN>(p, ti, L % p.ntiles_n, wave, lane, rows, src);
 #pragma unroll
   for (int q = 0; q < NCOPY; ++q) {
     rows_n[q] = 0;
@@ -319,12 +361,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
 
   // This wave's 64 rows of a slot: activation rows 64w.. of ring_a, weight rows 64(w-4).. of ring_w.
   const uint32_t my_ring = is_a ? lds_addr(ring_a) + 2 * 64 * wave * BK : lds_addr(ring_w) + 2 * 64 * (wave - 4) * BK;
+  // Elements between consecutive K positions of this wave's copy sources: 1, or N for the K-major
+  // weights of WKN (their slice offset moves down K rows).
+  const int kstride = WKN && !is_a ? p.N : 1;
 #define Q38_ISSUE(SLOT, SRC, KS, ROT)                                                    \
   do {                                                                                   \
     const uint32_t st_ = my_ring + (uint32_t)(SLOT) * (2 * SLOT_ELEMS);                  \
     const int ko_ = ((KS) + (ROT) < nk ? (KS) + (ROT) : (KS) + (ROT) - nk) * BK;         \
     _Pragma("unroll") for (int q_ = 0; q_ < NCOPY; ++q_)                                 \
-      dma16((SRC)[q_] + ko_, st_ + q_ * (2 * 16 * BK));                                  \
+      dma16((SRC)[q_] + (int64_t)ko_ * kstride, st_ + q_ * (2 * 16 * BK));               \
   } while (0)
 
   uint16_t* const sink = reinterpret_cast<uint16_t*>(q38moe_gemm_store_sink + 64 * wave + lane);
@@ -389,7 +434,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
     } else {                                                                               \
       gather_rows<MODE>(p, tin, wave, lane, rows_n);                                       \
     }                                                                                      \
-    copy_sources<MODE>(p, tin, Ln % p.ntiles_n, wave, lane, rows_n, src_n);                \
+    copy_sources<MODE, WKN>(p, tin, Ln % p.ntiles_n, wave, lane, rows_n, src_n);           \
   } while (0)
 #define Q38_COMPUTE()                                                                      \
   do {                                                                                     \
@@ -419,7 +464,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
       const uint16_t* bs_ = ring_w + rw * SLOT_ELEMS;                                      \
       u32x4_t wx[4], ax[2];                                                                \
       _Pragma("unroll") for (int t = 0; t < 4; ++t)                                        \
-        wx[t] = ld16(bs_ + swz(128 * wn + 32 * t + lr, lh));                               \
+        wx[t] = w_frag<WKN>(bs_, 128 * wn + 32 * t, 0, lane);                              \
       _Pragma("unroll") for (int mi = 0; mi < 2; ++mi)                                     \
         ax[mi] = ld16(as_ + swz(64 * wm + 32 * mi + lr, lh));                              \
       /* keeps these reads ahead of the MFMAs below (not sunk past the branch) */          \
@@ -430,7 +475,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
             acc[t][mi] = mfma32x32x16(wy[t], ay[mi], acc[t][mi]);                          \
       }                                                                                    \
       _Pragma("unroll") for (int t = 0; t < 4; ++t)                                        \
-        wy[t] = ld16(bs_ + swz(128 * wn + 32 * t + lr, 2 + lh));                           \
+        wy[t] = w_frag<WKN>(bs_, 128 * wn + 32 * t, 2, lane);                              \
       _Pragma("unroll") for (int mi = 0; mi < 2; ++mi)                                     \
         ay[mi] = ld16(as_ + swz(64 * wm + 32 * mi + lr, 2 + lh));                          \
       _Pragma("unroll") for (int t = 0; t < 4; ++t)                                        \
@@ -668,6 +713,25 @@ static hipError_t down_impl(const void* H, const int4* tiles, const int32_t* nti
     hipLaunchKernelGGL((grouped_gemm_kernel<MODE_DOWN, false, true>), grid, dim3(NTHREADS), 0, stream, p);
   else
     hipLaunchKernelGGL((grouped_gemm_kernel<MODE_DOWN, false, false>), grid, dim3(NTHREADS), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_down_kn(const uint16_t* A, const int4* tiles, const int32_t* ntiles_dev, int max_mtiles,
+                          const uint16_t* w_kn, uint16_t* Y, int N, int K, int E, hipStream_t stream) {
+  GemmParams p = {};
+  p.A = A;
+  p.tiles = tiles;
+  p.ntiles_dev = ntiles_dev;
+  p.W = w_kn;
+  p.C = Y;
+  p.N = N;
+  p.K = K;
+  p.E = E;
+  p.topk = 1;
+  p.ntiles_n = (N + BW - 1) / BW;
+  if (max_mtiles == 0) return hipSuccess;
+  const dim3 grid(grid_for(max_mtiles, p.ntiles_n));
+  hipLaunchKernelGGL((grouped_gemm_kernel<MODE_DOWN, false, false, true>), grid, dim3(NTHREADS), 0, stream, p);
   return hipGetLastError();
 }
 

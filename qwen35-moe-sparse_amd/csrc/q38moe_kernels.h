@@ -54,6 +54,11 @@ hipError_t launch_down(const uint16_t* H, const int4* tiles, const int32_t* ntil
                        const uint16_t* ws_down, uint16_t* Y, int N, int K, int E,
                        hipStream_t stream);
 
+// Grouped down-form product with K-major weights: Y[r, n] = bf16(sum_k A[r, k] w_kn[e, k, n]) for
+// the rows of each expert tile (tables without shared-expert rows), w_kn [E, K, N] bf16.
+hipError_t launch_down_kn(const uint16_t* A, const int4* tiles, const int32_t* ntiles_dev, int max_mtiles,
+                          const uint16_t* w_kn, uint16_t* Y, int N, int K, int E, hipStream_t stream);
+
 // The same two GEMMs (tile tables only, bf16) decomposed for few rows per expert: 16 weight rows x
 // up to 64 activation rows per workgroup, K split over its waves (q38moe_gemm_small.hip), for K in
 // {128, 256, 512, 1024, 2048} (small_gemm_supported); P = T * k routed rows, shared_rows after them.

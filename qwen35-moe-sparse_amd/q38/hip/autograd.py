@@ -9,9 +9,9 @@ the backward runs, with Y' = dout[t] * w[p] (the routed raw rows' gradient) in s
 
   dw[p]   = <dout[t], Y[p]>                       q38moe_pair_dots (which also writes Y')
   [g | u] = x[t] . gate_up_proj[e]^T              q38moe_gather_gemm (recomputed, sorted rows)
-  dH      = Y' . down_proj[e]                     q38moe_down on down_proj^T [E, I, h] (q38moe_transpose_experts)
+  dH      = Y' . down_proj[e]                     q38moe_down_kn on down_proj [E, h, I] as stored
   dGU     = SwiGLU backward (dH, g, u)            q38moe_swiglu_backward
-  dx_p    = dGU . gate_up_proj[e]                 q38moe_down on gate_up_proj^T [E, h, 2I]
+  dx_p    = dGU . gate_up_proj[e]                 q38moe_down_kn on gate_up_proj [E, 2I, h] as stored
   dx[t]   = sum_j dx_p[inv[t*k+j]]                q38moe_combine with unit weights
   d down_proj[e]    = Y'_e^T . H_e                q38moe_expert_wgrad (sorted rows)
   d gate_up_proj[e] = dGU_e^T . x_e               q38moe_expert_wgrad (x rows gathered through perm)
@@ -65,13 +65,13 @@ class HipExperts(torch.autograd.Function):
             if need_dn:
                 ddn_w = ops.expert_wgrad(d_raw, H, starts, counts, k)
             if need_x or need_gu:
-                dH = ops.down(d_raw, ops.transpose_experts(w_down), tiles, tcount, T, k)
+                dH = ops.down_kn(d_raw, w_down, tiles, tcount, T, k)
                 GU = ops.gather_gemm(x, perm, w_gate_up, tiles, tcount, k)
                 dGU = ops.swiglu_backward(dH, GU)
                 if need_gu:
                     dgu_w = ops.expert_wgrad(dGU, x, starts, counts, k, perm=perm)
                 if need_x:
-                    dxp = ops.down(dGU, ops.transpose_experts(w_gate_up), tiles, tcount, T, k)
+                    dxp = ops.down_kn(dGU, w_gate_up, tiles, tcount, T, k)
                     dx = ops.combine(dxp, inv, torch.ones_like(w), E, idx=idx)
         return dx, None, dw, dgu_w, ddn_w
 

@@ -298,6 +298,25 @@ def gather_rows(src, perm, starts, counts, k, w=None):
     return dst
 
 
+def down_kn(A, w_kn, tiles, tile_count, T, k):
+    """Grouped product with K-major expert weights (q38moe_down_kn): Y[r] = bf16(A[r] . w_kn[e]) for
+    the T*k sorted rows, w_kn [E, K, N] as stored (down_proj for dH, gate_up_proj for the input rows'
+    gradient). Bit-identical to ``down(A, transpose_experts(w_kn), ...)`` without the transpose.
+    A [T*k, K] bf16; returns Y [T*k, N] bf16. The tile table must hold no shared-expert rows."""
+    _need(A, "A", dtype=torch.bfloat16, ndim=2)
+    _need(w_kn, "w_kn", dtype=torch.bfloat16, ndim=3)
+    _need(tiles, "tiles", dtype=torch.int32, ndim=2)
+    E, K, N = w_kn.shape
+    if A.shape != (T * k, K):
+        raise ValueError(f"A {tuple(A.shape)} does not match ({T * k}, {K})")
+    if tiles.shape[0] != max_tiles(T, E, k, 0):
+        raise ValueError("tiles was not built for this shape (without shared-expert rows)")
+    Y = torch.empty(T * k, N, dtype=torch.bfloat16, device=A.device)
+    check(lib.q38moe_down_kn(_ptr(A), _ptr(w_kn), _ptr(tiles), _ptr(tile_count), _ptr(Y), T, K, N, E, k,
+                             _stream(A.device)), "q38moe_down_kn")
+    return Y
+
+
 def transpose_experts(w):
     """w [E, R, C] bf16 -> contiguous [E, C, R] (each expert's matrix transposed)."""
     _need(w, "w", ndim=3)

@@ -206,6 +206,45 @@ def test_transpose_experts(gpu, E, R, C):
     assert out.shape == (E, C, R) and torch.equal(out.cpu(), w.transpose(1, 2).contiguous())
 
 
+@pytest.mark.parametrize("E,k,T,K,N,drop", [(64, 5, 2048, 1024, 256, 0), (64, 5, 2048, 512, 1024, 37),
+                                             (3, 2, 700, 320, 192, 5), (17, 8, 300, 64, 448, 0),
+                                             (1, 1, 999, 128, 64, 0)])
+def test_down_kn(gpu, E, k, T, K, N, drop):
+    """q38moe_down_kn (weights [E, K, N] as stored, read with the transposing LDS read) against
+    q38moe_down on the per-expert transposes: bit-identical (same products, K order and rounding;
+    T*k > 32 E, so q38moe_down runs the persistent kernel too). And against exact per-expert
+    products: each value within one bf16 rounding plus 2^-20 of the sum of |a*w| (fp32
+    accumulation). Shapes: configuration 2's dH (K = h, N = I) and input-row (K = 2I, N = h)
+    products, N not a multiple of 256, K of one or two slices, a single expert, dropped pairs."""
+    from q38.hip import ops
+    g = torch.Generator().manual_seed(K * 7 + N)
+    idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(torch.int32)
+    if drop:
+        idx.view(-1)[torch.randperm(T * k, generator=g)[:drop]] = E
+    A = (torch.randn(T * k, K, generator=g) * 0.5).to(torch.bfloat16)
+    W = (torch.randn(E, K, N, generator=g) * 0.05).to(torch.bfloat16)
+    di = idx.to(gpu)
+    hist = ops.histogram(di, E)
+    counts, starts, perm, inv, tiles, tc = ops.permute(di, hist, E)
+    dA, dW = A.to(gpu), W.to(gpu)
+    Y = ops.down_kn(dA, dW, tiles, tc, T, k)
+    Yt = ops.down(dA, ops.transpose_experts(dW), tiles, tc, T, k)
+    torch.cuda.synchronize()
+    rows = int(counts.sum())
+    assert torch.equal(Y[:rows].cpu(), Yt[:rows].cpu())
+    st, ct = starts.cpu().tolist(), counts.cpu().tolist()
+    Yc = Y.cpu().double()
+    for e in range(E):
+        if ct[e] == 0:
+            continue
+        a = A[st[e]:st[e] + ct[e]].double()
+        exact = a @ W[e].double()
+        mag = a.abs() @ W[e].double().abs()
+        ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp_min(1e-38))) - 7)
+        err = (Yc[st[e]:st[e] + ct[e]] - exact).abs()
+        assert bool((err <= ulp + mag * 2.0 ** -20).all()), f"expert {e}: worst {float((err - ulp - mag * 2.0 ** -20).max()):.3e}"
+
+
 @pytest.mark.parametrize("name,T,drop", [("c2", 2048, 0), ("c1", 700, 40)])
 def test_pair_dots_rows_fused(gpu, name, T, drop):
     """pair_dots with top_k_weights writes the same routed-row gradient as gather_rows and the same
