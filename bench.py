@@ -421,11 +421,10 @@ def backward_bench(args):
         xb, wb, wgu, wdn = (t.detach() for t in leaves)
         hist = ops.histogram(idx, E)
         counts, starts, perm, inv, tiles, tcount = ops.permute(idx, hist, E)
-        H = ops.gate_up(xb, wgu, perm, tiles, tcount, k)
+        H, GU = ops.gate_up_save(xb, wgu, perm, tiles, tcount, k)
         Y = ops.down(H, wdn, tiles, tcount, T, k)
         d_raw = ops.gather_rows(dout, perm, starts, counts, k, w=wb)
         dH = ops.down_kn(d_raw, wdn, tiles, tcount, T, k)
-        GU = ops.gather_gemm(xb, perm, wgu, tiles, tcount, k)
         dGU = ops.swiglu_backward(dH, GU)
         dxp = ops.down_kn(dGU, wgu, tiles, tcount, T, k)
         ones = torch.ones_like(wb)
@@ -436,7 +435,8 @@ def backward_bench(args):
         stages = {
             "pair_dots_rows": (lambda: ops.pair_dots(dout, Y, inv, idx, E, w=wb), by(2 * (T * h + 2 * P * h) + 4 * P)),
             "dH_down_kn": (lambda: ops.down_kn(d_raw, wdn, tiles, tcount, T, k), fl(2 * P * h * I)),
-            "gate_up_recompute": (lambda: ops.gather_gemm(xb, perm, wgu, tiles, tcount, k), fl(2 * P * h * 2 * I)),
+            "fwd_gate_up_save": (lambda: ops.gate_up_save(xb, wgu, perm, tiles, tcount, k), fl(2 * P * h * 2 * I)),
+            "fwd_gate_up": (lambda: ops.gate_up(xb, wgu, perm, tiles, tcount, k), fl(2 * P * h * 2 * I)),
             "swiglu_backward": (lambda: ops.swiglu_backward(dH, GU), by(2 * (P * I + 2 * P * 2 * I))),
             "dx_down_kn": (lambda: ops.down_kn(dGU, wgu, tiles, tcount, T, k), fl(2 * P * 2 * I * h)),
             "dx_combine": (lambda: ops.combine(dxp, inv, ones, E, idx=idx), by(2 * (P * h + T * h))),
@@ -454,7 +454,9 @@ def backward_bench(args):
                              "peak": meta["peak"], "unit": meta["unit"], "frac": round(ach / meta["peak"], 4),
                              "work": meta["work"]}
     log("[bench] backward kernels: " + ", ".join(f"{n} {v['us']}us" for n, v in kernels.items()))
-    flops = 22 * P * h * I  # forward 6 P h I (gate/up 4, down 2) + backward 16 P h I
+    # Algorithmic FLOPs: forward 6 P h I (gate/up 4, down 2) + backward 12 P h I (dH 2, dx rows 4,
+    # gate_up_proj gradient 4, down_proj gradient 2); the forward keeps [g | u], nothing is recomputed.
+    flops = 18 * P * h * I
     res = {
         "metric": "routed-experts forward+backward tokens/sec (1 GPU)",
         "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,

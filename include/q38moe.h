@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define Q38MOE_ABI_VERSION 11
+#define Q38MOE_ABI_VERSION 12
 
 #define Q38MOE_OK 0
 #define Q38MOE_EINVAL (-1)   /* bad shape, null pointer, misalignment, unsupported dtype */
@@ -332,6 +332,18 @@ int q38moe_block_forward_fp8(const void* x, const void* w_router, const void* wq
 int q38moe_gather_gemm(const void* x, const int32_t* perm, const void* w, const int32_t* tiles,
                        const int32_t* tile_count, void* C, int64_t T, int32_t K, int32_t N, int32_t E,
                        int32_t k, void* stream);
+
+/*
+ * Training forward of the routed experts' gate/up (the padded path's bmm gate/up and SiLU * up,
+ * inference.py:370-378, whose inputs its backward needs): q38moe_gate_up on routed rows only (tile
+ * table without shared-expert rows), which also writes the rounded pre-activations
+ *   GU[r] = [bf16(x_r . w_gate_up[e, :I]) | bf16(x_r . w_gate_up[e, I:])]   [T*k, 2I] bf16
+ * next to H [T*k, I]. They are the values H is computed from, bit-identical to q38moe_gather_gemm
+ * on the same tiles, so the backward's SwiGLU step reads them instead of recomputing them.
+ */
+int q38moe_gate_up_save(const void* x, const void* w_gate_up, const int32_t* perm, const int32_t* tiles,
+                        const int32_t* tile_count, void* H, void* GU, int64_t T, int32_t h, int32_t E, int32_t k,
+                        int32_t I, void* stream);
 
 /*
  * Grouped product with K-major expert weights, for the input-gradient products of the padded

@@ -605,6 +605,31 @@ int q38moe_gather_gemm(const void* x, const int32_t* perm, const void* w, const 
   return Q38MOE_OK;
 }
 
+int q38moe_gate_up_save(const void* x, const void* w_gate_up, const int32_t* perm, const int32_t* tiles,
+                        const int32_t* tile_count, void* H, void* GU, int64_t T, int32_t h, int32_t E, int32_t k,
+                        int32_t I, void* stream) {
+  g_err[0] = 0;
+  Q38_CHECK(check_routing(T, E, k));
+  Q38_CHECK(check_dim(h, "h"));
+  Q38_CHECK(check_dim(I, "I"));
+  if (T == 0) return Q38MOE_OK;
+  Q38_CHECK(check_rows(T, h, k));
+  Q38_CHECK(check_rows(T, 2 * I, k));
+  Q38_CHECK(check_ptr(x, "x"));
+  Q38_CHECK(check_ptr(w_gate_up, "w_gate_up"));
+  Q38_CHECK(check_ptr(H, "H"));
+  Q38_CHECK(check_ptr(GU, "GU"));
+  Q38_CHECK(check_ptr(tiles, "tiles"));
+  if (perm == nullptr || tile_count == nullptr) return fail(Q38MOE_EINVAL, "perm and tile_count must not be NULL");
+  (void)hipGetLastError();
+  Q38_HIP(q38::launch_gate_up_save(static_cast<const uint16_t*>(x), perm, reinterpret_cast<const int4*>(tiles),
+                                   tile_count, (int)max_tiles_impl(T, E, k, 0), (int)(T * k),
+                                   static_cast<const uint16_t*>(w_gate_up), static_cast<uint16_t*>(H),
+                                   static_cast<uint16_t*>(GU), I, h, E, k, static_cast<hipStream_t>(stream)),
+          "gate_up_save launch");
+  return Q38MOE_OK;
+}
+
 int q38moe_down_kn(const void* A, const void* w_kn, const int32_t* tiles, const int32_t* tile_count, void* Y,
                    int64_t T, int32_t K, int32_t N, int32_t E, int32_t k, void* stream) {
   g_err[0] = 0;

@@ -68,6 +68,7 @@ struct GemmParams {
   const uint16_t* Ws_a;       // shared expert: gate [N, K] (gate/up) or down [N, K]
   const uint16_t* Ws_b;       // shared expert: up [N, K] (gate/up)
   uint16_t* C;                // output rows [*, N]
+  uint16_t* GU;               // gate/up with SAVE_GU: the bf16 pre-activations [g | u], rows [*, 2N]
   int P;                      // first shared-expert row of the row space
   int N, K, E, topk;
   int ntiles_n;               // output-column tiles per row tile
@@ -269,11 +270,16 @@ __device__ __forceinline__ void wait_vmcnt_barrier(int n) {
 #undef Q38_W
 }
 
-template <int MODE, bool ASYNC_ROWS, bool FP8, bool WKN = false>
+// SAVE_GU (bf16 gate/up only): the epilogue also stores the rounded pre-activations bf16(g) and
+// bf16(u) of every row to GU [rows, 2N] ([g | u], the operand of the SwiGLU backward), the values it
+// computes H from, so a training forward keeps them instead of recomputing them in the backward.
+template <int MODE, bool ASYNC_ROWS, bool FP8, bool WKN = false, bool SAVE_GU = false>
 __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p) {
   static_assert(!WKN || (MODE == MODE_DOWN && !FP8), "K-major weights: bf16 down only");
-  // 16-byte stores per wave and tile: 2 per 32x32 output block, 2 x 2 (gate/up) or 2 x 4 blocks.
-  constexpr int EPI_STORES = MODE == MODE_GATE_UP ? 8 : 16;
+  static_assert(!SAVE_GU || (MODE == MODE_GATE_UP && !FP8), "saved pre-activations: bf16 gate/up only");
+  // 16-byte stores per wave and tile: 2 per 32x32 output block, 2 x 2 (gate/up, and as many again
+  // for each of g and u with SAVE_GU) or 2 x 4 blocks.
+  constexpr int EPI_STORES = MODE == MODE_GATE_UP ? (SAVE_GU ? 24 : 8) : 16;
   constexpr int NT_OUT = MODE == MODE_GATE_UP ? 2 : 4;  // 32-column output blocks per wave
   __shared__ __attribute__((aligned(16))) uint16_t ring_a[NA * SLOT_ELEMS];
   __shared__ __attribute__((aligned(16))) uint16_t ring_w[NW * SLOT_ELEMS];
@@ -602,6 +608,36 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
             if (MODE == MODE_DOWN) st16_stream(r < ti.z && col < p.N ? dst : sink, d);
             else st16(r < ti.z && col < p.N ? dst : sink, d);
           }
+          if constexpr (SAVE_GU) {
+            // The same 32 rows x 64 columns of g (half 0) and of u (half 1), staged and stored
+            // like H (the staging area's earlier reads precede these writes: one wave's LDS
+            // operations complete in order).
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+#pragma unroll
+              for (int tt = 0; tt < 2; ++tt) {
+                const int to = 2 * tp + tt + 2 * half;
+#pragma unroll
+                for (int gq = 0; gq < 4; ++gq) {
+                  const int i = 4 * gq;
+                  const uint32_t v0 = pack_bf16x2(acc[to][mi][i], acc[to][mi][i + 1]);
+                  const uint32_t v1 = pack_bf16x2(acc[to][mi][i + 2], acc[to][mi][i + 3]);
+                  const int ch = 4 * tt + gq;
+                  *reinterpret_cast<uint2*>(stage + lr * 128 + ((ch ^ ((lr >> 1) & 7)) << 4) + 8 * lh) =
+                      make_uint2(v0, v1);
+                }
+              }
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const int row = 8 * j + (lane >> 3), ch = lane & 7;
+                const u32x4_t d = *reinterpret_cast<const u32x4_t*>(stage + row * 128 + ((ch ^ ((row >> 1) & 7)) << 4));
+                const int r = 64 * wm + 32 * mi + row;
+                const int col = col_wave + 64 * tp + 8 * ch;
+                uint16_t* dst = p.GU + (int64_t)(ti.y + r) * 2 * p.N + half * p.N + col;
+                st16(r < ti.z && col < p.N ? dst : sink, d);
+              }
+            }
+          }
         }
       }
     }
@@ -644,9 +680,10 @@ static hipError_t gate_up_impl(const void* x, const int32_t* perm, const int4* t
                                const void* w_gate_up, const void* ws_gate, const void* ws_up,
                                uint16_t* H, int N, int K, int E, int topk, bool fp8,
                                const float* a_scale, const float* w_scale, const float* ws_scale_gate,
-                               const float* ws_scale_up, hipStream_t stream) {
+                               const float* ws_scale_up, hipStream_t stream, uint16_t* GU = nullptr) {
   GemmParams p;
   p.A = static_cast<const uint16_t*>(x);
+  p.GU = GU;
   p.perm = perm;
   p.tiles = tiles;
   p.ntiles_dev = ntiles_dev;
@@ -674,6 +711,10 @@ static hipError_t gate_up_impl(const void* x, const int32_t* perm, const int4* t
     hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, true, true>), grid, dim3(NTHREADS), 0, stream, p);
   else if (fp8)
     hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, false, true>), grid, dim3(NTHREADS), 0, stream, p);
+  else if (GU != nullptr && async_rows)
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, true, false, false, true>), grid, dim3(NTHREADS), 0, stream, p);
+  else if (GU != nullptr)
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, false, false, false, true>), grid, dim3(NTHREADS), 0, stream, p);
   else if (async_rows)
     hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATE_UP, true, false>), grid, dim3(NTHREADS), 0, stream, p);
   else
@@ -687,6 +728,7 @@ static hipError_t down_impl(const void* H, const int4* tiles, const int32_t* nti
                             const float* w_scale, const float* ws_scale, hipStream_t stream) {
   GemmParams p;
   p.A = static_cast<const uint16_t*>(H);
+  p.GU = nullptr;
   p.perm = nullptr;
   p.tiles = tiles;
   p.ntiles_dev = ntiles_dev;
@@ -714,6 +756,13 @@ static hipError_t down_impl(const void* H, const int4* tiles, const int32_t* nti
   else
     hipLaunchKernelGGL((grouped_gemm_kernel<MODE_DOWN, false, false>), grid, dim3(NTHREADS), 0, stream, p);
   return hipGetLastError();
+}
+
+hipError_t launch_gate_up_save(const uint16_t* x, const int32_t* perm, const int4* tiles, const int32_t* ntiles_dev,
+                               int max_mtiles, int P, const uint16_t* w_gate_up, uint16_t* H, uint16_t* GU, int N,
+                               int K, int E, int topk, hipStream_t stream) {
+  return gate_up_impl(x, perm, tiles, ntiles_dev, max_mtiles, 0, P, w_gate_up, nullptr, nullptr, H, N, K, E, topk,
+                      false, nullptr, nullptr, nullptr, nullptr, stream, GU);
 }
 
 hipError_t launch_down_kn(const uint16_t* A, const int4* tiles, const int32_t* ntiles_dev, int max_mtiles,

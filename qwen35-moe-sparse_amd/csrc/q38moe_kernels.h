@@ -54,6 +54,12 @@ hipError_t launch_down(const uint16_t* H, const int4* tiles, const int32_t* ntil
                        const uint16_t* ws_down, uint16_t* Y, int N, int K, int E,
                        hipStream_t stream);
 
+// Grouped gate/up + SwiGLU over routed tiles (no shared-expert rows) that also stores the bf16
+// pre-activations GU [rows, 2N] = [bf16(g) | bf16(u)] next to H [rows, N].
+hipError_t launch_gate_up_save(const uint16_t* x, const int32_t* perm, const int4* tiles, const int32_t* ntiles_dev,
+                               int max_mtiles, int P, const uint16_t* w_gate_up, uint16_t* H, uint16_t* GU, int N,
+                               int K, int E, int topk, hipStream_t stream);
+
 // Grouped down-form product with K-major weights: Y[r, n] = bf16(sum_k A[r, k] w_kn[e, k, n]) for
 // the rows of each expert tile (tables without shared-expert rows), w_kn [E, K, N] bf16.
 hipError_t launch_down_kn(const uint16_t* A, const int4* tiles, const int32_t* ntiles_dev, int max_mtiles,

@@ -12,7 +12,7 @@ import torch  # noqa: F401  (loads the HIP runtime first)
 
 LIB_PATH = Path(os.environ.get("Q38MOE_LIB", Path(__file__).resolve().parent / "libq38moe.so"))
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 BF16 = 1
 FP32 = 2
 TILING_PERSISTENT = 1
@@ -60,6 +60,8 @@ SIGNATURES = {
     "q38moe_block_forward_fp8": (_c_int, [_vp] * 18 + [_c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _vp, _c_size, _vp]),
     "q38moe_gather_gemm": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _vp]),
     "q38moe_down_kn": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _vp]),
+    "q38moe_gate_up_save": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,
+                                     _vp]),
     "q38moe_pair_dots": (_c_int, [_vp] * 4 + [_c_i32, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _c_i32, _vp]),
     "q38moe_gather_rows": (_c_int, [_vp] * 6 + [_c_i64, _c_i32, _c_i32, _c_i32, _vp]),
     "q38moe_transpose_experts": (_c_int, [_vp, _vp, _c_i32, _c_i32, _c_i32, _vp]),

@@ -4,11 +4,12 @@ The reference's differentiable experts path is ``padded_batched_experts_forward`
 (q38/inference.py:358-384: gather, bmm gate/up, SiLU * up, bmm down, * top_k_weights, scatter-sum);
 its gradients of x, top_k_weights, gate_up_proj and down_proj are what
 scripts/check_q38_kernels.py:19-27 compares. Here the forward is the inference pipeline (histogram,
-permutation, grouped gate/up + SwiGLU, grouped down, combine) keeping the sorted H and Y rows, and
-the backward runs, with Y' = dout[t] * w[p] (the routed raw rows' gradient) in sorted order:
+permutation, grouped gate/up + SwiGLU, grouped down, combine) keeping the sorted H and Y rows and
+the rounded gate/up pre-activations [g | u] (q38moe_gate_up_save writes them next to H; 2I bf16
+per row), and the backward runs, with Y' = dout[t] * w[p] (the routed raw rows' gradient) in sorted
+order:
 
   dw[p]   = <dout[t], Y[p]>                       q38moe_pair_dots (which also writes Y')
-  [g | u] = x[t] . gate_up_proj[e]^T              q38moe_gather_gemm (recomputed, sorted rows)
   dH      = Y' . down_proj[e]                     q38moe_down_kn on down_proj [E, h, I] as stored
   dGU     = SwiGLU backward (dH, g, u)            q38moe_swiglu_backward
   dx_p    = dGU . gate_up_proj[e]                 q38moe_down_kn on gate_up_proj [E, 2I, h] as stored
@@ -38,15 +39,16 @@ class HipExperts(torch.autograd.Function):
         E = w_gate_up.shape[0]
         hist = ops.histogram(topk_idx, E)
         counts, starts, perm, inv, tiles, tcount = ops.permute(topk_idx, hist, E)
-        H = ops.gate_up(x, w_gate_up, perm, tiles, tcount, k)
+        H, GU = ops.gate_up_save(x, w_gate_up, perm, tiles, tcount, k)
         Y = ops.down(H, w_down, tiles, tcount, T, k)
         out = ops.combine(Y, inv, topk_w, E, idx=topk_idx)
-        ctx.save_for_backward(x, topk_idx, topk_w, w_gate_up, w_down, counts, starts, perm, inv, tiles, tcount, H, Y)
+        ctx.save_for_backward(x, topk_idx, topk_w, w_gate_up, w_down, counts, starts, perm, inv, tiles, tcount, H, Y,
+                              GU)
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        x, idx, w, w_gate_up, w_down, counts, starts, perm, inv, tiles, tcount, H, Y = ctx.saved_tensors
+        x, idx, w, w_gate_up, w_down, counts, starts, perm, inv, tiles, tcount, H, Y, GU = ctx.saved_tensors
         T, h = x.shape
         k = idx.shape[1]
         E, twoI, _ = w_gate_up.shape
@@ -66,7 +68,6 @@ class HipExperts(torch.autograd.Function):
                 ddn_w = ops.expert_wgrad(d_raw, H, starts, counts, k)
             if need_x or need_gu:
                 dH = ops.down_kn(d_raw, w_down, tiles, tcount, T, k)
-                GU = ops.gather_gemm(x, perm, w_gate_up, tiles, tcount, k)
                 dGU = ops.swiglu_backward(dH, GU)
                 if need_gu:
                     dgu_w = ops.expert_wgrad(dGU, x, starts, counts, k, perm=perm)

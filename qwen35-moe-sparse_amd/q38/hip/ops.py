@@ -298,6 +298,28 @@ def gather_rows(src, perm, starts, counts, k, w=None):
     return dst
 
 
+def gate_up_save(x, w_gate_up, perm, tiles, tile_count, k):
+    """Grouped gate/up + SwiGLU on routed rows that also returns the rounded pre-activations
+    (q38moe_gate_up_save): (H [T*k, I], GU [T*k, 2I] = [g | u]) bf16, GU bit-identical to
+    ``gather_gemm(x, perm, w_gate_up, ...)``. The tile table must hold no shared-expert rows."""
+    _need(x, "x", dtype=torch.bfloat16, ndim=2)
+    _need(w_gate_up, "w_gate_up", dtype=torch.bfloat16, ndim=3)
+    _need(perm, "perm", dtype=torch.int32)
+    _need(tiles, "tiles", dtype=torch.int32, ndim=2)
+    T, h = x.shape
+    E, twoI, hw = w_gate_up.shape
+    if hw != h:
+        raise ValueError(f"w_gate_up {tuple(w_gate_up.shape)} does not match x {tuple(x.shape)}")
+    if tiles.shape[0] != max_tiles(T, E, k, 0):
+        raise ValueError("tiles was not built for this shape (without shared-expert rows)")
+    I = twoI // 2
+    H = torch.empty(T * k, I, dtype=torch.bfloat16, device=x.device)
+    GU = torch.empty(T * k, twoI, dtype=torch.bfloat16, device=x.device)
+    check(lib.q38moe_gate_up_save(_ptr(x), _ptr(w_gate_up), _ptr(perm), _ptr(tiles), _ptr(tile_count), _ptr(H),
+                                  _ptr(GU), T, h, E, k, I, _stream(x.device)), "q38moe_gate_up_save")
+    return H, GU
+
+
 def down_kn(A, w_kn, tiles, tile_count, T, k):
     """Grouped product with K-major expert weights (q38moe_down_kn): Y[r] = bf16(A[r] . w_kn[e]) for
     the T*k sorted rows, w_kn [E, K, N] as stored (down_proj for dH, gate_up_proj for the input rows'

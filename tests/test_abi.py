@@ -35,7 +35,7 @@ def test_header_symbols_exported():
 
 def test_abi_version():
     m = _lib()
-    assert m.lib.q38moe_abi_version() == m.ABI_VERSION == 11
+    assert m.lib.q38moe_abi_version() == m.ABI_VERSION == 12
 
 
 def test_max_tiles_and_block_m():

@@ -245,6 +245,38 @@ def test_down_kn(gpu, E, k, T, K, N, drop):
         assert bool((err <= ulp + mag * 2.0 ** -20).all()), f"expert {e}: worst {float((err - ulp - mag * 2.0 ** -20).max()):.3e}"
 
 
+@pytest.mark.parametrize("name,T,drop,over", [("c2", 2048, 0, {}), ("c1", 700, 40, {}),
+                                              ("c2", 333, 9, {"experts": 7, "topk": 3, "hidden": 320, "inter": 192})])
+def test_gate_up_save(gpu, name, T, drop, over):
+    """q38moe_gate_up_save: H bit-identical to q38moe_gate_up on the same tiles (persistent kernel),
+    GU bit-identical to q38moe_gather_gemm's recomputation (the values H is computed from, same K
+    order), and GU within one bf16 rounding + fp32 accumulation of the exact products."""
+    from q38 import workloads
+    from q38.hip import ops
+    wl = workloads.get(name, **over)
+    x, params, _ = workloads.make(wl, tokens=T)
+    k, E = wl.topk, wl.experts
+    _, _, idx, _ = orc.router(x, params["gate.weight"], k)
+    if drop:
+        idx.view(-1)[torch.randperm(idx.numel(), generator=torch.Generator().manual_seed(5))[:drop]] = E
+    wgu = params["experts.gate_up_proj"]
+    dx, dwgu, di = x.to(gpu), wgu.to(gpu), idx.to(gpu)
+    hist = ops.histogram(di, E)
+    counts, starts, perm, inv, tiles, tc = ops.permute(di, hist, E)
+    H, GU = ops.gate_up_save(dx, dwgu, perm, tiles, tc, k)
+    GU2 = ops.gather_gemm(dx, perm, dwgu, tiles, tc, k)
+    torch.cuda.synchronize()
+    rows = int(counts.sum())
+    assert torch.equal(GU[:rows].cpu(), GU2[:rows].cpu())
+    if ops.gemm_tiling(T, wl.hidden, E, k, wl.inter, 0) == "persistent":
+        H2 = ops.gate_up(dx, dwgu, perm, tiles, tc, k)
+        torch.cuda.synchronize()
+        assert torch.equal(H[:rows].cpu(), H2[:rows].cpu())
+    xs = x[perm[:rows].cpu().long() // k]
+    e_of = torch.repeat_interleave(torch.arange(E), counts.cpu().long())
+    assert_gemm_bf16_rounding(GU[:rows].cpu()[e_of == 0], xs[e_of == 0], wgu[0], what="GU expert 0")
+
+
 @pytest.mark.parametrize("name,T,drop", [("c2", 2048, 0), ("c1", 700, 40)])
 def test_pair_dots_rows_fused(gpu, name, T, drop):
     """pair_dots with top_k_weights writes the same routed-row gradient as gather_rows and the same
