@@ -13,7 +13,7 @@
 
 namespace q38 {
 
-constexpr int WG_T = 128;  // weight-gradient output tile: G columns (X columns: WD_TN)
+constexpr int WG_T = 256;  // weight-gradient output tile: G columns (X columns: WD_TN)
 
 __device__ __forceinline__ float wave_sum_f(float v) {
 #pragma unroll
@@ -159,22 +159,26 @@ __global__ __launch_bounds__(256) void swiglu_backward_kernel(const uint16_t* __
 // X = H it is down_proj's [E, h, I] (torch's bf16 mm: fp32 accumulation, one rounding). The
 // reduction runs over rows, the strided dimension of both operands.
 //
-// 32-row slices of G[:, m0 .. m0+127] and X[:, n0 .. n0+255] are copied global -> LDS by
+// 32-row slices of G[:, m0 .. m0+255] and X[:, n0 .. n0+255] are copied global -> LDS by
 // global_load_lds_dwordx4 into a WD_NS-slot ring (WD_NS - 1 slices in flight, no register
 // staging; gathered X rows through an LDS ring of row indices) and the MFMA fragments are read
 // straight from the row-major slices with the gfx950 transposing LDS read ds_read_b64_tr_b16:
 // within each 16-lane group, component j of lane i is element i % 4 of the 8 bytes that lane
 // 4j + i/4 addresses, so lanes addressing rows k0 + s/4, columns c0 + 4 (s % 4) receive rows
-// k0 .. k0+3 of column c0 + i; two such reads are one 8-row fragment. Slices are row-major, 256
-// or 512 bytes per row (128 or 256 columns), 16-byte chunk c of row r at chunk c ^ 4 (r % 4): the
-// 32 lanes of a half-wave read 4 rows x 64 bytes and cover the 64 banks once. Rows past the
+// k0 .. k0+3 of column c0 + i; two such reads are one 8-row fragment. Slices are row-major, 512
+// bytes per row (256 columns), 16-byte chunk c of row r at chunk c ^ 4 (r % 4): the 32 lanes of a
+// half-wave read 4 rows x 64 bytes and cover the 64 banks once. Rows past the
 // expert's count are copied from its last row (in bounds) and zeroed in the fragments of the last
 // slice; columns past
-// M or N are copied from column 0 and never stored. One 256-thread block per 128 (G) x 256 (X)
-// tile; each wave multiplies 64 x 128 (2 x 4 blocks of mfma_f32_32x32x16_bf16, X as the A operand).
+// M or N are copied from column 0 and never stored. One 512-thread block per 256 (G) x 256 (X)
+// tile, one block per CU; each of the 8 waves multiplies 64 x 128 (2 x 4 blocks of
+// mfma_f32_32x32x16_bf16, X as the A operand). Against 128 x 256 tiles in two 4-wave blocks per CU
+// (the same per-wave work), a slice copies a third fewer bytes per FLOP, which the copies' LDS
+// writes had made the limit (gate_up_proj's gradient 137 -> 123 us, down_proj's 63 -> 58 us at
+// configuration 2).
 constexpr int WD_BK = 32;   // rows per slice
-constexpr int WD_NS = 3;    // ring slots (72 KB: two blocks per CU)
-constexpr int WD_TN = 256;  // X columns per tile (G columns: WG_T = 128)
+constexpr int WD_NS = 3;    // ring slots (96 KB + the index rings' 6 KB: one block per CU)
+constexpr int WD_TN = 256;  // X columns per tile (G columns: WG_T = 256)
 
 __device__ __forceinline__ uint32_t wd_lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane(
@@ -206,18 +210,18 @@ __device__ __forceinline__ int wd_off(int row, int col) {
 // GX: X rows gathered, X[perm[r] / k] (X = the tokens [T, N]). Each wave copies the 32 row
 // indices of slice t into its own LDS ring (global_load_lds_dword, issued two steps before slice
 // t's data copies, which read them), so the pipeline holds no compiler-visible loads: every step
-// issues the same 7 asynchronous copies per wave (6 data + 1 index) and waits with one constant.
+// issues the same 5 asynchronous copies per wave (4 data + 1 index) and waits with one constant.
 template <bool GX>
-__global__ __launch_bounds__(256) void expert_wgrad_dma_kernel(const uint16_t* G, const uint16_t* X,
+__global__ __launch_bounds__(512) void expert_wgrad_dma_kernel(const uint16_t* G, const uint16_t* X,
                                                                const int32_t* perm,
                                                                const int32_t* __restrict__ starts,
                                                                const int32_t* __restrict__ counts,
                                                                uint16_t* __restrict__ dW, int64_t P, int M,
                                                                int N, int k, int tm, int tn) {
   static_assert(!GX || WD_NS == 3, "the index lead below is written for a 3-slot ring");
-  __shared__ __align__(16) uint8_t ring_g[WD_NS][WD_BK * 2 * WG_T];   // [slot][row][128 columns]
+  __shared__ __align__(16) uint8_t ring_g[WD_NS][WD_BK * 2 * WG_T];   // [slot][row][256 columns]
   __shared__ __align__(16) uint8_t ring_x[WD_NS][WD_BK * 2 * WD_TN];  // [slot][row][256 columns]
-  __shared__ __align__(16) int32_t ring_i[GX ? 4 : 1][GX ? 3 : 1][64];  // [wave][slot][row (+32 copies)]
+  __shared__ __align__(16) int32_t ring_i[GX ? 8 : 1][GX ? 3 : 1][64];  // [wave][slot][row (+32 copies)]
   const int nb = gridDim.x, b = blockIdx.x;
   const int L = (nb & 7) == 0 ? (b & 7) * (nb >> 3) + (b >> 3) : b;
   const int e = L / (tm * tn), rem = L - e * tm * tn;
@@ -238,9 +242,9 @@ __global__ __launch_bounds__(256) void expert_wgrad_dma_kernel(const uint16_t* G
       for (int i = 0; i < 16; ++i) acc[a][c][i] = 0.0f;
 
   if (nsl > 0) {
-    // Copies: wave w fills slice rows 8w .. 8w+7 of both operands: G in 2 instructions of 4
-    // 256-byte rows (lane l: row 4q + l/16, position l % 16), X in 4 instructions of 2 512-byte
-    // rows (lane l: row 2q + l/32, position l % 32); position p of row r holds chunk p ^ 4 (r % 4).
+    // Copies: wave w fills slice rows 4w .. 4w+3 of both operands, each in 2 instructions of 2
+    // 512-byte rows (lane l: row 4w + 2q + l/32, position l % 32); position p of row r holds
+    // chunk p ^ 4 (r % 4).
     // perm[r] / k as a multiply-high by ceil(2^32 / k) (exact for pair indices below 2^29).
     const uint32_t kmagic = k > 1 ? (uint32_t)((0x100000000ull + (uint32_t)k - 1) / (uint32_t)k) : 0u;
     auto issue_idx = [&](int sl) {  // slice sl's 32 row indices (lanes 32-63 repeat them)
@@ -251,32 +255,32 @@ __global__ __launch_bounds__(256) void expert_wgrad_dma_kernel(const uint16_t* G
       const int slot = sl % WD_NS;
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        const int row = 8 * wave + 4 * q + (lane >> 4);
-        const int col = m0 + 8 * ((lane & 15) ^ (4 * (row & 3)));
+        const int row = 4 * wave + 2 * q + (lane >> 5);
+        const int col = m0 + 8 * ((lane & 31) ^ (4 * (row & 3)));
         const int64_t grow = r0 + min(sl * WD_BK + row, cnt - 1);
-        wd_dma16(G + grow * M + (col < M ? col : 0), wd_lds_addr(&ring_g[slot][(8 * wave + 4 * q) * 2 * WG_T]));
+        wd_dma16(G + grow * M + (col < M ? col : 0), wd_lds_addr(&ring_g[slot][(4 * wave + 2 * q) * 2 * WG_T]));
       }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int row = 8 * wave + 2 * q + (lane >> 5);
+      for (int q = 0; q < 2; ++q) {
+        const int row = 4 * wave + 2 * q + (lane >> 5);
         const int col = n0 + 8 * ((lane & 31) ^ (4 * (row & 3)));
         const int64_t grow = GX ? (int64_t)xrow[q] : r0 + min(sl * WD_BK + row, cnt - 1);
-        wd_dma16(X + grow * N + (col < N ? col : 0), wd_lds_addr(&ring_x[slot][(8 * wave + 2 * q) * 2 * WD_TN]));
+        wd_dma16(X + grow * N + (col < N ? col : 0), wd_lds_addr(&ring_x[slot][(4 * wave + 2 * q) * 2 * WD_TN]));
       }
     };
     // This wave's X source rows of slice sl (rows 8 wave + 2q + lane / 32): from memory for the
     // first two slices (nothing is in flight yet), then from the index ring.
     auto xrows_direct = [&](int sl, int (&xr)[4]) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t pr = (uint32_t)perm[r0 + min(sl * WD_BK + 8 * wave + 2 * q + (lane >> 5), cnt - 1)];
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t pr = (uint32_t)perm[r0 + min(sl * WD_BK + 4 * wave + 2 * q + (lane >> 5), cnt - 1)];
         xr[q] = (int)(k > 1 ? __umulhi(pr, kmagic) : pr);
       }
     };
     auto xrows_ring = [&](int sl, int (&xr)[4]) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t pr = (uint32_t)ring_i[wave][sl % 3][8 * wave + 2 * q + (lane >> 5)];
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t pr = (uint32_t)ring_i[wave][sl % 3][4 * wave + 2 * q + (lane >> 5)];
         xr[q] = (int)(k > 1 ? __umulhi(pr, kmagic) : pr);
       }
     };
@@ -295,7 +299,7 @@ __global__ __launch_bounds__(256) void expert_wgrad_dma_kernel(const uint16_t* G
       // true of every wave and orders the LDS reads of slice s-1 (drained by the lgkmcnt wait)
       // before its slot is refilled with slice s+NS-1.
       __builtin_amdgcn_s_waitcnt(0xC07F);
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((GX ? 7 : 6) * (WD_NS - 2)) : "memory");
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((GX ? 5 : 4) * (WD_NS - 2)) : "memory");
       if (GX) xrows_ring(s + WD_NS - 1, xr);
       issue(s + WD_NS - 1, xr);
       if (GX) issue_idx(s + 2 * (WD_NS - 1));
@@ -451,10 +455,10 @@ hipError_t launch_expert_wgrad(const uint16_t* G, const uint16_t* X, const int32
   const int tnd = (N + WD_TN - 1) / WD_TN;
   const dim3 grid((unsigned)((int64_t)E * tm * tnd));
   if (perm == nullptr)
-    hipLaunchKernelGGL(expert_wgrad_dma_kernel<false>, grid, dim3(256), 0, stream, G, X, perm, starts, counts, dW, P,
+    hipLaunchKernelGGL(expert_wgrad_dma_kernel<false>, grid, dim3(512), 0, stream, G, X, perm, starts, counts, dW, P,
                        M, N, k, tm, tnd);
   else
-    hipLaunchKernelGGL(expert_wgrad_dma_kernel<true>, grid, dim3(256), 0, stream, G, X, perm, starts, counts, dW, P,
+    hipLaunchKernelGGL(expert_wgrad_dma_kernel<true>, grid, dim3(512), 0, stream, G, X, perm, starts, counts, dW, P,
                        M, N, k, tm, tnd);
   return hipGetLastError();
 }
