@@ -390,7 +390,7 @@ __device__ void route_token(float z, int lane, int E, int& out_idx, float& out_w
   select_token<K>(p, all_nan, lane, E, out_idx, out_w, sv, si);
 }
 
-constexpr int ROUTE_TOKENS = 64;   // per block: 4 MFMA waves x 16 tokens
+constexpr int ROUTE_TOKENS = 64;   // tokens per histogram row (and per block, unless TOK = 128)
 constexpr int ROUTE_KCHUNK = 1024; // router-weight K columns staged in LDS at a time
 constexpr int ROUTE_WROWS = 65;    // 64 expert rows + the shared-expert gate row
 
@@ -529,7 +529,8 @@ __device__ __forceinline__ int group_select(float* row, const float* bias, int E
 }
 
 
-// One block = 64 tokens, 8 waves. Phase 1: logits on 16x16x32 MFMA (waves 0-3, 16 tokens each),
+// One block = TOK tokens (64, or 128 when a launch would need more than one round of 64-token
+// blocks), 8 waves. Phase 1: logits on 16x16x32 MFMA (TOK / 16 waves, 16 tokens each),
 // router weights (+ the shared-expert gate row as column 64) staged in LDS per 1024-wide K chunk
 // by all waves, each multiplying wave's 16 x rows loaded straight into registers with the whole
 // chunk in flight. Phase 2: bf16-rounded logits to LDS.
@@ -542,30 +543,36 @@ constexpr int ROUTE_THREADS = 512;  // 8 waves: 0-3 multiply, all select and rep
 // F32IO: the fp32 path (fp32 models): logits come in as fp32 (logits_in, computed by the fp32
 // router GEMM) and the renormalised weights leave as fp32 (no bf16 rounding, modeling:812 with
 // the fp32 logits dtype); x is unused.
-template <int KT, bool F32IO>
+template <int KT, bool F32IO, int TOK = ROUTE_TOKENS>
 __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
     const uint16_t* __restrict__ wsg, const void* __restrict__ logits_in,
     const float* __restrict__ bias, uint16_t* __restrict__ logits_out,
     int32_t* __restrict__ idx_out, void* __restrict__ w_out,
     uint16_t* __restrict__ gate_out, int32_t* __restrict__ hist, int64_t T, int h, int E, int k) {
-  __shared__ __attribute__((aligned(16))) u32x4_t s_w[ROUTE_WROWS * (ROUTE_KCHUNK / 8)];
-  // Row stride 72 (= 8 mod 64 banks): the selection's 8 lanes x 8 tokens per wave read 64
+  static_assert(TOK == 64 || TOK == 128, "64 or 128 tokens per block");
+  // Staged router weights (phase 1) and logits (from phase 2 on). With 128 tokens both do not fit
+  // side by side: they share one LDS area, and the logits are written once every wave has finished
+  // its MFMAs.
+  // Logit row stride 72 (= 8 mod 64 banks): the selection's 8 lanes x 8 tokens per wave read 64
   // distinct banks.
-  __shared__ float s_logit[ROUTE_TOKENS][72];
+  constexpr bool ALIAS = TOK > 64;
+  constexpr int W_BYTES = ROUTE_WROWS * (ROUTE_KCHUNK / 8) * 16, L_BYTES = TOK * 72 * 4;
+  __shared__ __attribute__((aligned(16)))
+  uint8_t s_wl[ALIAS ? (W_BYTES > L_BYTES ? W_BYTES : L_BYTES) : W_BYTES + L_BYTES];
+  u32x4_t* const s_w = reinterpret_cast<u32x4_t*>(s_wl);
+  float (*const s_logit)[72] = reinterpret_cast<float (*)[72]>(s_wl + (ALIAS ? 0 : W_BYTES));
   __shared__ float s_bias[64];
-  __shared__ int s_hist[64];
-  __shared__ int s_ties[ROUTE_TOKENS];
+  __shared__ int s_hist[TOK / 64][64];  // per 64-token histogram row
+  __shared__ int s_ties[TOK];
   __shared__ int s_nties;
   __shared__ float s_sv[ROUTE_THREADS / 64][64];
   __shared__ int s_si[ROUTE_THREADS / 64][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);  // the same, as a scalar
-  const int64_t tb = (int64_t)blockIdx.x * ROUTE_TOKENS;
-  if (tid < 64) {
-    s_hist[tid] = 0;
-    s_bias[tid] = (bias != nullptr && tid < E) ? bias[tid] : 0.0f;
-  }
+  const int64_t tb = (int64_t)blockIdx.x * TOK;
+  if (tid < TOK) s_hist[tid >> 6][tid & 63] = 0;
+  if (tid < 64) s_bias[tid] = (bias != nullptr && tid < E) ? bias[tid] : 0.0f;
   if (tid == 0) s_nties = 0;
 
   if (!F32IO && logits_in == nullptr) {
@@ -575,8 +582,8 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     f32x4_t acc[5];
 #pragma unroll
     for (int j = 0; j < 5; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const bool mma = wave < 4;
-    const int64_t trow = tb + (wave & 3) * 16 + (lane & 15);
+    const bool mma = wave < TOK / 16;
+    const int64_t trow = tb + (wave & (TOK / 16 - 1)) * 16 + (lane & 15);
     const uint16_t* xa = x + (trow < T ? trow : T - 1) * (int64_t)h + 8 * (lane >> 4);
     // Tiles of experts >= E (and the gate tile without wsg) multiply LDS rows that are never
     // filled; their columns are never stored. Computing them keeps the MFMA loop branch-free.
@@ -630,6 +637,7 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
         }
       }
     }
+    if (ALIAS) __syncthreads();  // every wave's MFMAs have read the staged weights
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if (mma && j < ntile) {
@@ -645,7 +653,7 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
       for (int i = 0; i < 4; ++i) s_logit[wave * 16 + 4 * (lane >> 4) + i][64] = round_bf16(acc[4][i]);
     }
   } else {
-    for (int i = tid; i < ROUTE_TOKENS * E; i += ROUTE_THREADS) {
+    for (int i = tid; i < TOK * E; i += ROUTE_THREADS) {
       const int tl = i / E, e = i - tl * E;
       const int64_t t = tb + tl;
       if (F32IO)
@@ -657,20 +665,20 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
   __syncthreads();
 
   if (logits_out != nullptr && logits_in == nullptr) {
-    for (int i = tid; i < ROUTE_TOKENS * E; i += ROUTE_THREADS) {
+    for (int i = tid; i < TOK * E; i += ROUTE_THREADS) {
       const int tl = i / E, e = i - tl * E;
       const int64_t t = tb + tl;
       if (t < T) logits_out[t * E + e] = (uint16_t)f32_to_bf16_rne(s_logit[tl][e]);
     }
   }
-  if (gate_out != nullptr && wsg != nullptr && logits_in == nullptr && tid < ROUTE_TOKENS) {
+  if (gate_out != nullptr && wsg != nullptr && logits_in == nullptr && tid < TOK) {
     const int64_t t = tb + tid;
     if (t < T) gate_out[t] = (uint16_t)f32_to_bf16_rne(s_logit[tid][64]);
   }
 
-  // Phase 3: SEL_LANES lanes per token (token wave * 64 / SEL_LANES + lane / SEL_LANES).
-  {
-    const int tl = wave * (64 / SEL_LANES) + lane / SEL_LANES;
+  // Phase 3: SEL_LANES lanes per token (token 64 pass + wave * 64 / SEL_LANES + lane / SEL_LANES).
+  for (int pass = 0; pass < TOK / 64; ++pass) {
+    const int tl = 64 * pass + wave * (64 / SEL_LANES) + lane / SEL_LANES;
     const int64_t t = tb + tl;
     if (t < T) {  // uniform over the token's lanes
       int oi[KMAX];
@@ -694,7 +702,7 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
           idx_out[t * KT + s] = my_i;
           if (F32IO) static_cast<float*>(w_out)[t * KT + s] = my_w;
           else static_cast<uint16_t*>(w_out)[t * KT + s] = (uint16_t)f32_to_bf16_rne(my_w);
-          atomicAdd(&s_hist[my_i], 1);
+          atomicAdd(&s_hist[tl >> 6][my_i], 1);
         }
       } else if (s == 0) {
         s_ties[atomicAdd(&s_nties, 1)] = tl | (sel == SEL_REPLAY_PROBS ? 0x100 : 0);
@@ -721,23 +729,50 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
       idx_out[t * k + lane] = oi;
       if (F32IO) static_cast<float*>(w_out)[t * k + lane] = ow;
       else static_cast<uint16_t*>(w_out)[t * k + lane] = (uint16_t)f32_to_bf16_rne(ow);
-      atomicAdd(&s_hist[oi], 1);
+      atomicAdd(&s_hist[tl >> 6][oi], 1);
     }
   }
   __syncthreads();
-  if (hist != nullptr && tid < E) hist[(int64_t)blockIdx.x * E + tid] = s_hist[tid];
+  // One histogram row per 64 tokens; rows wholly past T (the second half of a last 128-token
+  // block) do not exist.
+  if (hist != nullptr && tid < (TOK / 64) * 64 && (tid & 63) < E) {
+    const int64_t row = (int64_t)blockIdx.x * (TOK / 64) + (tid >> 6);
+    if (row * 64 < T) hist[row * E + (tid & 63)] = s_hist[tid >> 6][tid & 63];
+  }
+}
+
+// Compute units of the current device (cached per device).
+static int route_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
 }
 
 hipError_t launch_route(const uint16_t* x, const uint16_t* wr, const uint16_t* wsg,
                         const uint16_t* logits_in, const float* bias, uint16_t* logits_out,
                         int32_t* idx_out, uint16_t* w_out, uint16_t* gate_out, int32_t* hist,
                         int64_t T, int h, int E, int k, hipStream_t stream) {
-  const int64_t nblk = (T + ROUTE_TOKENS - 1) / ROUTE_TOKENS;
-  if (nblk == 0) return hipSuccess;
+  const int64_t nblk64 = (T + ROUTE_TOKENS - 1) / ROUTE_TOKENS;
+  if (nblk64 == 0) return hipSuccess;
+  // One block per CU at a time (the staged router weights fill most of its LDS). When 64-token
+  // blocks would take more than one round, 128-token blocks take half as many: each stages the
+  // weights once for twice the tokens (configuration 4, T = 32768: 71 -> 54 us).
+  const bool wide = nblk64 > route_cus();
+  const int64_t nblk = wide ? (T + 127) / 128 : nblk64;
 #define Q38_ROUTE(KT)                                                                                         \
   case KT:                                                                                                    \
-    hipLaunchKernelGGL((route_kernel<KT, false>), dim3((unsigned)nblk), dim3(ROUTE_THREADS), 0, stream, x, wr, \
-                       wsg, logits_in, bias, logits_out, idx_out, w_out, gate_out, hist, T, h, E, k);         \
+    if (wide)                                                                                                 \
+      hipLaunchKernelGGL((route_kernel<KT, false, 128>), dim3((unsigned)nblk), dim3(ROUTE_THREADS), 0, stream, \
+                         x, wr, wsg, logits_in, bias, logits_out, idx_out, w_out, gate_out, hist, T, h, E, k); \
+    else                                                                                                      \
+      hipLaunchKernelGGL((route_kernel<KT, false, 64>), dim3((unsigned)nblk), dim3(ROUTE_THREADS), 0, stream, \
+                         x, wr, wsg, logits_in, bias, logits_out, idx_out, w_out, gate_out, hist, T, h, E, k); \
     break;
   switch (k) {
     Q38_ROUTE(1) Q38_ROUTE(2) Q38_ROUTE(3) Q38_ROUTE(4) Q38_ROUTE(5) Q38_ROUTE(6) Q38_ROUTE(7) Q38_ROUTE(8)

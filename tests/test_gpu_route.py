@@ -48,6 +48,7 @@ def _check_selection(logits, k, gpu, bias=None):
     (1000, 8, 3, 1.0, 2),      # the reference's parity-script routing shape (E=8, k=3)
     (777, 64, 8, 0.5, 3),      # k = 8, ragged T
     (129, 17, 4, 0.5, 4),      # E not a multiple of 16
+    (40001, 64, 5, 0.64, 5),   # more 64-token blocks than CUs: 128-token blocks, ragged last block
 ])
 def test_route_from_logits_random(gpu, T, E, k, scale, seed):
     g = torch.Generator().manual_seed(seed)
@@ -125,9 +126,11 @@ def test_route_collision_bias(gpu, E, k):
     _check_selection(collision_bias_logits(4096, E=E, seed=k), k, gpu, bias=bias)
 
 
-@pytest.mark.parametrize("wl_name,T", [("c1", 2048), ("c2", 16384)])
+@pytest.mark.parametrize("wl_name,T", [("c1", 2048), ("c2", 16384), ("c2", 20000), ("c2", 33333)])
 def test_route_full(gpu, wl_name, T):
-    """Logits GEMM on MFMA: within 1 bf16 ulp of the fp32 reference; selection exact on them."""
+    """Logits GEMM on MFMA: within 1 bf16 ulp of the fp32 reference; selection exact on them.
+    T = 20000 and 33333 (more 64-token blocks than CUs) run 128-token blocks, the last one ragged
+    (33333: its second 64-token half lies past T and has no histogram row)."""
     from q38 import workloads
     wl = workloads.get(wl_name)
     x, params, _ = workloads.make(wl, tokens=T)
