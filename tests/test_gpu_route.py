@@ -49,6 +49,8 @@ def _check_selection(logits, k, gpu, bias=None):
     (777, 64, 8, 0.5, 3),      # k = 8, ragged T
     (129, 17, 4, 0.5, 4),      # E not a multiple of 16
     (40001, 64, 5, 0.64, 5),   # more 64-token blocks than CUs: 128-token blocks, ragged last block
+    (33000, 17, 4, 0.5, 6),    # the same with E not a multiple of 16
+    (20001, 64, 8, 0.5, 7),    # and k = 8
 ])
 def test_route_from_logits_random(gpu, T, E, k, scale, seed):
     g = torch.Generator().manual_seed(seed)
