@@ -14,11 +14,11 @@
 // Weights are [N, K] row-major (experts.gate_up_proj[e], experts.down_proj[e], nn.Linear), so
 // both MFMA operands are K-contiguous. One down instantiation (WKN) takes them K-major, [K, N]: the
 // experts backward multiplies by gate_up_proj[e] and down_proj[e] themselves (dx rows, dH), and
-// reads them as stored through the transposing LDS read instead of transposing them first. A tile is 256 activation rows x 256 weight rows; K runs in
-// 32-wide slices. One 512-thread workgroup per CU (8 waves, two per SIMD); wave w owns activation
-// rows 64*(w/2).. and weight rows 128*(w%2).., i.e. 2x4 blocks of mfma_f32_32x32x16_bf16 with the
-// weight fragment as the first operand, so lane = activation row and each lane holds runs of 4
-// consecutive output columns. For gate/up a wave's 128 weight rows are [64 gate | 64 up] of the
+// reads them as stored through the transposing LDS read instead of transposing them first. A tile
+// is 256 activation rows x 256 weight rows; K runs in 32-wide slices. One 512-thread workgroup per
+// CU (8 waves, two per SIMD); wave w owns activation rows 64*(w/2).. and weight rows 128*(w%2)..,
+// i.e. 2x4 blocks of mfma_f32_32x32x16_bf16 with the weight fragment as the first operand, so
+// lane = activation row and each lane holds runs of 4 consecutive output columns. For gate/up a wave's 128 weight rows are [64 gate | 64 up] of the
 // same 64 output columns, so SwiGLU runs in registers. Waves whose 64 rows are all past the
 // tile's row count skip their MFMAs; rows are paired across SIMDs (waves 0-3 hold rows 0-127), so
 // a tile of <= 128 rows costs half a full one.
