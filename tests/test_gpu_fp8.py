@@ -113,6 +113,33 @@ def test_fp8_gemm_stages(gpu, name, T):
     assert torch.equal(Hq.cpu(), rHq) and torch.equal(sH.cpu(), rsH)
 
 
+@pytest.mark.parametrize("T", [2048, 20000])
+def test_block_fp8_equals_staged_pipeline(gpu, T):
+    """The fp8 block equals bit for bit the same pipeline staged through the separate entry points
+    (route, quantize_rows of x, permute, gate_up_fp8, quantize_rows of H, down_fp8, combine): the
+    block adds no arithmetic of its own. T = 20000 runs the router's 128-token blocks (the last one
+    ragged)."""
+    ops = _ops()
+    wl, x, params, _ = _setup("c4", T)
+    k, E = wl.topk, wl.experts
+    d = {n: p.to(gpu) for n, p in params.items()}
+    wq = ops.quantize_weights_fp8(d)
+    dx = x.to(gpu)
+    out, _, idx, w = ops.block_forward_fp8(dx, d["gate.weight"], wq, d["shared_expert_gate.weight"], k,
+                                           return_router=True)
+    _, idx2, w2, gate, hist = ops.route(dx, d["gate.weight"], k, w_shared_gate=d["shared_expert_gate.weight"],
+                                        want_hist=True)
+    xq, sx = ops.quantize_rows(dx)
+    counts, starts, perm, inv, tiles, tc = ops.permute(idx2, hist, E, shared_rows=T)
+    H = ops.gate_up_fp8(xq, torch.cat([sx[perm.long() // k], sx]), wq, perm, tiles, tc, k, shared_rows=T)
+    Hq, sH = ops.quantize_rows(H)
+    Y = ops.down_fp8(Hq, sH, wq, tiles, tc, T, k, shared_rows=T)
+    out2 = ops.combine(Y[:T * k], inv, w2, E, idx=idx2, shared_out=Y[T * k:], shared_gate_logit=gate)
+    torch.cuda.synchronize()
+    assert torch.equal(idx.cpu(), idx2.cpu()) and torch.equal(w.cpu(), w2.cpu())
+    assert torch.equal(out.cpu(), out2.cpu())
+
+
 @pytest.mark.parametrize("name,T", [("c1", 2048), ("c4", 2048), ("c4", 999)])
 def test_block_forward_fp8(gpu, name, T):
     """Whole fp8 block vs the fake-quant oracle on the GPU's own routing (bit-exact routing)."""
