@@ -113,6 +113,35 @@ def test_block_forward(gpu, name, T):
     print(f"{name} T={T}: max-abs {mx:.3e} rel {r:.3e}")
 
 
+@pytest.mark.parametrize("name,T", [("c2", 16384), ("c3", 16384), ("c2", 20000), ("c2", 300)])
+def test_block_forward_equals_staged_pipeline(gpu, name, T):
+    """The fused block equals bit for bit the same pipeline staged through the separate entry points
+    (route, permute with the shared rows, gate_up with the fused shared rows, down, combine with the
+    gated shared row): the block adds no arithmetic of its own, whatever the tiling (T = 300: small
+    tiles) or the router's block size (T = 20000: 128-token blocks)."""
+    ops = _ops()
+    wl, x, params, bias = _setup(name, T)
+    k, E = wl.topk, wl.experts
+    d = {n: p.to(gpu) for n, p in params.items()}
+    dx, db = x.to(gpu), (None if bias is None else bias.to(gpu))
+    out, _, idx, w = ops.block_forward(
+        dx, d["gate.weight"], d["experts.gate_up_proj"], d["experts.down_proj"],
+        d["shared_expert.gate_proj.weight"], d["shared_expert.up_proj.weight"], d["shared_expert.down_proj.weight"],
+        d["shared_expert_gate.weight"], k, logit_bias=db, return_router=True)
+    _, idx2, w2, gate, hist = ops.route(dx, d["gate.weight"], k, w_shared_gate=d["shared_expert_gate.weight"],
+                                        logit_bias=db, want_hist=True)
+    counts, starts, perm, inv, tiles, tc = ops.permute(idx2, hist, E, shared_rows=T)
+    H = ops.gate_up(dx, d["experts.gate_up_proj"], perm, tiles, tc, k,
+                    shared_weights=(d["shared_expert.gate_proj.weight"], d["shared_expert.up_proj.weight"]),
+                    shared_rows=T)
+    Y = ops.down(H, d["experts.down_proj"], tiles, tc, T, k, w_shared_down=d["shared_expert.down_proj.weight"],
+                 shared_rows=T)
+    out2 = ops.combine(Y[:T * k], inv, w2, E, idx=idx2, shared_out=Y[T * k:], shared_gate_logit=gate)
+    torch.cuda.synchronize()
+    assert torch.equal(idx.cpu(), idx2.cpu()) and torch.equal(w.cpu(), w2.cpu())
+    assert torch.equal(out.cpu(), out2.cpu())
+
+
 @pytest.mark.parametrize("name,T", [("c1", 3001), ("c2", 16384)])
 def test_block_forward_all_tokens_tie(gpu, name, T):
     """Router rows 32..63 copy rows 0..31, so every logit has an equal twin and every token's top-k
