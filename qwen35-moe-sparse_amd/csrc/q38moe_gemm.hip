@@ -662,16 +662,9 @@ int gemm_block_m() { return BM; }
 
 // One workgroup per CU (the kernel is persistent), never more than there are tiles.
 static unsigned grid_for(int max_mtiles, int ntiles_n) {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
+  const int cus = device_cus();
   const int64_t tiles = (int64_t)max_mtiles * ntiles_n;
-  return (unsigned)(tiles < cus[dev] ? tiles : cus[dev]);
+  return (unsigned)(tiles < cus ? tiles : cus);
 }
 
 // K is in elements; e4m3 operands pass it to the kernel in 16-bit units (two elements each).

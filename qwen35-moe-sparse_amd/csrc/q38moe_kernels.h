@@ -3,7 +3,22 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace q38 {
+
+// Compute units of the current device (the persistent kernels' grid), queried once per device.
+inline int device_cus() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
 
 hipError_t launch_route(const uint16_t* x, const uint16_t* wr, const uint16_t* wsg,
                         const uint16_t* logits_in, const float* bias, uint16_t* logits_out,

@@ -741,19 +741,6 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
   }
 }
 
-// Compute units of the current device (cached per device).
-static int route_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
 hipError_t launch_route(const uint16_t* x, const uint16_t* wr, const uint16_t* wsg,
                         const uint16_t* logits_in, const float* bias, uint16_t* logits_out,
                         int32_t* idx_out, uint16_t* w_out, uint16_t* gate_out, int32_t* hist,
@@ -763,7 +750,7 @@ hipError_t launch_route(const uint16_t* x, const uint16_t* wr, const uint16_t* w
   // One block per CU at a time (the staged router weights fill most of its LDS). When 64-token
   // blocks would take more than one round, 128-token blocks take half as many: each stages the
   // weights once for twice the tokens (configuration 4, T = 32768: 71 -> 54 us).
-  const bool wide = nblk64 > route_cus();
+  const bool wide = nblk64 > device_cus();
   const int64_t nblk = wide ? (T + 127) / 128 : nblk64;
 #define Q38_ROUTE(KT)                                                                                         \
   case KT:                                                                                                    \
