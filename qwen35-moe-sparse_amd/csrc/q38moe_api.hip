@@ -300,7 +300,7 @@ int run_block(const void* x, const void* w_router, const void* w_gate_up, const 
   int32_t* idx = topk_idx != nullptr ? topk_idx : at<int32_t>(workspace, L.idx);
   int32_t* hist = at<int32_t>(workspace, L.ex.hist);
   if (f32) {
-    // fp32 block: router logits and the shared gate logit as dense fp32 GEMMs (modeling:807, 831),
+    // fp32 block: router logits and the shared gate logit in one dense fp32 GEMM (modeling:807, 831),
     // selection on them, shared expert (separate when Is != I), routed experts, gated sum.
     const float* xf = static_cast<const float*>(x);
     float* w = topk_w != nullptr ? static_cast<float*>(topk_w) : at<float>(workspace, L.w);
@@ -319,12 +319,9 @@ int run_block(const void* x, const void* w_router, const void* w_gate_up, const 
               "shared down fp32 launch");
       sh_out = sh;
     }
-    Q38_HIP(q38::launch_plain_f32(xf, nullptr, nullptr, 0, T, nullptr, static_cast<const float*>(w_router), lg, E, h,
-                                  0, st),
-            "router logits fp32 launch");
-    Q38_HIP(q38::launch_plain_f32(xf, nullptr, nullptr, 0, T, nullptr, static_cast<const float*>(w_sh_gate_proj),
-                                  gate, 1, h, 0, st),
-            "shared gate logit fp32 launch");
+    Q38_HIP(q38::launch_logits_f32(xf, static_cast<const float*>(w_router), static_cast<const float*>(w_sh_gate_proj),
+                                   lg, gate, T, E, h, st),
+            "router and shared gate logits fp32 launch");
     Q38_HIP(q38::launch_route_from_f32_logits(lg, logit_bias, idx, w, hist, T, E, k, st), "route fp32 launch");
     return run_experts(x, idx, false, w, w_gate_up, w_down, L.fused ? w_sh_gate : nullptr,
                        L.fused ? w_sh_up : nullptr, L.fused ? w_sh_down : nullptr, sh_out, gate, out, T, h, E, k, I,
@@ -429,14 +426,10 @@ int q38moe_route(const void* x, const void* w_router, const void* w_shared_gate,
     // fp32: logits as a dense fp32 GEMM into the caller's logits buffer, then the selection on them.
     if (logits == nullptr) return fail(Q38MOE_EINVAL, "dtype FP32: logits must not be NULL (the selection reads them)");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    Q38_HIP(q38::launch_plain_f32(static_cast<const float*>(x), nullptr, nullptr, 0, T, nullptr,
-                                  static_cast<const float*>(w_router), static_cast<float*>(logits), E, h, 0, st),
+    Q38_HIP(q38::launch_logits_f32(static_cast<const float*>(x), static_cast<const float*>(w_router),
+                                   shared_gate_logit != nullptr ? static_cast<const float*>(w_shared_gate) : nullptr,
+                                   static_cast<float*>(logits), static_cast<float*>(shared_gate_logit), T, E, h, st),
             "router logits fp32 launch");
-    if (shared_gate_logit != nullptr)
-      Q38_HIP(q38::launch_plain_f32(static_cast<const float*>(x), nullptr, nullptr, 0, T, nullptr,
-                                    static_cast<const float*>(w_shared_gate), static_cast<float*>(shared_gate_logit), 1,
-                                    h, 0, st),
-              "shared gate logit fp32 launch");
     Q38_HIP(q38::launch_route_from_f32_logits(static_cast<const float*>(logits), logit_bias, topk_idx,
                                               static_cast<float*>(topk_w), hist, T, E, k, st),
             "route fp32 launch");

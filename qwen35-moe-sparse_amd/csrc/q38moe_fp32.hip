@@ -44,6 +44,7 @@ struct F32Params {
   float* C;                  // output rows [*, N]
   int P;                     // first shared-expert row of the row space
   int N, K, E, topk;
+  float* C2;                 // dense plain only: one extra output column (weight row Ws_b), C2[row]
 };
 
 __device__ __forceinline__ f32x16_t mfma32x32x2_f32(float w, float a, f32x16_t c) {
@@ -113,6 +114,10 @@ __global__ __launch_bounds__(F32_THREADS) void gemm_f32_kernel(F32Params p) {
     } else {
       col = col0 + r;
       base = routed ? p.W + (int64_t)group * N * K : p.Ws_a;
+      if (!routed && p.C2 != nullptr && col == N) {  // the extra column: weight row Ws_b
+        base = p.Ws_b;
+        col = 0;
+      }
     }
     wsrc[q] = base + (int64_t)(col < N ? col : 0) * K + 4 * (tid & 7);
   }
@@ -183,8 +188,10 @@ __global__ __launch_bounds__(F32_THREADS) void gemm_f32_kernel(F32Params p) {
       *reinterpret_cast<f32x4_t*>(crow + c) = v;
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i) {
         if (c + i < N) crow[c + i] = v[i];
+        if (MODE == F32_PLAIN && p.C2 != nullptr && c + i == N) p.C2[row0 + r] = v[i];
+      }
     }
   }
 }
@@ -258,6 +265,22 @@ hipError_t launch_plain_f32(const float* A, const int4* tiles, const int32_t* nt
   const int64_t rb = tiles != nullptr ? 4 * (int64_t)max_mtiles : (M_dense + F32_BM - 1) / F32_BM;
   if (rb == 0) return hipSuccess;
   hipLaunchKernelGGL(gemm_f32_kernel<F32_PLAIN>, dim3((unsigned)rb, (unsigned)((N + F32_BN - 1) / F32_BN)),
+                     dim3(F32_THREADS), 0, stream, p);
+  return hipGetLastError();
+}
+
+// Router logits [T, E] = x . w_router^T and, with w_gate, the shared-expert gate logit [T] =
+// x . w_gate as column E of the same launch (modeling:807, 831): the same fp32 products and
+// summation order as separate dense GEMMs, in one launch.
+hipError_t launch_logits_f32(const float* x, const float* w_router, const float* w_gate, float* logits, float* gate,
+                             int64_t T, int E, int K, hipStream_t stream) {
+  if (gemm_block_m() != 4 * F32_BM) return hipErrorInvalidValue;
+  if ((w_gate == nullptr) != (gate == nullptr)) return hipErrorInvalidValue;
+  F32Params p{x, nullptr, nullptr, nullptr, T, nullptr, w_router, w_gate, logits, 0, E, K, 0, 1, gate};
+  const int64_t rb = (T + F32_BM - 1) / F32_BM;
+  if (rb == 0) return hipSuccess;
+  const int ncols = E + (gate != nullptr ? 1 : 0);
+  hipLaunchKernelGGL(gemm_f32_kernel<F32_PLAIN>, dim3((unsigned)rb, (unsigned)((ncols + F32_BN - 1) / F32_BN)),
                      dim3(F32_THREADS), 0, stream, p);
   return hipGetLastError();
 }

@@ -38,6 +38,11 @@ hipError_t launch_gate_up_f32(const float* x, const int32_t* perm, const int4* t
 hipError_t launch_plain_f32(const float* A, const int4* tiles, const int32_t* ntiles_dev, int max_mtiles,
                             int64_t M_dense, const float* W, const float* Ws, float* C, int N, int K, int E,
                             hipStream_t stream);
+
+// Router logits [T, E] and, with w_gate (and gate), the shared gate logit [T] as column E of one
+// dense fp32 launch (gemm_f32_kernel), results as from separate launch_plain_f32 calls.
+hipError_t launch_logits_f32(const float* x, const float* w_router, const float* w_gate, float* logits, float* gate,
+                             int64_t T, int E, int K, hipStream_t stream);
 hipError_t launch_combine_f32(const float* Y, const int32_t* inv, const void* idx, bool idx64, const float* w,
                               const float* shared, const float* gate, float* out, int64_t T, int h, int E, int k,
                               hipStream_t stream);
