@@ -512,8 +512,8 @@ __device__ __forceinline__ int group_select(float* row, const float* bias, int E
     id[r] = ix;
   }
   if (tie) {
-    // The replay starts from these probabilities: they replace the row's logits in LDS (read by
-    // nothing else from here on).
+    // The replay starts from these probabilities: they replace the row's logits in LDS (the
+    // logits output, when requested, has read them all before the selection starts).
 #pragma unroll
     for (int j = 0; j < PER; ++j)
       if (s + SEL_LANES * j < E) row[s + SEL_LANES * j] = ex[j] * rs;
@@ -670,6 +670,9 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
       const int64_t t = tb + tl;
       if (t < T) logits_out[t * E + e] = (uint16_t)f32_to_bf16_rne(s_logit[tl][e]);
     }
+    // The selection below overwrites tied rows' logits with their probabilities: every wave's
+    // reads of the logits come first.
+    __syncthreads();
   }
   if (gate_out != nullptr && wsg != nullptr && logits_in == nullptr && tid < TOK) {
     const int64_t t = tb + tid;

@@ -461,7 +461,7 @@ def _qsa(m, ix, x, cos, sin, cfg):
     iq = _rotate(F.linear(x, ix.wq.weight).view(B, S, nih, dih).transpose(1, 2), cos, sin)[:, :, ::BLK]
     ik = _rotate(F.linear(x, ix.wk.weight).view(B, S, 1, dih).transpose(1, 2), cos, sin)
     iw = (F.linear(x, ix.ww.weight).float() * nih ** -0.5)[:, ::BLK]
-    s = torch.matmul(iq, ik.transpose(-1, -2))
+    s = torch.matmul(iq, ik.transpose(-1, -2).contiguous())  # bf16 batched product: no transposed view
     score = (F.relu(s.float()) * dih ** -0.5 * iw.transpose(1, 2)[..., None]).sum(1)  # [B, nb, S]
     keys = torch.arange(S, device=x.device)
     starts = torch.arange(0, S, BLK, device=x.device)

@@ -128,6 +128,35 @@ def test_route_collision_bias(gpu, E, k):
     _check_selection(collision_bias_logits(4096, E=E, seed=k), k, gpu, bias=bias)
 
 
+@pytest.mark.parametrize("T", [16384, 40001])
+def test_route_logits_output_on_tied_rows(gpu, T):
+    """The logits output with most rows tied: 0/1 activations and router weights make every logit
+    an exact small integer (the MFMA sums are exact and bf16 holds them), so nearly every row ties
+    within its top k + 1 and takes the replay, whose probabilities replace the row's logits in LDS.
+    The logits written out must still be the exact integers, and the selection exact on them, on
+    each of several launches (T = 40001 runs 128-token blocks)."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(T)
+    h, E, k = 256, 64, 5
+    x = (torch.rand(T, h, generator=g) < 0.5).to(torch.bfloat16)
+    wr = (torch.rand(E, h, generator=g) < 0.1).to(torch.bfloat16)
+    ws = (torch.rand(1, h, generator=g) < 0.1).to(torch.bfloat16)
+    exact = (x.double() @ wr.double().T).to(torch.bfloat16)
+    gate_exact = (x.double() @ ws.double().reshape(-1)).to(torch.bfloat16)
+    top = exact.float().topk(k + 1, dim=1).values
+    tied = (top[:, 1:] == top[:, :-1]).any(dim=1)
+    assert float(tied.float().mean()) > 0.9
+    _, _, ridx, rw = orc.router(None, None, k, logits=exact)
+    xg, wg, wsg = x.to(gpu), wr.to(gpu), ws.to(gpu)
+    for rep in range(4):
+        logits, idx, w, gate, _ = ops.route(xg, wg, k, w_shared_gate=wsg, want_logits=True, want_hist=True)
+        torch.cuda.synchronize()
+        assert torch.equal(logits.cpu(), exact), f"launch {rep}: router logits output differs"
+        assert torch.equal(gate.cpu().reshape(-1), gate_exact), f"launch {rep}: shared gate logit differs"
+        assert torch.equal(idx.cpu().long(), ridx), f"launch {rep}: indices differ"
+        assert torch.equal(w.cpu(), rw), f"launch {rep}: weights differ"
+
+
 @pytest.mark.parametrize("wl_name,T", [("c1", 2048), ("c2", 16384), ("c2", 20000), ("c2", 33333)])
 def test_route_full(gpu, wl_name, T):
     """Logits GEMM on MFMA: within 1 bf16 ulp of the fp32 reference; selection exact on them.
