@@ -41,6 +41,16 @@ def _bf16_rows(bits):
     return (bits.astype(np.uint32) << 16).view(np.float32)
 
 
+def _assert_deterministic(logits, again):
+    """Two forwards on the same ids must agree bit for bit; on failure, say how many positions
+    differ and the first one in each sequence."""
+    if not torch.equal(logits, again):
+        diff = (logits != again).any(-1)  # [B, S]
+        first = [int(torch.nonzero(r)[0]) if r.any() else -1 for r in diff]
+        raise AssertionError(f"the HIP prefill must be deterministic: {int(diff.sum())} of {diff.numel()} "
+                             f"positions differ; first differing position per sequence {first}")
+
+
 def _rel(a, b):
     return float(np.linalg.norm(a - b) / np.linalg.norm(b))
 
@@ -76,7 +86,7 @@ def test_prefill_bf16_hip_within_reference_bf16_spread(gpu, golden, params):
     aux_ref = float(golden["aux_loss_fp32"])
     print(f"aux loss {float(out.aux_loss):.7f} vs reference fp32 {aux_ref:.7f} (bf16 {float(golden['aux_loss_bf16']):.7f})")
     assert abs(float(out.aux_loss) - aux_ref) <= max(2 * spread_aux, 0.1 * abs(aux_ref - k))
-    assert torch.equal(logits, again), "the HIP prefill must be deterministic"
+    _assert_deterministic(logits, again)
     ref32, ref16 = golden["logits_fp32"], _bf16_rows(golden["logits_bf16"])
     spread = _rel(ref16, ref32)
     spread_lse = np.abs(golden["lse_bf16"] - golden["lse_fp32"]).max()
@@ -147,7 +157,7 @@ def test_prefill_full_config5_bf16_hip(gpu, golden_full, params):
     logits = out.logits
     assert logits.shape == (4, 4096, cfg.vocab)
     assert torch.isfinite(logits).all()
-    assert torch.equal(logits, again), "the HIP prefill must be deterministic"
+    _assert_deterministic(logits, again)
     k = cfg.topk
     spread_aux = abs(float(g["aux_loss_bf16"]) - float(g["aux_loss_fp32"]))
     aux_ref = float(g["aux_loss_fp32"])
