@@ -487,6 +487,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
       _Pragma("unroll") for (int t = 0; t < 4; ++t)                                        \
         _Pragma("unroll") for (int mi = 0; mi < 2; ++mi)                                   \
           acc[t][mi] = mfma32x32x16(wx[t], ax[mi], acc[t][mi]);                            \
+      /* Issue order of the second half's reads and the first half's MFMAs: one read after */ \
+      /* each of the first six MFMAs, so the eight waves' LDS reads spread over the matrix */  \
+      /* pipe's work instead of arriving together (bit-identical; the configuration-2 block */ \
+      /* 0.2713-0.2723 -> 0.2685-0.2691 ms, same box, three interleaved runs). */          \
+      _Pragma("unroll") for (int i_ = 0; i_ < 6; ++i_) {                                   \
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); /* one MFMA */                  \
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); /* one LDS read */              \
+      }                                                                                    \
+      __builtin_amdgcn_sched_group_barrier(0x008, 10, 0);                                  \
     }                                                                                      \
     ra = ra + 1 == NA ? 0 : ra + 1;                                                        \
     rw = rw + 1 == NW ? 0 : rw + 1;                                                        \
