@@ -491,9 +491,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
       /* each of the first six MFMAs, so the eight waves' LDS reads spread over the matrix */  \
       /* pipe's work instead of arriving together (bit-identical; the configuration-2 block */ \
       /* 0.2713-0.2723 -> 0.2685-0.2691 ms, same box, three interleaved runs). */          \
-      _Pragma("unroll") for (int i_ = 0; i_ < 6; ++i_) {                                   \
+      /* (K-major weights: ten reads, two transposing reads per weight fragment, two after  */ \
+      /* each of the first five MFMAs.) */                                                  \
+      _Pragma("unroll") for (int i_ = 0; i_ < (WKN ? 5 : 6); ++i_) {                       \
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); /* one MFMA */                  \
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); /* one LDS read */              \
+        __builtin_amdgcn_sched_group_barrier(0x100, WKN ? 2 : 1, 0); /* LDS reads */       \
       }                                                                                    \
       __builtin_amdgcn_sched_group_barrier(0x008, 10, 0);                                  \
     }                                                                                      \
