@@ -5,6 +5,7 @@ q38/hip/libq38moe.so next to the ctypes loader. Every call recompiles.
 """
 import argparse
 import os
+import re
 import subprocess
 import sys
 from concurrent.futures import ThreadPoolExecutor
@@ -14,7 +15,7 @@ CSRC = Path(__file__).resolve().parent
 PKG_ROOT = CSRC.parent
 REPO = PKG_ROOT.parent
 OUT = PKG_ROOT / "q38" / "hip" / "libq38moe.so"
-SOURCES = ["q38moe_route.hip", "q38moe_permute.hip", "q38moe_gemm.hip", "q38moe_gemm_small.hip", "q38moe_combine.hip", "q38moe_quant.hip",
+SOURCES = ["q38moe_route.hip", "q38moe_permute.hip", "q38moe_gemm.hip", "q38moe_gemm4w.hip", "q38moe_gemm_small.hip", "q38moe_combine.hip", "q38moe_quant.hip",
            "q38moe_backward.hip", "q38moe_fp32.hip", "q38moe_api.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -26,13 +27,64 @@ FLAGS = [
 ]
 
 
+# Sources whose kernels issue MFMAs from inline asm: the compiler's hazard recognizer does not see
+# them, so their generated code is kept (-save-temps) and checked by mfma_operand_hazards.
+ASM_MFMA_SOURCES = ["q38moe_gemm4w.hip"]
+
+
+def mfma_operand_hazards(asm_text):
+    """VALU writes of a VGPR that an MFMA reads as its A or B operand with fewer than two wait states
+    in between (gfx950 requires two). Returns the offending (write, mfma) instruction pairs."""
+    def regs(tok):
+        out = set()
+        for m in re.finditer(r"\bv(\d+)\b|\bv\[(\d+):(\d+)\]", tok):
+            if m.group(1):
+                out.add(int(m.group(1)))
+            else:
+                out.update(range(int(m.group(2)), int(m.group(3)) + 1))
+        return out
+    ins = []
+    for line in asm_text.splitlines():
+        t = line.split(";")[0].strip()
+        if t and not t.startswith(".") and not t.endswith(":"):
+            ins.append(t)
+    bad = []
+    for k, t in enumerate(ins):
+        op = t.split()[0]
+        if not op.startswith("v_") or op.startswith("v_mfma") or len(t.split(None, 1)) < 2:
+            continue
+        dst = t.split(None, 1)[1].split(",")[0].strip()
+        if not dst.startswith("v"):
+            continue
+        d, waits = regs(dst), 0
+        for u in ins[k + 1:k + 4]:
+            if u.startswith("s_nop"):
+                waits += int(u.split()[1]) + 1
+                continue
+            if u.startswith("v_mfma") and waits < 2:
+                srcs = ",".join(u.split(None, 1)[1].split(",")[1:3])
+                if d & regs(srcs):
+                    bad.append((t, u))
+            waits += 1
+    return bad
+
+
 def _compile(src):
     obj = CSRC / "_build" / (Path(src).stem + ".o")
     cmd = [HIPCC, *FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
+    if src in ASM_MFMA_SOURCES:
+        cmd.append("-save-temps=obj")
+    res = subprocess.run(cmd, capture_output=True, text=True, cwd=str(CSRC / "_build"))
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
-    return src, res.returncode, err, obj
+    rc = res.returncode
+    if rc == 0 and src in ASM_MFMA_SOURCES:
+        asm = CSRC / "_build" / (Path(src).stem + "-hip-amdgcn-amd-amdhsa-gfx950.s")
+        bad = mfma_operand_hazards(asm.read_text())
+        if bad:
+            rc = 1
+            err += "\n".join(["MFMA operand written by VALU without wait states:"] + [f"  {a}  ->  {b}" for a, b in bad[:8]])
+    return src, rc, err, obj
 
 
 def build(jobs=None, verbose=False):

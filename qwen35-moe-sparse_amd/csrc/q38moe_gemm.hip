@@ -36,6 +36,9 @@
 // Slices are XOR-swizzled (16-byte chunk c of row r at slot c ^ ((r >> 2) & 3): conflict-free
 // fragment reads). The epilogue transposes each wave's output through a private LDS staging area so
 // that every store instruction writes whole 128-byte lines.
+#include <cstdlib>
+#include <cstring>
+
 #include "q38moe_common.h"
 #include "q38moe_kernels.h"
 
@@ -812,11 +815,27 @@ hipError_t launch_gather_gemm(const uint16_t* A, const int32_t* perm, const int4
   return hipGetLastError();
 }
 
+// Q38MOE_GEMM_WAVES=8 (read once) keeps the bf16 gate/up launch on the eight-wave kernel where the
+// four-wave one (q38moe_gemm4w.hip) would run: for A/B timing. Results differ only in fp32 summation
+// order.
+static bool use_gemm4w(int N, int K, int64_t a_rows) {
+  static const bool off = [] {
+    const char* e = std::getenv("Q38MOE_GEMM_WAVES");
+    return e != nullptr && std::strcmp(e, "8") == 0;
+  }();
+  return !off && gemm4w_supported(N, K, a_rows);
+}
+
 hipError_t launch_gate_up(const uint16_t* x, const int32_t* perm, const int4* tiles,
                           const int32_t* ntiles_dev, int max_mtiles, int64_t M_dense, int P,
                           const uint16_t* w_gate_up, const uint16_t* ws_gate,
                           const uint16_t* ws_up, uint16_t* H, int N, int K, int E, int topk,
                           hipStream_t stream) {
+  // x rows: T = P / topk tokens (tile tables) or the dense rows.
+  const int64_t x_rows = tiles != nullptr ? (int64_t)P / (topk > 0 ? topk : 1) : M_dense;
+  if (use_gemm4w(N, K, x_rows))
+    return launch_gate_up_4w(x, x_rows, perm, tiles, ntiles_dev, max_mtiles, M_dense, P, w_gate_up, ws_gate, ws_up, H,
+                             N, K, E, topk, stream);
   return gate_up_impl(x, perm, tiles, ntiles_dev, max_mtiles, M_dense, P, w_gate_up, ws_gate, ws_up, H, N, K,
                       E, topk, false, nullptr, nullptr, nullptr, nullptr, stream);
 }

@@ -74,6 +74,15 @@ hipError_t launch_down(const uint16_t* H, const int4* tiles, const int32_t* ntil
                        const uint16_t* ws_down, uint16_t* Y, int N, int K, int E,
                        hipStream_t stream);
 
+// Four-wave bf16 grouped gate/up + SwiGLU (q38moe_gemm4w.hip): same arguments and results (up to fp32
+// summation order) as launch_gate_up, which calls it when gemm4w_supported(N, K, x_rows); x_rows
+// bounds every row of x read.
+bool gemm4w_supported(int N, int K, int64_t x_rows);
+hipError_t launch_gate_up_4w(const uint16_t* x, int64_t x_rows, const int32_t* perm, const int4* tiles,
+                             const int32_t* ntiles_dev, int max_mtiles, int64_t M_dense, int P,
+                             const uint16_t* w_gate_up, const uint16_t* ws_gate, const uint16_t* ws_up, uint16_t* H,
+                             int N, int K, int E, int topk, hipStream_t stream);
+
 // Grouped gate/up + SwiGLU over routed tiles (no shared-expert rows) that also stores the bf16
 // pre-activations GU [rows, 2N] = [bf16(g) | bf16(u)] next to H [rows, N].
 hipError_t launch_gate_up_save(const uint16_t* x, const int32_t* perm, const int4* tiles, const int32_t* ntiles_dev,
