@@ -158,10 +158,15 @@ def router(x, w_router, k, logit_bias=None, logits=None, dtype=torch.bfloat16):
     return logits, probs, torch.from_numpy(idx), vals.to(dtype)
 
 
-def experts_grouped(x, idx, w, w_gate_up, w_down, return_sorted=False):
+def experts_grouped(x, idx, w, w_gate_up, w_down, return_sorted=False, _skip_rounding=()):
     """Routed experts, rounding of inference:60-130 and the k-sum of inference:199. Also returns
     the weighted per-pair rows y [T*k,h] bf16 (pair order) and H [T*k,I] bf16 (sorted order);
-    with return_sorted, also Y_raw = bf16(H . Wd^T) [T*k,h] in sorted order."""
+    with return_sorted, also Y_raw = bf16(H . Wd^T) [T*k,h] in sorted order.
+
+    _skip_rounding (tests only: planted mistakes the rounding-point test must reject) names bf16
+    roundings to leave out: "g" (gate), "u" (up), "silu", "down" (the down product)."""
+    skip = set(_skip_rounding)
+    rnd = {key: (_f if key in skip else (lambda t: _f(bf16(t)))) for key in ("g", "u", "silu", "down")}
     T, h = x.shape
     k = idx.shape[1]
     E, twoI, _ = w_gate_up.shape
@@ -180,12 +185,12 @@ def experts_grouped(x, idx, w, w_gate_up, w_down, return_sorted=False):
         rows = perm_t[s:s + c]
         A = xf[rows // k]
         gu = A @ _f(w_gate_up[e]).T
-        g = _f(bf16(gu[:, :I]))
-        u = _f(bf16(gu[:, I:]))
-        act = _f(bf16(F.silu(g)))
+        g = rnd["g"](gu[:, :I])
+        u = rnd["u"](gu[:, I:])
+        act = rnd["silu"](F.silu(g))
         He = bf16(act * u)
         H[s:s + c] = He
-        d = bf16(_f(He) @ _f(w_down[e]).T)
+        d = rnd["down"](_f(He) @ _f(w_down[e]).T)
         Y_raw[s:s + c] = d
         y[rows] = bf16(_f(d) * wflat[rows][:, None])
     out = bf16(_f(y).view(T, k, h).sum(dim=1))
