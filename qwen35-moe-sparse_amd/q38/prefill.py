@@ -349,6 +349,19 @@ def _rotate(x, cos, sin):
     return torch.cat([xr * cos + turned * sin, xp], dim=-1)
 
 
+def prefix_sum(g):
+    """Inclusive prefix sums along the last dimension (torch.cumsum(g, -1)) in a fixed order: log-step
+    doubling, elementwise adds in float64, rounded once to g's dtype. torch documents its GPU cumsum
+    of floating-point tensors as non-deterministic; this has no reduction whose order can vary. The
+    reference's CPU cumsum of float32 also accumulates in float64 (left to right)."""
+    c = g.double()
+    s = 1
+    while s < c.shape[-1]:
+        c = torch.cat([c[..., :s], c[..., s:] + c[..., :-s]], dim=-1)
+        s *= 2
+    return c.to(g.dtype)
+
+
 def gated_delta_rule(q, k, v, g, beta, chunk=64):
     """Gated delta rule over a sequence (modeling:215-349 defines it; 352-413 is the token recurrence).
 
@@ -374,7 +387,7 @@ def gated_delta_rule(q, k, v, g, beta, chunk=64):
     n = (S + pad) // chunk
     q, k, v = (t.reshape(B, H, n, chunk, -1) for t in (q, k, v))
     beta = beta.reshape(B, H, n, chunk)
-    c = g.reshape(B, H, n, chunk).cumsum(-1)
+    c = prefix_sum(g.reshape(B, H, n, chunk))
     lower = torch.ones(chunk, chunk, dtype=torch.bool, device=q.device).tril()
     decay = torch.where(lower, c[..., :, None] - c[..., None, :], torch.full((), float("-inf"),
                                                                               device=q.device)).exp()

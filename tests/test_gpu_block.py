@@ -275,3 +275,59 @@ def test_block_forward_deterministic(gpu, name):
     torch.cuda.synchronize()
     for a, b in zip(first, second):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("name,T", [("c2", 16384), ("c3", 16384), ("c2", 20000), ("c2", 300)])
+def test_block_forward_router_outputs_change_nothing(gpu, name, T):
+    """The two calls the packed prefill makes of one block, ``hip_moe_block_forward_with_router``
+    (return_router=True) and ``block(x)`` (return_router=False), over one reused workspace that
+    holds another call's data or a byte pattern: out bit-identical in every call; idx, w and the
+    logits equal the standalone router's. T = 20000 takes 128-token router blocks, T = 300 the
+    small GEMM tiles."""
+    ops = _ops()
+    wl, x, params, bias = _setup(name, T)
+    d = {n: p.to(gpu) for n, p in params.items()}
+    dx = x.to(gpu)
+    args = (dx, d["gate.weight"], d["experts.gate_up_proj"], d["experts.down_proj"],
+            d["shared_expert.gate_proj.weight"], d["shared_expert.up_proj.weight"],
+            d["shared_expert.down_proj.weight"], d["shared_expert_gate.weight"], wl.topk)
+    lb = None if bias is None else bias.to(gpu)
+    nbytes = ops.block_workspace_bytes(T, wl.hidden, wl.experts, wl.topk, wl.inter, wl.shared_inter)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+    runs = []
+    for fill, want in ((0xFF, False), (0x00, True), (0x7F, False), (None, True), (None, False), (0xFF, True)):
+        if fill is not None:
+            ws.fill_(fill)  # bf16 0xFFFF is a NaN, 0x7F7F the largest finite value
+        res = ops.block_forward(*args, logit_bias=lb, return_router=want, workspace=ws)
+        runs.append(res if want else (res,))
+    logits, idx, w, _, _ = ops.route(dx, d["gate.weight"], wl.topk, w_shared_gate=d["shared_expert_gate.weight"],
+                                     logit_bias=lb, want_logits=True)
+    torch.cuda.synchronize()
+    out0 = runs[0][0]
+    assert torch.isfinite(out0).all()
+    for i, r in enumerate(runs):
+        assert torch.equal(r[0], out0), f"call {i}: out differs"
+        if len(r) == 4:
+            assert torch.equal(r[1], logits), f"call {i}: logits differ from the router's"
+            assert torch.equal(r[2], idx), f"call {i}: idx differs from the router's"
+            assert torch.equal(r[3], w), f"call {i}: w differs from the router's"
+
+
+def test_dropin_block_with_and_without_router_logits(gpu):
+    """The drop-in module's two prefill calls on its cached workspace give the same bits."""
+    from q38.inference import hip_moe_block_forward_with_router
+    from q38.models.qwen3_8_moe import Qwen3_8MoeSparseMoeBlock, new_config
+    wl, x, params, _ = _setup("c2", 4096)
+    cfg = new_config(hidden_size=wl.hidden, num_experts=wl.experts, num_experts_per_tok=wl.topk,
+                     moe_intermediate_size=wl.inter, shared_expert_intermediate_size=wl.shared_inter)
+    block = Qwen3_8MoeSparseMoeBlock(cfg).to(torch.bfloat16)
+    block.load_state_dict(params, strict=True)
+    block = block.to(gpu)
+    xs = x.view(2, -1, wl.hidden).to(gpu)
+    with torch.inference_mode():
+        plain = block(xs)
+        with_router, logits = hip_moe_block_forward_with_router(block, xs)
+        again = block(xs)
+    torch.cuda.synchronize()
+    assert torch.equal(plain, with_router) and torch.equal(plain, again)
+    assert logits.shape == (4096, wl.experts)

@@ -41,14 +41,42 @@ def _bf16_rows(bits):
     return (bits.astype(np.uint32) << 16).view(np.float32)
 
 
-def _assert_deterministic(logits, again):
-    """Two forwards on the same ids must agree bit for bit; on failure, say how many positions
-    differ and the first one in each sequence."""
-    if not torch.equal(logits, again):
-        diff = (logits != again).any(-1)  # [B, S]
-        first = [int(torch.nonzero(r)[0]) if r.any() else -1 for r in diff]
-        raise AssertionError(f"the HIP prefill must be deterministic: {int(diff.sum())} of {diff.numel()} "
-                             f"positions differ; first differing position per sequence {first}")
+def _record_blocks(model):
+    """Keep every MoE call's input and output: the list gets one (x, y) per layer and forward."""
+    calls = []
+    inner = model._moe
+
+    def moe(block, x, with_router):
+        res = inner(block, x, with_router)
+        calls.append((x.clone(), (res[0] if with_router else res).clone()))
+        return res
+
+    model._moe = moe
+    return calls
+
+
+def _assert_deterministic(logits, again, first, second):
+    """Two forwards on the same ids (the first with the router-logits output, the second without)
+    must agree bit for bit. On failure, say how many positions differ and the first one in each
+    sequence, and name where the forwards parted: the first layer whose MoE block received different
+    inputs (a trunk op diverged before it), or whose block gave different outputs for identical
+    inputs (the block diverged)."""
+    if torch.equal(logits, again):
+        return
+    diff = (logits != again).any(-1)  # [B, S]
+    first_pos = [int(torch.nonzero(r)[0]) if r.any() else -1 for r in diff]
+    where = "every block's input and output identical: after the last block (final norm, head)"
+    for i, ((x1, y1), (x2, y2)) in enumerate(zip(first, second)):
+        if not torch.equal(x1, x2):
+            n = int((x1 != x2).any(-1).sum())
+            where = f"layer {i}: the MoE block's input differs at {n} tokens (the trunk diverged before it)"
+            break
+        if not torch.equal(y1, y2):
+            n = int((y1 != y2).any(-1).sum())
+            where = f"layer {i}: identical block input, block output differs at {n} tokens (the block diverged)"
+            break
+    raise AssertionError(f"the HIP prefill must be deterministic: {int(diff.sum())} of {diff.numel()} "
+                         f"positions differ; first differing position per sequence {first_pos}; {where}")
 
 
 def _rel(a, b):
@@ -73,8 +101,11 @@ def test_prefill_fp32_trunk_on_gpu(gpu, golden, params):
 def test_prefill_bf16_hip_within_reference_bf16_spread(gpu, golden, params):
     model = P.Q38Prefill(P.c5_config()).load_params(params).to(device=gpu, dtype=torch.bfloat16)
     ids = torch.from_numpy(golden["ids"].astype(np.int64)).to(gpu)
+    calls = _record_blocks(model)
     with torch.inference_mode():
         out = model(ids, output_router_logits=True)
+        first = list(calls)
+        calls.clear()
         again = model(ids)
     logits = out.logits
     assert logits.dtype == torch.bfloat16 and torch.isfinite(logits).all()
@@ -86,7 +117,7 @@ def test_prefill_bf16_hip_within_reference_bf16_spread(gpu, golden, params):
     aux_ref = float(golden["aux_loss_fp32"])
     print(f"aux loss {float(out.aux_loss):.7f} vs reference fp32 {aux_ref:.7f} (bf16 {float(golden['aux_loss_bf16']):.7f})")
     assert abs(float(out.aux_loss) - aux_ref) <= max(2 * spread_aux, 0.1 * abs(aux_ref - k))
-    _assert_deterministic(logits, again)
+    _assert_deterministic(logits, again, first, calls)
     ref32, ref16 = golden["logits_fp32"], _bf16_rows(golden["logits_bf16"])
     spread = _rel(ref16, ref32)
     spread_lse = np.abs(golden["lse_bf16"] - golden["lse_fp32"]).max()
@@ -151,13 +182,16 @@ def test_prefill_full_config5_bf16_hip(gpu, golden_full, params):
     cfg = P.c5_config()
     model = P.Q38Prefill(cfg).load_params(params).to(device=gpu, dtype=torch.bfloat16)
     ids = torch.from_numpy(g["ids"].astype(np.int64)).to(gpu)
+    calls = _record_blocks(model)
     with torch.inference_mode():
         out = model(ids, output_router_logits=True)
+        first = list(calls)
+        calls.clear()
         again = model(ids)
     logits = out.logits
     assert logits.shape == (4, 4096, cfg.vocab)
     assert torch.isfinite(logits).all()
-    _assert_deterministic(logits, again)
+    _assert_deterministic(logits, again, first, calls)
     k = cfg.topk
     spread_aux = abs(float(g["aux_loss_bf16"]) - float(g["aux_loss_fp32"]))
     aux_ref = float(g["aux_loss_fp32"])

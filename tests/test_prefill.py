@@ -34,6 +34,25 @@ def _recurrent_delta(q, k, v, g, beta):
     return out
 
 
+@pytest.mark.parametrize("n", [1, 2, 17, 64])
+def test_prefix_sum_is_cpu_cumsum(n):
+    """The fixed-order prefix sum in the delta rule equals torch's CPU cumsum (float64 accumulation,
+    left to right) bit for bit on gate values of the DeltaNet's range and on magnitudes spread over
+    2^-40 .. 2^20; a first-order (float32) doubling scan is not."""
+    torch.manual_seed(n)
+    g = -torch.rand(64, 7, n).exp() * torch.nn.functional.softplus(torch.randn(64, 7, n) * 4)
+    wide = -torch.exp2(torch.randint(-40, 21, (64, 7, n)).float()) * torch.rand(64, 7, n)
+    for t in (g, wide):
+        assert torch.equal(P.prefix_sum(t), t.cumsum(-1))
+    if n == 64:
+        c = g.clone()
+        s = 1
+        while s < n:  # the same doubling in float32: a different rounding sequence
+            c = torch.cat([c[..., :s], c[..., s:] + c[..., :-s]], dim=-1)
+            s *= 2
+        assert not torch.equal(c, g.cumsum(-1))
+
+
 @pytest.mark.parametrize("S", [1, 64, 150])
 def test_delta_rule_matches_recurrence(S):
     torch.manual_seed(S)
