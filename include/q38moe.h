@@ -340,6 +340,8 @@ int q38moe_gather_gemm(const void* x, const int32_t* perm, const void* w, const 
  *   GU[r] = [bf16(x_r . w_gate_up[e, :I]) | bf16(x_r . w_gate_up[e, I:])]   [T*k, 2I] bf16
  * next to H [T*k, I]. They are the values H is computed from, bit-identical to q38moe_gather_gemm
  * on the same tiles, so the backward's SwiGLU step reads them instead of recomputing them.
+ * Shared-expert tiles in the table (group E, from q38moe_permute with shared_rows > 0) are skipped:
+ * their rows are neither read nor written.
  */
 int q38moe_gate_up_save(const void* x, const void* w_gate_up, const int32_t* perm, const int32_t* tiles,
                         const int32_t* tile_count, void* H, void* GU, int64_t T, int32_t h, int32_t E, int32_t k,
@@ -354,6 +356,7 @@ int q38moe_gate_up_save(const void* x, const void* w_gate_up, const int32_t* per
  * on the per-expert transposes of w_kn (bit-identical results), without the transposes:
  *   dH rows:       A = routed rows' gradient (K = h), w_kn = down_proj [E,h,I]     -> N = I
  *   dx rows:       A = [d_g | d_u] (K = 2I),          w_kn = gate_up_proj [E,2I,h] -> N = h
+ * Shared-expert tiles in the table (group E) are skipped: their rows are neither read nor written.
  */
 int q38moe_down_kn(const void* A, const void* w_kn, const int32_t* tiles, const int32_t* tile_count, void* Y,
                    int64_t T, int32_t K, int32_t N, int32_t E, int32_t k, void* stream);

@@ -184,7 +184,9 @@ __global__ __launch_bounds__(F32_THREADS) void gemm_f32_kernel(F32Params p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       v[i] = MODE == F32_GATE_UP ? swiglu_f32(acc[0][4 * g4 + i], acc[1][4 * g4 + i]) : acc[0][4 * g4 + i];
-    if (c + 3 < N) {
+    // 16-byte stores only where the row stride keeps them aligned (N % 4 == 0; c is a multiple of
+    // 4); narrow or odd widths (router logits with E % 4 != 0) store element by element.
+    if ((N & 3) == 0 && c + 3 < N) {
       *reinterpret_cast<f32x4_t*>(crow + c) = v;
     } else {
 #pragma unroll

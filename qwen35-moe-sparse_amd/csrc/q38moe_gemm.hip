@@ -126,6 +126,15 @@ __device__ __forceinline__ int4 tile_entry(const GemmParams& p, int mt) {
   return make_int4(p.E, row0, (int)min((int64_t)BM, p.M - (int64_t)row0), 0);
 }
 
+// Entry of a table that must hold expert groups only (the K-major down and the saving gate/up,
+// whose callers permute without shared rows): a shared-expert tile found there runs as an empty
+// tile of expert 0 from row 0, so every read stays in bounds and nothing is stored.
+template <bool EXPERTS_ONLY>
+__device__ __forceinline__ int4 tile_entry_of(const GemmParams& p, int mt) {
+  const int4 t = tile_entry(p, mt);
+  return EXPERTS_ONLY && t.x >= p.E ? make_int4(0, 0, 0, 0) : t;
+}
+
 // True when the activation rows of tile `ti` are gathered through perm (routed gate/up rows).
 template <int MODE>
 __device__ __forceinline__ bool gathered(const GemmParams& p, int4 ti) {
@@ -338,10 +347,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
   // on one XCD) keep one order, so their copies of the same weight rows and, for the output-column
   // tiles of a row tile, of the same gathered activation rows meet in that XCD's L2.
   auto rot_of = [&](int4 t_, int u) { return (t_.x < p.E ? 2 * t_.x : 2 * (u / p.ntiles_n)) % nk; };
-  int4 ti = tile_entry(p, L / p.ntiles_n);
+  int4 ti = tile_entry_of<WKN || SAVE_GU>(p, L / p.ntiles_n);
   int rot = rot_of(ti, L);
   int Ln = L + step;
-  int4 tin = (Ln >= 0 && Ln < used) ? tile_entry(p, Ln / p.ntiles_n) : make_int4(0, 0, 0, 0);
+  int4 tin = (Ln >= 0 && Ln < used) ? tile_entry_of<WKN || SAVE_GU>(p, Ln / p.ntiles_n) : make_int4(0, 0, 0, 0);
   int rows[NCOPY], rows_n[NCOPY];
   const uint16_t* src[NCOPY];
   const uint16_t* src_n[NCOPY];
@@ -409,7 +418,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams p)
         const int r = 64 * wave + lane;
         dma4(p.perm + tin.y + (r < tin.z ? r : 0), lds_addr(next_rows + 64 * wave));
       }
-      if (Lnn >= 0 && Lnn < used) tinn = tile_entry(p, Lnn / p.ntiles_n);
+      if (Lnn >= 0 && Lnn < used) tinn = tile_entry_of<WKN || SAVE_GU>(p, Lnn / p.ntiles_n);
     }
 
     // Step: wait until at most N of this wave's vector-memory operations are outstanding, which

@@ -277,6 +277,43 @@ def test_gate_up_save(gpu, name, T, drop, over):
     assert_gemm_bf16_rounding(GU[:rows].cpu()[e_of == 0], xs[e_of == 0], wgu[0], what="GU expert 0")
 
 
+def test_expert_only_kernels_skip_shared_tiles(gpu):
+    """q38moe_down_kn and q38moe_gate_up_save given a tile table that also holds shared-expert rows
+    (q38moe_permute with shared_rows = T, through the C ABI: the Python wrappers refuse it): the
+    routed rows equal the expert-only table's results and the rows from T*k on stay untouched."""
+    from q38 import workloads
+    from q38.hip import ops
+    wl = workloads.get("c2")
+    T, k, E, h, I = 2048, wl.topk, wl.experts, wl.hidden, wl.inter
+    x, params, _ = workloads.make(wl, tokens=T)
+    _, _, idx, _ = orc.router(x, params["gate.weight"], k)
+    dx, di = x.to(gpu), idx.to(gpu)
+    dwgu, dwdn = params["experts.gate_up_proj"].to(gpu), params["experts.down_proj"].to(gpu)
+    hist = ops.histogram(di, E)
+    counts, starts, perm, inv, tiles, tc = ops.permute(di, hist, E)
+    _, _, perm_s, _, tiles_s, tc_s = ops.permute(di, hist, E, shared_rows=T)
+    P = T * k
+    H_ref, GU_ref = ops.gate_up_save(dx, dwgu, perm, tiles, tc, k)
+    A = (torch.randn(P, h, generator=torch.Generator().manual_seed(3)) * 0.5).to(torch.bfloat16).to(gpu)
+    Y_ref = ops.down_kn(A, dwdn, tiles, tc, T, k)
+    pattern = torch.tensor(0x7F7F, dtype=torch.int16).view(torch.bfloat16)  # largest finite bf16
+    H = torch.full((P + T, I), float(pattern), dtype=torch.bfloat16, device=gpu)
+    GU = torch.full((P + T, 2 * I), float(pattern), dtype=torch.bfloat16, device=gpu)
+    Y = torch.full((P + T, I), float(pattern), dtype=torch.bfloat16, device=gpu)
+    st = ops._stream(dx.device)
+    ops.check(ops.lib.q38moe_gate_up_save(ops._ptr(dx), ops._ptr(dwgu), ops._ptr(perm_s), ops._ptr(tiles_s),
+                                          ops._ptr(tc_s), ops._ptr(H), ops._ptr(GU), T, h, E, k, I, st),
+              "q38moe_gate_up_save")
+    ops.check(ops.lib.q38moe_down_kn(ops._ptr(A), ops._ptr(dwdn), ops._ptr(tiles_s), ops._ptr(tc_s), ops._ptr(Y),
+                                     T, h, I, E, k, st), "q38moe_down_kn")
+    torch.cuda.synchronize()
+    assert int(tc_s.item()) > int(tc.item())  # the table does hold shared-expert tiles
+    assert torch.equal(perm_s[:P], perm[:P])
+    assert torch.equal(H[:P], H_ref) and torch.equal(GU[:P], GU_ref) and torch.equal(Y[:P], Y_ref)
+    for nm, t in (("H", H), ("GU", GU), ("Y", Y)):
+        assert bool((t[P:] == pattern).all()), f"{nm}: rows past T*k were written"
+
+
 @pytest.mark.parametrize("name,T,drop", [("c2", 2048, 0), ("c1", 700, 40)])
 def test_pair_dots_rows_fused(gpu, name, T, drop):
     """pair_dots with top_k_weights writes the same routed-row gradient as gather_rows and the same
