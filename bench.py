@@ -242,31 +242,30 @@ def cpu_baseline(wl, budget_s=8.0):
                 variants=variants, **host)
 
 
-# Kernel symbol prefix of each stage, as rocprofv3 names it (the committed PMC byte counts are keyed
-# by stage and record the full kernel name they were read from).
+# Kernel symbol of each stage, as rocprofv3 names it (the committed PMC byte counts are keyed by stage
+# and record the full kernel name they were read from): bf16 gate/up runs the four-wave kernel where
+# its shape rule allows, the eight-wave grouped kernel otherwise (fp8, narrow K or N).
 KERNEL_SYMBOLS = {
-    "route": "q38::route_kernel",
-    "permute": "q38::permute_kernel",
-    "gate_up": "q38::grouped_gemm_kernel<0,",
-    "down": "q38::grouped_gemm_kernel<1,",
-    "combine": "q38::combine_kernel",
+    "route": ("q38::route_kernel",),
+    "permute": ("q38::permute_kernel",),
+    "gate_up": ("gemm4w_gate_up_kernel", "q38::grouped_gemm_kernel<0,"),
+    "down": ("q38::grouped_gemm_kernel<1,",),
+    "combine": ("q38::combine_kernel",),
 }
 TRAFFIC_FILE = REPO / "profiles" / "hbm_traffic.json"
 
 
 def hbm_traffic(workload, stage):
-    """HBM bytes per launch of `stage` from the committed rocprofv3 PMC summary: FETCH_SIZE and
-    WRITE_SIZE (KiB per dispatch), each scaled by the factor a plain copy of known size gives those
-    counters on the same device. None when no summary for this workload and stage exists."""
+    """HBM bytes per launch of `stage` from the committed rocprofv3 PMC summary: the read requests that
+    leave L2 weighted by their size (TCC_EA0_RDREQ_32B/64B/128B) plus WRITE_SIZE, each scaled by the
+    factor a plain 256 MiB copy gives the same counters. None when no summary for this workload and
+    stage exists."""
     try:
         data = json.loads(TRAFFIC_FILE.read_text())
     except (OSError, ValueError):
         return None
     entry = data.get("workloads", {}).get(workload, {}).get(stage)
-    if not entry:
-        return None
-    f = data["copy_calibration"]
-    return round(entry["FETCH_SIZE_KiB"] * f["fetch_factor"] * 1024 + entry["WRITE_SIZE_KiB"] * f["write_factor"] * 1024)
+    return entry.get("hbm_bytes") if entry else None
 
 
 MFMA_FILE = REPO / "profiles" / "mfma_busy.json"
