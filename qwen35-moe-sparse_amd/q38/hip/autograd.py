@@ -1,4 +1,5 @@
-"""Differentiable routed experts on HIP: the training counterpart of ``ops.experts_forward``.
+"""Differentiable HIP MoE pieces: the routed experts (the training counterpart of
+``ops.experts_forward``), the router and the shared expert.
 
 The reference's differentiable experts path is ``padded_batched_experts_forward``
 (q38/inference.py:358-384: gather, bmm gate/up, SiLU * up, bmm down, * top_k_weights, scatter-sum);
@@ -95,3 +96,75 @@ def experts(x, topk_idx, topk_w, w_gate_up, w_down):
     args = [t.to(torch.bfloat16).contiguous() for t, _ in named]
     out = HipExperts.apply(args[0], topk_idx.contiguous(), args[1], args[2], args[3])
     return out.to(x.dtype) if cast else out
+
+
+class HipRouter(torch.autograd.Function):
+    """Qwen3_8MoeTopKRouter.forward (modeling:805-812) with a backward. Forward: the HIP route kernel
+    (logits on MFMA, fp32 softmax, top-k, renormalised weights). Backward, differentiating the same
+    steps in fp32 from the saved logits: the renormalisation w = v / sum(v) of the top-k
+    probabilities v, torch.topk's scatter of their gradient into the probability row, the softmax,
+    plus the logits' own gradient (the load-balancing loss reads them through the gate's forward
+    hook, q38/train.py:228-233); then the linear layer's two products in the logits' dtype."""
+
+    @staticmethod
+    def forward(ctx, x, w_router, k, logit_bias):
+        logits, idx, w, _, _ = ops.route(x, w_router, k, logit_bias=logit_bias, want_logits=True)
+        ctx.save_for_backward(x, w_router, logits, idx, logit_bias)
+        ctx.mark_non_differentiable(idx)
+        return logits, w, idx
+
+    @staticmethod
+    def backward(ctx, d_logits, d_w, _):
+        x, w_router, logits, idx, bias = ctx.saved_tensors
+        need_x, need_w = ctx.needs_input_grad[:2]
+        return (*router_backward(x, w_router, logits, idx, bias, d_logits, d_w, need_x, need_w), None, None)
+
+
+def router_backward(x, w_router, logits, idx, bias, d_logits, d_w, need_x=True, need_w=True):
+    """Gradients (dx, d w_router) of the router's outputs (logits, renormalised top-k weights) given
+    their gradients (either may be None), from the forward's logits and indices."""
+    z = logits.float() if bias is None else logits.float() + bias
+    p = torch.softmax(z, dim=-1)
+    dz = None
+    if d_w is not None:
+        il = idx.long()
+        v = p.gather(1, il)
+        s = v.sum(1, keepdim=True)
+        gw = d_w.float()
+        dv = (gw - (gw * (v / s)).sum(1, keepdim=True)) / s  # through w = v / sum(v)
+        dp = torch.zeros_like(p).scatter_(1, il, dv)           # torch.topk's backward
+        dz = p * (dp - (dp * p).sum(1, keepdim=True))           # softmax's backward
+    if d_logits is not None:
+        dz = d_logits.float() if dz is None else dz + d_logits.float()
+    if dz is None:
+        return None, None
+    dz = dz.to(logits.dtype)
+    dx = dz @ w_router if need_x else None
+    dwr = dz.t().contiguous() @ x if need_w else None
+    return dx, dwr
+
+
+def router(x, w_router, k, logit_bias=None):
+    """Router with autograd: (logits [T,E], weights [T,k], indices int32 [T,k]) as the gate module
+    returns them (modeling:805-813); gradients flow to x and w_router through the weights and the
+    logits. bf16 or fp32 tensors; under bf16 autocast other float dtypes are cast to bf16
+    differentiably (autocast's F.linear), and the logits and weights come out in bf16."""
+    if _bf16_autocast() and (x.dtype != torch.bfloat16 or w_router.dtype != torch.bfloat16):
+        x, w_router = x.to(torch.bfloat16), w_router.to(torch.bfloat16)
+    if logit_bias is not None:
+        logit_bias = logit_bias.float().contiguous()
+    return HipRouter.apply(x.contiguous(), w_router.contiguous(), k, logit_bias)
+
+
+def shared_expert(x, w_gate, w_up, w_down):
+    """The shared SwiGLU MLP (modeling:751-753) with autograd, as the routed experts' path with one
+    expert and every token routed to it at weight 1: gate/up, bf16 SiLU * up and down round at the
+    MLP's own points, and the k-sum of one exact term changes nothing. Gradients flow to x and the
+    three weights (through the concatenation [gate; up] = gate_up_proj[0])."""
+    T = x.shape[0]
+    idx = torch.zeros(T, 1, dtype=torch.int32, device=x.device)
+    ones = torch.ones(T, 1, dtype=torch.bfloat16, device=x.device)
+    w_gate_up = torch.cat([w_gate, w_up], 0).unsqueeze(0)
+    out = experts(x, idx, ones, w_gate_up, w_down.unsqueeze(0))
+    # Under autocast the MLP's last nn.Linear returns the autocast dtype, whatever x's dtype.
+    return out.to(torch.bfloat16) if _bf16_autocast() else out

@@ -18,9 +18,14 @@ from .hip import ops
 EXPERTS_IMPLEMENTATION = "q38_hip"
 
 
+def _needs_grad(*tensors):
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors)
+
+
 def _forward_only(*tensors):
-    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
-        raise RuntimeError("The HIP MoE path has no backward; run it under torch.inference_mode()")
+    if _needs_grad(*tensors):
+        raise RuntimeError("The fused HIP MoE block has no backward; run it under torch.inference_mode() "
+                           "or call the block module, which runs its differentiable submodules")
 
 
 def _check_act(act_name):

@@ -10,10 +10,13 @@ of ``q38.prefill``; it is registered for the Auto classes like the reference (__
 ``save_pretrained`` exports this file and ``from_pretrained(..., trust_remote_code=True)`` runs the
 kernels again. The imports of the library are absolute because an export runs this file outside
 the package: the ``q38`` package must be importable where an export is loaded.
-Under autograd the routed experts (``Qwen3_8MoeExperts``) are differentiable (the HIP backward:
-bf16 tensors, or fp32 parameters under bf16 autocast); the router, the shared MLP, the fused block
-and the causal LM are forward-only and raise under autograd. Inputs and weights are CUDA tensors;
-there is no CPU path.
+Under autograd the block is differentiable: the routed experts and the shared MLP through the HIP
+experts backward (bf16 tensors, or fp32 parameters under bf16 autocast), the router through its
+HIP forward and a backward of the softmax / top-k / renormalisation steps, and the shared gate
+through torch; the block then runs as its submodules, so a forward hook on ``gate`` (the reference
+trainer's router recorder, q38/train.py:228-233) sees the router output and its gradient reaches
+the router. Without autograd and hooks the block is one fused HIP call. The causal LM is
+forward-only. Inputs and weights are CUDA tensors; there is no CPU path.
 """
 import torch
 from torch import nn
@@ -22,7 +25,7 @@ from transformers.modeling_utils import PreTrainedModel
 
 from q38 import prefill as _prefill
 from q38.hip import ops
-from q38.inference import (EXPERTS_IMPLEMENTATION, _check_act, _forward_only, hip_experts_forward,
+from q38.inference import (EXPERTS_IMPLEMENTATION, _check_act, _needs_grad, hip_experts_forward,
                            hip_moe_block_forward, hip_moe_block_forward_with_router,
                            register_experts_implementation)
 
@@ -53,8 +56,12 @@ class Qwen3_8MoeMLP(nn.Module):
         self.act_fn = nn.SiLU()
 
     def forward(self, x):
-        _forward_only(x, self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight)
         shape = x.shape
+        if _needs_grad(x, self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight):
+            from q38.hip import autograd
+            out = autograd.shared_expert(x.reshape(-1, shape[-1]), self.gate_proj.weight, self.up_proj.weight,
+                                         self.down_proj.weight)
+            return out.view(*shape[:-1], out.shape[-1])
         out = ops.shared_expert(x.reshape(-1, shape[-1]).contiguous(), self.gate_proj.weight,
                                 self.up_proj.weight, self.down_proj.weight)
         return out.view(shape)
@@ -94,8 +101,12 @@ class Qwen3_8MoeTopKRouter(nn.Module):
         self.routing_bias = None  # optional fp32 [E] logit bias (routing-skew workload only)
 
     def forward(self, hidden_states):
-        _forward_only(hidden_states, self.weight)
-        hidden_states = hidden_states.reshape(-1, self.hidden_dim).contiguous()
+        hidden_states = hidden_states.reshape(-1, self.hidden_dim)
+        if _needs_grad(hidden_states, self.weight):
+            from q38.hip import autograd
+            logits, scores, idx = autograd.router(hidden_states, self.weight, self.top_k, logit_bias=self.routing_bias)
+            return logits, scores, idx.long()
+        hidden_states = hidden_states.contiguous()
         logits, idx, scores, _, _ = ops.route(hidden_states, self.weight, self.top_k, logit_bias=self.routing_bias,
                                               want_logits=True)
         return logits, scores, idx.long()
@@ -116,22 +127,29 @@ class Qwen3_8MoeSparseMoeBlock(nn.Module):
         return self.gate.routing_bias
 
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
-        if self.gate._forward_hooks or self.gate._forward_pre_hooks:
+        if (self.gate._forward_hooks or self.gate._forward_pre_hooks
+                or _needs_grad(hidden_states, *(p for p in self.parameters()))):
             # Observers of the router output (modeling:928; q38/train.py:228) see the gate
-            # module's tuple: run the block as its submodules, each on the HIP kernels.
+            # module's tuple, and autograd needs the pieces: run the block as its submodules.
             return self._forward_by_submodules(hidden_states)
         return hip_moe_block_forward(self, hidden_states)
 
     def _forward_by_submodules(self, hidden_states):
+        """modeling:824-835 as its submodules, each on the HIP kernels."""
         batch_size, sequence_length, hidden_dim = hidden_states.shape
         x = hidden_states.view(-1, hidden_dim)
         shared_expert_output = self.shared_expert(x)
         _, routing_weights, selected_experts = self.gate(x)
         expert_output = self.experts(x, selected_experts, routing_weights)
-        gate_logit = ops.route(x.contiguous(), self.gate.weight, self.gate.top_k,
-                               w_shared_gate=self.shared_expert_gate.weight)[3]
+        gate_logit = self.shared_expert_gate(x)
+        if torch.is_grad_enabled() and (gate_logit.requires_grad or expert_output.requires_grad
+                                        or shared_expert_output.requires_grad):
+            # The reference's own ops (modeling:831-833), differentiable.
+            out = expert_output + torch.sigmoid(gate_logit) * shared_expert_output
+            return out.reshape(batch_size, sequence_length, hidden_dim)
         # sigmoid(shared_expert_gate(x)) * shared + routed, in x's dtype (modeling:831-833): the
         # combine with one pair per token, weight 1 (exact) and the identity row map.
+        gate_logit = gate_logit.reshape(-1).to(x.dtype)
         T = x.shape[0]
         ident = torch.arange(T, dtype=torch.int32, device=x.device)
         ones = torch.ones(T, 1, dtype=x.dtype, device=x.device)

@@ -42,3 +42,44 @@ def test_registered_experts_route_to_autograd_under_grad():
 
     with pytest.raises(RuntimeError, match="CUDA/HIP tensor"):
         hip_experts_forward(Experts(), x, idx, w)
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_router_backward_matches_autograd(bias):
+    """q38.hip.autograd.router_backward (the differentiable router's backward, run after the HIP
+    route kernel) against torch autograd of the reference router's op sequence (modeling:805-812:
+    linear, softmax in fp32, top-k, renormalisation), in float64 on the same logits and indices,
+    with gradients on both outputs (the routing weights and the logits, as the load-balancing loss
+    reads them)."""
+    from q38.hip import autograd
+    g = torch.Generator().manual_seed(5)
+    T, h, E, k = 37, 48, 16, 4
+    x = torch.randn(T, h, generator=g, dtype=torch.float64, requires_grad=True)
+    wr = (torch.randn(E, h, generator=g, dtype=torch.float64) * 0.2).requires_grad_(True)
+    b = torch.randn(E, generator=g, dtype=torch.float64) * 0.3 if bias else None
+    logits = torch.nn.functional.linear(x, wr)
+    z = logits if b is None else logits + b
+    probs = torch.softmax(z, dim=-1)
+    top, idx = torch.topk(probs, k, dim=-1)
+    w = top / top.sum(dim=-1, keepdim=True)
+    d_w = torch.randn(T, k, generator=g, dtype=torch.float64)
+    d_logits = torch.randn(T, E, generator=g, dtype=torch.float64) * 0.1
+    (w * d_w).sum().add_((logits * d_logits).sum()).backward()
+    dx, dwr = autograd.router_backward(x.detach(), wr.detach(), logits.detach(), idx, b, d_logits, d_w)
+    # router_backward works in float32 internally: compare at float32 accuracy
+    assert torch.allclose(dx, x.grad, rtol=1e-5, atol=1e-6)
+    assert torch.allclose(dwr, wr.grad, rtol=1e-5, atol=1e-6)
+    # each output's gradient alone
+    for dl, dww in ((None, d_w), (d_logits, None)):
+        x.grad = wr.grad = None
+        lo = torch.nn.functional.linear(x, wr)
+        zz = lo if b is None else lo + b
+        t2, _ = torch.topk(torch.softmax(zz, -1), k, -1)
+        terms = []
+        if dww is not None:
+            terms.append((t2 / t2.sum(-1, keepdim=True) * dww).sum())
+        if dl is not None:
+            terms.append((lo * dl).sum())
+        sum(terms).backward()
+        dx1, dwr1 = autograd.router_backward(x.detach(), wr.detach(), lo.detach(), idx, b, dl, dww)
+        assert torch.allclose(dx1, x.grad, rtol=1e-5, atol=1e-6) and torch.allclose(dwr1, wr.grad, rtol=1e-5, atol=1e-6)

@@ -331,3 +331,68 @@ def test_pair_dots_rows_fused(gpu, name, T, drop):
     filled = int(counts.sum())
     assert torch.equal(dw_alone, dw_fused)
     assert torch.equal(d_raw[:filled], rows[:filled])
+
+
+@pytest.mark.parametrize("main", [1.0, 0.0], ids=["main+aux", "aux-only"])
+def test_dropin_block_trains_under_autocast(gpu, main):
+    """The drop-in Qwen3_8MoeSparseMoeBlock trained as the reference trainer runs it: fp32
+    parameters under bf16 autocast, a forward hook on ``gate`` recording the router logits
+    (q38/train.py:228-233) and the load-balancing loss over them (modeling:1289-1355) added to the
+    main loss (main = 0: the router's gradient from the auxiliary loss alone). Every gradient, of x
+    and of the eight parameters, within relative L2 2.5e-2 of fp32 CPU autograd of the reference's
+    op sequence (modeling:805-835) and loss on the same selections (the GPU's top-k sets, so that
+    bf16 near-ties do not pick other experts)."""
+    from q38 import prefill as P
+    from q38 import workloads
+    from q38.models.qwen3_8_moe import Qwen3_8MoeSparseMoeBlock, new_config
+    F = torch.nn.functional
+    wl = workloads.get("c2")
+    T, h, E, k = 2048, wl.hidden, wl.experts, wl.topk
+    x, params, _ = workloads.make(wl, tokens=T)
+    x = x.float()
+    params = {n: t.float() for n, t in params.items()}
+    dout = torch.randn(T, h, generator=torch.Generator().manual_seed(21)) * 0.05
+    cfg = new_config(hidden_size=h, num_experts=E, num_experts_per_tok=k, moe_intermediate_size=wl.inter,
+                     shared_expert_intermediate_size=wl.shared_inter)
+    block = Qwen3_8MoeSparseMoeBlock(cfg)
+    block.load_state_dict(params, strict=True)
+    block = block.to(gpu)
+    seen = []
+    block.gate.register_forward_hook(lambda m, a, o: seen.append(o))
+    xg = x.to(gpu).requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = block(xg.view(1, T, h))
+        aux = P.load_balancing_loss((seen[0][0],), E, k)
+    loss = main * (out.view(T, h).float() * dout.to(gpu)).sum() + aux
+    loss.backward()
+    torch.cuda.synchronize()
+    assert len(seen) == 1 and seen[0][0].dtype == torch.bfloat16 and out.dtype == torch.float32
+    idx = seen[0][2].cpu()
+
+    leaves = {n: t.clone().requires_grad_(True) for n, t in params.items()}
+    xc = x.clone().requires_grad_(True)
+    logits = F.linear(xc, leaves["gate.weight"])
+    probs = torch.softmax(logits, dim=-1, dtype=torch.float)
+    top = probs.gather(1, idx)
+    top = top / top.sum(dim=-1, keepdim=True)
+    routed = orc.experts_eager(xc, idx, top, leaves["experts.gate_up_proj"], leaves["experts.down_proj"])
+    sh = F.linear(F.silu(F.linear(xc, leaves["shared_expert.gate_proj.weight"]))
+                  * F.linear(xc, leaves["shared_expert.up_proj.weight"]), leaves["shared_expert.down_proj.weight"])
+    ref = routed + torch.sigmoid(F.linear(xc, leaves["shared_expert_gate.weight"])) * sh
+    # The loss's expert counts (its own top-k of the softmax, not differentiated) as the GPU run
+    # chose them: a few bf16 near-ties moving a count shift the small per-expert deviations the
+    # auxiliary gradient is made of.
+    chosen = torch.topk(torch.softmax(seen[0][0].detach().float(), dim=-1), k, dim=-1).indices
+    counts = torch.bincount(chosen.reshape(-1), minlength=E).float().cpu()
+    ref_aux = E * ((counts / T) * (torch.softmax(logits, dim=-1).sum(0) / T)).sum()
+    ref_loss = main * (ref * dout).sum() + ref_aux
+    ref_loss.backward()
+    assert abs(float(aux.detach()) - float(ref_aux.detach())) < 1e-3
+    pairs = [("x", xg.grad, xc.grad)] + [(n, p.grad, leaves[n].grad) for n, p in block.named_parameters()]
+    if main == 0.0:
+        pairs = [q for q in pairs if q[0] in ("x", "gate.weight")]
+    for n, got, want in pairs:
+        assert got is not None and got.dtype == torch.float32, n
+        r = _rel(got, want)
+        print(f"{n}: rel L2 {r:.2e}")
+        assert r <= REL, f"{n}: rel L2 {r:.3e}"
