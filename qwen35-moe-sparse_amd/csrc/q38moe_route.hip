@@ -591,40 +591,91 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
       const int kc = min(ROUTE_KCHUNK, h - k0);  // multiple of 64
       __syncthreads();                            // previous chunk fully consumed
       const bool full = kc == ROUTE_KCHUNK;
-      // Router weights -> LDS by asynchronous copies, issued before the x loads so that they are
-      // not queued behind them: one wave instruction fills 64 slots (1 KiB) of a row; lane l takes
-      // the 16-byte chunk that the swizzle puts in slot l. A chunk narrower than 512 columns leaves
-      // slots past kc/8 unused; their lanes copy chunk 0. The loop is wave-uniform (scalar
-      // control), and each block starts at a different row so that the blocks, which all copy the
-      // same weights at once, spread over the L2 channels.
+      // Router weights -> LDS in 1 KiB row segments: segment q = (row n, half part) fills slots
+      // n * 128 + part * 64 + lane, lane l holding the 16-byte chunk the swizzle puts in slot l. A
+      // chunk narrower than 512 columns leaves slots past kc/8 unused; their lanes copy chunk 0.
+      // Each block starts at a different segment so that the blocks, which all copy the same
+      // weights at once, spread over the L2 channels.
       const int halves = (kc + 511) / 512;        // 1 KiB row segments in this chunk: 1 or 2
       const int nseg = nrows_w * halves;
       const int seg0 = (int)((blockIdx.x * 37u) % (unsigned)nseg);
-      for (int q = wave_u; q < nseg; q += ROUTE_THREADS / 64) {
+      auto seg_src = [&](int q, int& slot) -> const uint16_t* {
         int qq = q + seg0;
         qq = qq >= nseg ? qq - nseg : qq;
         const int n = halves == 2 ? qq >> 1 : qq, part = halves == 2 ? qq & 1 : 0;
         const uint16_t* src = n < 64 ? (n < E ? wr + (int64_t)n * h : nullptr) : wsg;
-        if (src != nullptr) {
-          const int c = (part * 64 + lane) ^ (n & 15);
-          load_lds16(src + k0 + (c < kc / 8 ? c : 0) * 8, &s_w[n * (ROUTE_KCHUNK / 8) + part * 64]);
-        }
-      }
-      // This wave's x rows for a full chunk: all loads in flight before the MFMAs.
-      u32x4_t a[32];
-      if (full && mma) {
+        const int c = (part * 64 + lane) ^ (n & 15);
+        slot = n * (ROUTE_KCHUNK / 8) + part * 64 + lane;
+        return src == nullptr ? nullptr : src + k0 + (c < kc / 8 ? c : 0) * 8;
+      };
+      u32x4_t a[32];  // this wave's x rows for a full chunk
+      if constexpr (!ALIAS) {
+        // 64-token blocks: waves 0-3 multiply, waves 4-7 copy the weights (asynchronous copies,
+        // complete at their vmcnt(0)). The multiplying waves start their x loads at once and do not
+        // wait for them at the barrier: the MFMAs below take the rows as they arrive. (With the
+        // copies in other waves, the compiler's wait placement sees no LDS copy in flight in the
+        // multiplying waves and puts no vmcnt(0) before their LDS reads.)
+        if (!mma) {
+          for (int q = wave_u - TOK / 16; q < nseg; q += ROUTE_THREADS / 64 - TOK / 16) {
+            int slot;
+            const uint16_t* src = seg_src(q, slot);
+            if (src != nullptr) load_lds16(src, &s_w[slot - lane]);
+          }
+          wait_vmcnt0();
+        } else if (full) {
 #pragma unroll
-        for (int s = 0; s < 32; ++s) a[s] = ld16(xa + k0 + s * 32);
+          for (int s = 0; s < 32; ++s) a[s] = ld16(xa + k0 + s * 32);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      } else {
+        // 128-token blocks: every wave multiplies and copies weight segments asynchronously, issued
+        // before its x loads so that they are not queued behind them.
+        for (int q = wave_u; q < nseg; q += ROUTE_THREADS / 64) {
+          int slot;
+          const uint16_t* src = seg_src(q, slot);
+          if (src != nullptr) load_lds16(src, &s_w[slot - lane]);
+        }
+        if (full && mma) {
+#pragma unroll
+          for (int s = 0; s < 32; ++s) a[s] = ld16(xa + k0 + s * 32);
+        }
+        wait_vmcnt0();
+        __syncthreads();
       }
-      wait_vmcnt0();
-      __syncthreads();
       if (full && mma) {
+        // Weight fragments of step s + 1 are read from LDS while step s multiplies. Fragment (j, s)
+        // of this lane is wr_slot(16 j + lr, 4 s + lq): with s = 4 m + r its byte offset is
+        // 32768 j + 256 m + (2048 lr + 64 (r ^ (lr >> 2)) + 16 (lq ^ (lr & 3))), so four per-lane
+        // bases and immediate offsets cover all 32 steps (the gate row 64 is the same in every
+        // lane: 131072 + 64 s + 16 lq).
+        const uint8_t* const sb = reinterpret_cast<const uint8_t*>(s_w);
+        const uint32_t lr = lane & 15, lq = lane >> 4;
+        // (The empty asm keeps each base in one register: folded into the constants, every step's
+        // address would be a register of its own.)
+        const uint8_t* fb[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          uint32_t off = 2048u * lr + 64u * ((uint32_t)r ^ (lr >> 2)) + 16u * (lq ^ (lr & 3u));
+          asm volatile("" : "+v"(off));
+          fb[r] = sb + off;
+        }
+        uint32_t goff = (uint32_t)wr_slot(64, 0) * 16u + 16u * lq;
+        asm volatile("" : "+v"(goff));
+        const uint8_t* const gb = sb + goff;
+        u32x4_t bf[2][5];
+        auto bload = [&](int s, u32x4_t(&d)[5]) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) d[j] = *reinterpret_cast<const u32x4_t*>(fb[s & 3] + (32768 * j + 256 * (s >> 2)));
+          d[4] = *reinterpret_cast<const u32x4_t*>(gb + 64 * s);
+        };
+        bload(0, bf[0]);
 #pragma unroll
         for (int s = 0; s < 32; ++s) {
-          const int c = 4 * s + (lane >> 4);
+          if (s + 1 < 32) bload(s + 1, bf[(s + 1) & 1]);
+          __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of this step's MFMAs
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[j] = mfma16x16x32(a[s], s_w[wr_slot(16 * j + (lane & 15), c)], acc[j]);
-          acc[4] = mfma16x16x32(a[s], s_w[wr_slot(64, c)], acc[4]);
+          for (int j = 0; j < 5; ++j) acc[j] = mfma16x16x32(a[s], bf[s & 1][j], acc[j]);
+          __builtin_amdgcn_sched_barrier(0);
         }
       } else if (mma) {
         // Narrow last chunk (h not a multiple of the chunk): one 32-wide slice at a time.
