@@ -610,22 +610,19 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
       };
       u32x4_t a[32];  // this wave's x rows for a full chunk
       if constexpr (!ALIAS) {
-        // 64-token blocks: waves 0-3 multiply, waves 4-7 copy the weights (asynchronous copies,
-        // complete at their vmcnt(0)). The multiplying waves start their x loads at once and do not
-        // wait for them at the barrier: the MFMAs below take the rows as they arrive. (With the
-        // copies in other waves, the compiler's wait placement sees no LDS copy in flight in the
-        // multiplying waves and puts no vmcnt(0) before their LDS reads.)
-        if (!mma) {
-          for (int q = wave_u - TOK / 16; q < nseg; q += ROUTE_THREADS / 64 - TOK / 16) {
-            int slot;
-            const uint16_t* src = seg_src(q, slot);
-            if (src != nullptr) load_lds16(src, &s_w[slot - lane]);
-          }
-          wait_vmcnt0();
-        } else if (full) {
+        // 64-token blocks: waves 0-3 multiply. Their x loads go first; then all eight waves copy
+        // the weights (asynchronous copies; spread over every wave they arrive sooner than from
+        // four). The multiply starts once both are in.
+        if (mma && full) {
 #pragma unroll
           for (int s = 0; s < 32; ++s) a[s] = ld16(xa + k0 + s * 32);
         }
+        for (int q = wave_u; q < nseg; q += ROUTE_THREADS / 64) {
+          int slot;
+          const uint16_t* src = seg_src(q, slot);
+          if (src != nullptr) load_lds16(src, &s_w[slot - lane]);
+        }
+        wait_vmcnt0();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       } else {
         // 128-token blocks: every wave multiplies and copies weight segments asynchronously, issued
