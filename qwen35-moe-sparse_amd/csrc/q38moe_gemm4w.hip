@@ -24,6 +24,11 @@
 // 16 (4 f + w) ..), so a unit of at most 128 rows leaves every wave two fragments instead of idling
 // whole SIMDs; such units run the body specialised for two fragments (half the MFMAs).
 //
+// The last, partial round of units: with at most half as many units left as workgroups, each of them
+// runs as two column halves (64 H columns: 64 gate + 64 up weight rows, 8 fragments per K step) on
+// two workgroups, so the round ends in about half the time and no workgroup idles through it. Every
+// output element keeps its products and K order, so the bits do not change.
+//
 // The MFMAs are inline asm (see g4_mfma); every global and LDS access is an ordinary
 // compiler-visible load or store, so the compiler's own waits track all of them, and the only
 // hand-written synchronisation is the per-slice barrier.
@@ -88,6 +93,7 @@ __device__ __forceinline__ u32x4_t g4_bload(__amdgpu_buffer_rsrc_t r, uint32_t v
 struct G4Unit {
   int4 ti;
   int nt;                 // output-column tile
+  int half;               // -1: all 128 columns of the tile; 0, 1: that 64-column half
   int rot;                // K-slice rotation (64-K slices)
   const uint8_t* wb;      // wave-uniform: the first of the 64 weight rows this wave stages (all K)
   uint32_t xo[4];         // byte offset of this lane's activation row of fragment f (+ 16 (lane / 16))
@@ -97,18 +103,34 @@ struct G4Unit {
 // rotated per expert (slice j of a unit of expert e is K slice (j + e) mod nk; shared-expert units
 // rotate by row tile): the units of an expert run together on one XCD and meet in its L2 on the
 // same rows at the same time, while different experts spread over the L2 channels.
-__device__ __forceinline__ void g4_unit_head(const G4Params& p, int L, int nk, int wave, G4Unit& u) {
-  u.ti = g4_tile_entry(p, L / p.ntiles_n);
-  u.nt = L % p.ntiles_n;
-  u.rot = (u.ti.x < p.E ? u.ti.x : L / p.ntiles_n) % nk;
+// Work item L: unit L below U0; past it (split > 0), column half (L - U0) % 2 of unit U0 + (L - U0) / 2.
+__device__ __forceinline__ void g4_unit_head(const G4Params& p, int L, int nk, int wave, int U0, bool split,
+                                             G4Unit& u) {
+  int Lu = L;
+  u.half = -1;
+  if (split && L >= U0) {
+    Lu = U0 + ((L - U0) >> 1);
+    u.half = (L - U0) & 1;
+  }
+  u.ti = g4_tile_entry(p, Lu / p.ntiles_n);
+  u.nt = Lu % p.ntiles_n;
+  u.rot = (u.ti.x < p.E ? u.ti.x : Lu / p.ntiles_n) % nk;
   const bool shared_grp = u.ti.x >= p.E;
   const int64_t K = p.K;
   // Staging load i of wave w carries weight rows 64 w + 8 i + lane / 8 of the unit: rows [0, 128)
-  // are the gate rows of H columns nt * 128 + [0, 128), rows [128, 256) the matching up rows.
+  // are the gate rows of H columns nt * 128 + [0, 128), rows [128, 256) the matching up rows. A
+  // column half has 128 weight rows, wave w staging rows 32 w + 8 i + lane / 8 (i < 4): rows
+  // [0, 64) the gate rows of H columns nt * 128 + 64 half + [0, 64), rows [64, 128) the up rows.
   const bool up = wave >= 2;
   const uint16_t* base = shared_grp ? (up ? p.Ws_b : p.Ws_a)
                                     : p.W + (int64_t)u.ti.x * 2 * p.N * K + (up ? (int64_t)p.N * K : 0);
-  u.wb = reinterpret_cast<const uint8_t*>(base + (int64_t)(u.nt * 128 + 64 * (wave & 1)) * K);
+  const int row0 = u.half < 0 ? u.nt * 128 + 64 * (wave & 1) : u.nt * 128 + 64 * u.half + 32 * (wave & 1);
+  u.wb = reinterpret_cast<const uint8_t*>(base + (int64_t)row0 * K);
+}
+
+// Row tile of work item L (the mapping of g4_unit_head).
+__device__ __forceinline__ int g4_tile_index(const G4Params& p, int L, int U0, bool split) {
+  return (split && L >= U0 ? U0 + ((L - U0) >> 1) : L) / p.ntiles_n;
 }
 
 // Source row index of this lane's fragment-f activation row: the sorted pair of a routed row (a
@@ -176,8 +198,14 @@ __device__ __forceinline__ void g4_barrier() { asm volatile("s_waitcnt lgkmcnt(8
 __device__ __forceinline__ void g4_mfma(f32x4_t& acc, const u32x4_t& a, const u32x4_t& b) {
   asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
-__device__ __forceinline__ void g4_mfma_first(f32x4_t& acc, const u32x4_t& a, const u32x4_t& b) {
-  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(acc) : "v"(a), "v"(b));
+// The same with two wait states ahead: where AGPRs are free (a unit's first step, before its
+// accumulators exist; the column-half units, which use half of them) the compiler parks operand
+// VGPRs there and copies them back (v_accvgpr_read, a VALU write) right before their MFMA.
+__device__ __forceinline__ void g4_mfma_nop(f32x4_t& acc, const u32x4_t& a, const u32x4_t& b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void g4_mfma_first_nop(f32x4_t& acc, const u32x4_t& a, const u32x4_t& b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(acc) : "v"(a), "v"(b));
 }
 // Wait states between the last MFMA and VALU reads of its result (ample for the 8-pass XDL op).
 __device__ __forceinline__ void g4_mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
@@ -194,34 +222,47 @@ __device__ __forceinline__ int g4_lane() {
 // through the wave's staging area (rows padded by 16 bytes, so the 16 rows a write instruction spans
 // start 4 banks apart: conflict-free writes and reads, and per-block offsets that are immediates) to
 // whole-line stores (4 rows x 256 B per instruction).
-template <int NF>
-__device__ __forceinline__ void g4_epilogue_frag(const G4Params& p, const f32x4_t (&acc)[16][NF], const G4Unit& u,
+// NW: weight fragments per K step (16; 8 for a column half: 64 columns, 2 rows x 128 B per store).
+template <int NF, int NW>
+__device__ __forceinline__ void g4_epilogue_frag(const G4Params& p, const f32x4_t (&acc)[NW][NF], const G4Unit& u,
                                                  int f, int wave, uint8_t* stage) {
+  constexpr int NG = NW / 2;  // gate fragments (the up fragments follow)
   const int lane = g4_lane();
   const int lr = lane & 15, lq = lane >> 4;
   const int rbase = 16 * (4 * f + wave);
   uint8_t* const wr = stage + lr * G4_PITCH + 8 * lq;
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
+  for (int t = 0; t < NG; ++t) {
     uint32_t v[2];
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
       // Reference rounding (inference.py:90-96): bf16 gate and up, bf16 silu(gate), bf16 product.
       float g0, g1, u0, u1, s0, s1;
       unpack_bf16x2(pack_bf16x2(acc[t][f][2 * h2], acc[t][f][2 * h2 + 1]), g0, g1);
-      unpack_bf16x2(pack_bf16x2(acc[t + 8][f][2 * h2], acc[t + 8][f][2 * h2 + 1]), u0, u1);
+      unpack_bf16x2(pack_bf16x2(acc[t + NG][f][2 * h2], acc[t + NG][f][2 * h2 + 1]), u0, u1);
       unpack_bf16x2(pack_bf16x2(g0 * __builtin_amdgcn_rcpf(1.0f + __expf(-g0)),
                                 g1 * __builtin_amdgcn_rcpf(1.0f + __expf(-g1))), s0, s1);
       v[h2] = pack_bf16x2(s0 * u0, s1 * u1);
     }
     *reinterpret_cast<uint2*>(wr + 32 * t) = make_uint2(v[0], v[1]);
   }
+  if constexpr (NW == 16) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int rr = 4 * j + lq;
-    const u32x4_t d = *reinterpret_cast<const u32x4_t*>(stage + rr * G4_PITCH + 16 * lr);
-    const int r = rbase + rr;
-    if (r < u.ti.z) st16(p.C + (int64_t)(u.ti.y + r) * p.N + u.nt * 128 + 8 * lr, d);
+    for (int j = 0; j < 4; ++j) {
+      const int rr = 4 * j + lq;
+      const u32x4_t d = *reinterpret_cast<const u32x4_t*>(stage + rr * G4_PITCH + 16 * lr);
+      const int r = rbase + rr;
+      if (r < u.ti.z) st16(p.C + (int64_t)(u.ti.y + r) * p.N + u.nt * 128 + 8 * lr, d);
+    }
+  } else {
+    const int l8 = lane & 7;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int rr = 8 * j + (lane >> 3);
+      const u32x4_t d = *reinterpret_cast<const u32x4_t*>(stage + rr * G4_PITCH + 16 * l8);
+      const int r = rbase + rr;
+      if (r < u.ti.z) st16(p.C + (int64_t)(u.ti.y + r) * p.N + u.nt * 128 + 64 * u.half + 8 * l8, d);
+    }
   }
 }
 
@@ -231,7 +272,8 @@ struct G4State {
   uint8_t* stage;         // this wave's staging area
   uint32_t rd_off[2];     // this lane's fragment-read offset within a slot, for step half s = 0, 1
   uint32_t wl[2];         // this lane's staging-load source offsets (even, odd loads)
-  uint32_t ws_off;        // this lane's staging-store offset within a slot (wave block + 16 lane)
+  uint32_t ws_lane;       // this lane's staging-store offset within the wave's block (16 lane)
+  int wave;
   __amdgpu_buffer_rsrc_t xrs;  // the activation rows A
   int gslice;             // slices started so far (ring slot of the slice being multiplied = gslice % 4)
   int nk;                 // 64-K slices per unit
@@ -251,9 +293,10 @@ __device__ __forceinline__ const uint8_t* g4_frag_base(const G4State& st, int sl
 __device__ __forceinline__ u32x4_t g4_frag(const uint8_t* base, int t) {
   return *reinterpret_cast<const u32x4_t*>(base + 2048 * t);
 }
-// The same for the staging stores of ring slot `slot`.
-__device__ __forceinline__ uint8_t* g4_store_base(const G4State& st, int slot) {
-  uint32_t off = (uint32_t)(slot * G4_SLOT) + st.ws_off;
+// The same for the staging stores of ring slot `slot`, for a unit (half: a column half, whose waves
+// stage 32 rows each).
+__device__ __forceinline__ uint8_t* g4_store_base(const G4State& st, int slot, bool half) {
+  uint32_t off = (uint32_t)(slot * G4_SLOT) + (half ? 4096u : 8192u) * (uint32_t)st.wave + st.ws_lane;
   asm volatile("" : "+v"(off));
   return st.ring + off;
 }
@@ -267,25 +310,32 @@ __device__ __forceinline__ uint8_t* g4_store_base(const G4State& st, int slot) {
 // (the slice barriers), and a burst of them from each would queue at the CU's texture addresser
 // while the waves waiting to issue leave their matrix pipes idle. FIRST: the unit's first step,
 // whose MFMAs add to zero.
-template <int NF, int XNF, int XB, int XL, bool RNEXT, bool WS, bool FIRST = false>
-__device__ __forceinline__ void g4_step(f32x4_t (&acc)[16][NF], u32x4_t (&wf)[G4_WIN], u32x4_t (&xb)[G4_XBUF][4],
+// NW (16, or 8 for a column half) groups; the activation loads then follow groups 1, 3, 5, 7. RT: the
+// staged slices may belong to a unit of the other kind (the next unit's first slices, at a unit's
+// end), so the counts of staging stores (nst) and loads (nld), 8 for a whole unit and 4 for a column
+// half, are taken at run time.
+template <int NF, int XNF, int XB, int XL, bool RNEXT, bool WS, bool FIRST, int NW, bool RT>
+__device__ __forceinline__ void g4_step(f32x4_t (&acc)[NW][NF], u32x4_t (&wf)[G4_WIN], u32x4_t (&xb)[G4_XBUF][4],
                                         u32x4_t (&wst)[8], const G4State& st, const uint32_t (&xo)[4], uint32_t kb,
                                         const uint8_t* rcur, const uint8_t* rnext, uint8_t* wdst, const G4Unit& wu,
-                                        int wj) {
+                                        int wj, int nst, int nld) {
+  constexpr int XS = NW / 4;
 #pragma unroll
-  for (int t = 0; t < 16; ++t) {
+  for (int t = 0; t < NW; ++t) {
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-      if (FIRST) g4_mfma_first(acc[t][f], wf[t % G4_WIN], xb[XB][f]);
+      // A unit's first step (its accumulators' AGPRs still free) and the column halves: see g4_mfma_nop.
+      if (FIRST) g4_mfma_first_nop(acc[t][f], wf[t % G4_WIN], xb[XB][f]);
+      else if constexpr (NW == 8) g4_mfma_nop(acc[t][f], wf[t % G4_WIN], xb[XB][f]);
       else g4_mfma(acc[t][f], wf[t % G4_WIN], xb[XB][f]);
     }
-    if (t + G4_WIN < 16) wf[t % G4_WIN] = g4_frag(rcur, t + G4_WIN);
-    else if (RNEXT) wf[t % G4_WIN] = g4_frag(rnext, t + G4_WIN - 16);
-    if ((t & 3) == 1 && (t >> 2) < XNF) xb[XL][t >> 2] = g4_bload(st.xrs, xo[t >> 2], kb);
+    if (t + G4_WIN < NW) wf[t % G4_WIN] = g4_frag(rcur, t + G4_WIN);
+    else if (RNEXT) wf[t % G4_WIN] = g4_frag(rnext, t + G4_WIN - NW);
+    if (t % XS == 1 && t / XS < XNF) xb[XL][t / XS] = g4_bload(st.xrs, xo[t / XS], kb);
     if (WS && (t & 1) == 0) {
       const int i = t >> 1;
-      *reinterpret_cast<u32x4_t*>(wdst + 1024 * i) = wst[i];
-      wst[i] = g4_wload(wu, wj, st.nk, st.K2, st.wl, i);
+      if (!RT || i < nst) *reinterpret_cast<u32x4_t*>(wdst + 1024 * i) = wst[i];
+      if (!RT || i < nld) wst[i] = g4_wload(wu, wj, st.nk, st.K2, st.wl, i);
     }
   }
 }
@@ -298,15 +348,19 @@ __device__ __forceinline__ void g4_step(f32x4_t (&acc)[16][NF], u32x4_t (&wf)[G4
 // to the next unit (its steps 0-2, all four fragments: its row count may differ). Slice j's first
 // step stores slice j + 2 into the slot slice j - 2 used and loads slice j + 3 (this unit's, or the
 // next unit's past the end).
-template <int NF>
+template <int NF, int NW>
 __device__ __forceinline__ void g4_unit(const G4Params& p, G4State& st, u32x4_t (&wf)[G4_WIN],
                                         u32x4_t (&xb)[G4_XBUF][4], u32x4_t (&wst)[8], const G4Unit& cur,
                                         const G4Unit& nxt, int wave) {
   // The unit's accumulators (AGPRs). Every value they take is an MFMA result (the first K step adds
   // to a zero operand): a zero initialisation, or values carried from unit to unit, would make the
   // compiler hold them in VGPRs across the K loop and copy them into AGPRs for every MFMA.
-  f32x4_t acc[16][NF];
+  f32x4_t acc[NW][NF];
   const int nk = st.nk, S = 2 * nk;
+  // Staging counts and layout of the next unit (its first slices are staged during this unit's last
+  // iteration).
+  const bool nxt_half = nxt.half >= 0;
+  const int nxt_n = nxt_half ? 4 : 8;
   // Step K_ (0..7) of the iteration starting at slice J: multiplies buffer K_ % 4, reads the next
   // step's fragments (none after the unit's last step), loads activation step q + 3 into buffer
   // (K_ + 3) % 4 (this unit's while q + 3 < S, else the next unit's step q + 3 - S).
@@ -315,20 +369,21 @@ __device__ __forceinline__ void g4_unit(const G4Params& p, G4State& st, u32x4_t 
     const int j_ = (J) + (K_) / 2, q_ = 2 * j_ + ((K_) & 1);                                            \
     const uint8_t* rc_ = g4_frag_base(st, g4_slot(st.gslice), (K_) & 1);                                \
     const uint8_t* rn_ = g4_frag_base(st, g4_slot(st.gslice + ((K_) & 1)), ((K_) & 1) ^ 1);             \
+    const bool sc_ = j_ + 2 < nk, wc_ = j_ + 3 < nk; /* slices j + 2, j + 3 this unit's */              \
     uint8_t* ws_ = nullptr;                                                                             \
     if (((K_) & 1) == 0) {                                                                              \
       g4_barrier();                                                                                     \
-      ws_ = g4_store_base(st, g4_slot(st.gslice + 2));                                                  \
+      ws_ = g4_store_base(st, g4_slot(st.gslice + 2), (LAST_) && !sc_ ? nxt_half : NW == 8);            \
     }                                                                                                   \
-    const bool wc_ = j_ + 3 < nk;                                                                       \
+    const int nst_ = (LAST_) && !sc_ ? nxt_n : NW / 2, nld_ = (LAST_) && !wc_ ? nxt_n : NW / 2;         \
     if (!(LAST_) || (K_) < 5)                                                                           \
-      g4_step<NF, NF, (K_) & 3, ((K_) + 3) & 3, true, ((K_) & 1) == 0, FIRST_ && (K_) == 0>(             \
+      g4_step<NF, NF, (K_) & 3, ((K_) + 3) & 3, true, ((K_) & 1) == 0, FIRST_ && (K_) == 0, NW, LAST_>(  \
           acc, wf, xb, wst, st, cur.xo, g4_kbyte(q_ + 3, cur.rot, nk), rc_, rn_, ws_, wc_ ? cur : nxt,  \
-          wc_ ? j_ + 3 : j_ + 3 - nk);                                                                  \
+          wc_ ? j_ + 3 : j_ + 3 - nk, nst_, nld_);                                                      \
     else                                                                                                \
-      g4_step<NF, 4, (K_) & 3, ((K_) + 3) & 3, (K_) != 7, ((K_) & 1) == 0>(                              \
+      g4_step<NF, 4, (K_) & 3, ((K_) + 3) & 3, (K_) != 7, ((K_) & 1) == 0, false, NW, LAST_>(            \
           acc, wf, xb, wst, st, nxt.xo, g4_kbyte(q_ + 3 - S, nxt.rot, nk), rc_, rn_, ws_, wc_ ? cur : nxt, \
-          wc_ ? j_ + 3 : j_ + 3 - nk);                                                                  \
+          wc_ ? j_ + 3 : j_ + 3 - nk, nst_, nld_);                                                      \
     if ((K_) & 1) ++st.gslice;                                                                          \
   } while (0)
 #define Q38_G4_ITER(J, FIRST_, LAST_)                                                                   \
@@ -347,7 +402,7 @@ __device__ __forceinline__ void g4_unit(const G4Params& p, G4State& st, u32x4_t 
   const int nf = g4_nfrag(cur.ti.z, wave);
 #pragma unroll
   for (int f = 0; f < NF; ++f)
-    if (f < nf) g4_epilogue_frag<NF>(p, acc, cur, f, wave, st.stage);
+    if (f < nf) g4_epilogue_frag<NF, NW>(p, acc, cur, f, wave, st.stage);
   // The next unit's first fragments (its slice 0 was published by the last barrier).
   {
     const uint8_t* const rb = g4_frag_base(st, g4_slot(st.gslice), 0);
@@ -365,7 +420,11 @@ __global__ __launch_bounds__(G4_THREADS, 1) void gemm4w_gate_up_kernel(G4Params 
   // Slots are spread over the 8 XCDs in contiguous runs (workgroup b runs on XCD b % 8), so units
   // that share an expert's weights or gathered rows run in one XCD's L2 at the same time.
   const int slot = (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
-  const int used = (p.tiles != nullptr ? load_uniform(p.ntiles_dev) : p.ntiles_host) * p.ntiles_n;
+  const int units = (p.tiles != nullptr ? load_uniform(p.ntiles_dev) : p.ntiles_host) * p.ntiles_n;
+  // The last, partial round (units U0 ..): split into column halves when they fit one round.
+  const int U0 = units - units % G;
+  const bool split = units > U0 && 2 * (units - U0) <= G;
+  const int used = split ? U0 + 2 * (units - U0) : units;  // work items
   if (slot >= used) return;
   int L = slot;
   const int nk = p.K >> 6;
@@ -377,7 +436,8 @@ __global__ __launch_bounds__(G4_THREADS, 1) void gemm4w_gate_up_kernel(G4Params 
   st.nk = nk;
   st.K2 = 2u * (uint32_t)p.K;
   st.xrs = g4_rsrc(p.A, p.a_bytes);
-  st.ws_off = 64u * 128u * (uint32_t)wave + 16u * (uint32_t)lane;
+  st.ws_lane = 16u * (uint32_t)lane;
+  st.wave = wave;
   {
     const uint32_t c0 = (uint32_t)((lane & 7) ^ (lane >> 4));
     st.wl[0] = (uint32_t)(lane >> 3) * st.K2 + 16u * c0;
@@ -394,30 +454,35 @@ __global__ __launch_bounds__(G4_THREADS, 1) void gemm4w_gate_up_kernel(G4Params 
   // and the row sources of the one after, loaded a unit ahead of their use.
   G4Unit cur, nxt;
   int src[4], src2[4];
-  g4_unit_head(p, L, nk, wave, cur);
+  g4_unit_head(p, L, nk, wave, U0, split, cur);
   g4_row_sources(p, cur.ti, wave, lane, src);
   g4_unit_rows(p, cur.ti, lane, src, cur);
   int Ln = L + G < used ? L + G : L;
-  g4_unit_head(p, Ln, nk, wave, nxt);
+  g4_unit_head(p, Ln, nk, wave, U0, split, nxt);
   g4_row_sources(p, nxt.ti, wave, lane, src);
   g4_unit_rows(p, nxt.ti, lane, src, nxt);
   int Lnn = Ln + G < used ? Ln + G : Ln;
-  int4 tinn = g4_tile_entry(p, Lnn / p.ntiles_n);
+  int4 tinn = g4_tile_entry(p, g4_tile_index(p, Lnn, U0, split));
   g4_row_sources(p, tinn, wave, lane, src2);
 
   // Prologue: slices 0 and 1 into the ring, slice 2 in wst; activation steps 0-2 in flight; step 0's
   // fragments.
   u32x4_t wf[G4_WIN], xb[G4_XBUF][4], wst[8];
+  const bool half0 = cur.half >= 0;
+  const int n0 = half0 ? 4 : 8;
 #pragma unroll
   for (int sl = 0; sl < 2; ++sl) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) wst[i] = g4_wload(cur, sl, nk, st.K2, st.wl, i);
-    uint8_t* const dst = g4_store_base(st, sl);
+    for (int i = 0; i < 8; ++i)
+      if (i < n0) wst[i] = g4_wload(cur, sl, nk, st.K2, st.wl, i);
+    uint8_t* const dst = g4_store_base(st, sl, half0);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4_t*>(dst + 1024 * i) = wst[i];
+    for (int i = 0; i < 8; ++i)
+      if (i < n0) *reinterpret_cast<u32x4_t*>(dst + 1024 * i) = wst[i];
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) wst[i] = g4_wload(cur, 2, nk, st.K2, st.wl, i);
+  for (int i = 0; i < 8; ++i)
+    if (i < n0) wst[i] = g4_wload(cur, 2, nk, st.K2, st.wl, i);
   const int nf0 = cur.ti.z > 128 ? 4 : 2;
 #pragma unroll
   for (int q = 0; q < G4_XBUF - 1; ++q)
@@ -430,16 +495,21 @@ __global__ __launch_bounds__(G4_THREADS, 1) void gemm4w_gate_up_kernel(G4Params 
 
   for (;;) {
     // Units of at most 128 rows: every wave has at most two active fragments.
-    if (cur.ti.z > 128) g4_unit<4>(p, st, wf, xb, wst, cur, nxt, wave);
-    else g4_unit<2>(p, st, wf, xb, wst, cur, nxt, wave);
+    if (cur.half < 0) {
+      if (cur.ti.z > 128) g4_unit<4, 16>(p, st, wf, xb, wst, cur, nxt, wave);
+      else g4_unit<2, 16>(p, st, wf, xb, wst, cur, nxt, wave);
+    } else {
+      if (cur.ti.z > 128) g4_unit<4, 8>(p, st, wf, xb, wst, cur, nxt, wave);
+      else g4_unit<2, 8>(p, st, wf, xb, wst, cur, nxt, wave);
+    }
     if (Ln == L) break;
     L = Ln;
     cur = nxt;
     Ln = Lnn;
-    g4_unit_head(p, Ln, nk, wave, nxt);
+    g4_unit_head(p, Ln, nk, wave, U0, split, nxt);
     g4_unit_rows(p, nxt.ti, lane, src2, nxt);
     Lnn = Ln + G < used ? Ln + G : Ln;
-    tinn = g4_tile_entry(p, Lnn / p.ntiles_n);
+    tinn = g4_tile_entry(p, g4_tile_index(p, Lnn, U0, split));
     g4_row_sources(p, tinn, wave, lane, src2);
   }
   // Retire the lookahead loads of the (absent) next unit before the wave ends.
