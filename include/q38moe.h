@@ -138,8 +138,10 @@ int32_t q38moe_gemm_block_m(void);
  * 256-row x 256-column tile per CU at a time) or Q38MOE_TILING_SMALL (16 weight rows x up to 64
  * rows per workgroup with K split over its waves, for few rows per expert). Both compute the same
  * roundings. Rule: small tiles when h and I are in {128, 256, 512, 1024, 2048} and
- * T*k + shared_rows <= 32 * (E + (shared_rows > 0)), i.e. at most 32 rows per group on average
- * (the measured crossover at the benchmark's shapes); the environment variable
+ * T*k + shared_rows <= R * (E + (shared_rows > 0)), i.e. at most R rows per group on average, with
+ * R = 32 * cbrt(2^18 / (h * I)) clamped to [8, 64] (32 at h = 1024, I = 256; 20.2 at h = 2048,
+ * I = 512: the measured crossovers at those shapes, the small tiles' cost per row growing with K);
+ * the environment variable
  * Q38MOE_GEMM_TILING=small|persistent, read once, overrides the row condition. The reference picks
  * its Triton tiles per shape by timing candidates on the first call (inference.py:133-155, 181-183);
  * this is the build's fixed, shape-keyed counterpart, and the query lets callers and tests see

@@ -3,6 +3,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <cmath>
 #include <cstring>
 #include <mutex>
 
@@ -76,17 +77,18 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 int64_t hist_blocks(int64_t T) { return (T + 63) / 64; }
 
-// GEMM tiling by shape. The persistent kernels (q38moe_gemm.hip) hand each CU whole (256-row tile,
-// 256 weight rows) units: with few rows per expert those units are few, each streams 512 KiB of one
-// expert's weights through one CU, and the kernel's time stays near 20-30 us (configuration 2's
-// shapes) from T = 1 up to T ~ 1000. The small-tile kernels (q38moe_gemm_small.hip: 16 weight rows
-// per workgroup, K split over its waves, every weight block in flight at once) take 6 us (gate/up)
-// and 4 us (down) at T = 1 but grow with the rows per expert, since each workgroup walks its rows in
-// 16-row blocks. Measured on MI355X at configuration 2's shapes (E = 64, k = 5, fused shared rows)
-// the two meet near T = 350, i.e. about 32 rows per group (E experts + the shared group): the rule
-// takes the small tiles up to that average. Q38MOE_GEMM_TILING=small|persistent (read once)
+// GEMM tiling by shape. The persistent kernels (q38moe_gemm.hip, q38moe_gemm4w.hip) hand each CU
+// whole (256-row tile, 256 weight rows) units: with few rows per expert those units are few, each
+// streams 512 KiB (h = 1024) of one expert's weights through one CU, and the kernels' time stays near
+// 20-30 us (configuration 2's shapes) from T = 1 up to T ~ 1000. The small-tile kernels
+// (q38moe_gemm_small.hip: 16 weight rows per workgroup, K split over its waves, every weight block in
+// flight at once) take 6 us (gate/up) and 4 us (down) at T = 1 but grow with the rows per expert,
+// since each workgroup walks its rows in 16-row blocks, and their cost per row grows with K. The
+// rule takes the small tiles up to R(h, I) rows per group on average (E experts + the shared group),
+// R = 32 (2^18 / (h I))^(1/3): the measured block crossovers (MI355X, both tilings forced) are about
+// 32-40 rows per group at h = 1024, I = 256 (configuration 2; R = 32) and about 23 at h = 2048,
+// I = 512 (configuration 4's shapes in bf16; R = 20). Q38MOE_GEMM_TILING=small|persistent (read once)
 // overrides the rule, to time one tiling against the other on the same shapes.
-constexpr int64_t kSmallRowsPerGroup = 32;
 int tiling_override() {
   static const int v = [] {
     const char* e = std::getenv("Q38MOE_GEMM_TILING");
@@ -97,10 +99,14 @@ int tiling_override() {
   }();
   return v;
 }
+double small_rows_per_group(int32_t h, int32_t I) {
+  const double r = 32.0 * std::cbrt(262144.0 / ((double)h * (double)I));
+  return r < 8.0 ? 8.0 : (r > 64.0 ? 64.0 : r);
+}
 bool small_tiles(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int64_t shared_rows) {
   if (!q38::small_gemm_supported(h) || !q38::small_gemm_supported(I)) return false;
   if (tiling_override() != 0) return tiling_override() == Q38MOE_TILING_SMALL;
-  return T * k + shared_rows <= kSmallRowsPerGroup * (E + (shared_rows > 0 ? 1 : 0));
+  return (double)(T * k + shared_rows) <= small_rows_per_group(h, I) * (double)(E + (shared_rows > 0 ? 1 : 0));
 }
 
 hipError_t gate_up_bf16(const uint16_t* x, const int32_t* perm, const int4* tiles, const int32_t* tile_count,

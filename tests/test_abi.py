@@ -49,8 +49,9 @@ def test_max_tiles_and_block_m():
 
 
 def test_gemm_tiling_rule():
-    """Small tiles up to 32 pair rows per group on average (E experts, plus the shared group when its
-    rows are fused), for K in {128, ..., 2048} only; monotone in T; the environment override
+    """Small tiles up to R pair rows per group on average (E experts, plus the shared group when its
+    rows are fused), R = 32 at h = 1024, I = 256 and 20.16 at h = 2048, I = 512 (32 (2^18 / (h I))^(1/3)),
+    for K in {128, ..., 2048} only; monotone in T; the environment override
     switches the row condition in a fresh process (the variable is read once)."""
     m = _lib()
     tiling = lambda T, sh, h=1024, E=64, k=5, I=256: m.lib.q38moe_gemm_tiling(T, h, E, k, I, sh)  # noqa: E731
@@ -63,6 +64,10 @@ def test_gemm_tiling_rule():
     assert tiling(1, 1, h=4096) == m.TILING_PERSISTENT
     assert tiling(1, 1, I=192) == m.TILING_PERSISTENT
     assert tiling(1, 1, h=2048, I=512) == m.TILING_SMALL
+    assert tiling(218, 218, h=2048, I=512) == m.TILING_SMALL        # 218 * 6 = 1308 <= 20.16 * 65
+    assert tiling(219, 219, h=2048, I=512) == m.TILING_PERSISTENT
+    assert tiling(550, 550, h=512, I=128) == m.TILING_SMALL         # R = 50.8 at h I = 2^16
+    assert tiling(551, 551, h=512, I=128) == m.TILING_PERSISTENT
     assert tiling(40, 40, E=8, k=2) == m.TILING_SMALL    # 120 <= 32 * 9
     assert tiling(100, 100, E=8, k=2) == m.TILING_PERSISTENT
     kinds = [tiling(T, T) for T in range(1, 5000, 7)]

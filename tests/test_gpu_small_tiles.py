@@ -104,6 +104,8 @@ def test_small_tile_stages(gpu, name, T, hot):
     ("c2", 40, {"hidden": 2048, "inter": 512, "shared_inter": 512}),  # K = 2048 (gate/up), 512 (down)
     ("c2", 25, {"experts": 1, "topk": 1, "hidden": 128, "inter": 128, "shared_inter": 128}),  # K = 128
     ("c2", 500, {"shared_inter": 128}),  # persistent, 128 units in one partial round: all column halves
+    ("c2", 218, {"hidden": 2048, "inter": 512, "shared_inter": 512}),  # last T on the small side at K = 2048
+    ("c2", 219, {"hidden": 2048, "inter": 512, "shared_inter": 512}),  # first persistent T there
 ])
 def test_small_tile_block(gpu, name, T, over):
     """Whole block through the tiling rule: routing bit-exact on the GPU's logits, output within the
@@ -112,7 +114,7 @@ def test_small_tile_block(gpu, name, T, over):
     wl, x, p, bias = _setup(name, T, **over)
     fused = wl.shared_inter == wl.inter
     kind = ops.gemm_tiling(T, wl.hidden, wl.experts, wl.topk, wl.inter, T if fused else 0)
-    assert kind == ("persistent" if T in (347, 500) else "small")
+    assert kind == ("persistent" if (T, over.get("hidden")) in ((347, None), (500, None), (219, 2048)) else "small")
     d = {n: t.to(gpu) for n, t in p.items()}
     out, logits, idx, w = ops.block_forward(x.to(gpu), *_block_args(d, wl), return_router=True,
                                             logit_bias=None if bias is None else bias.to(gpu))
