@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define Q38MOE_ABI_VERSION 12
+#define Q38MOE_ABI_VERSION 13
 
 #define Q38MOE_OK 0
 #define Q38MOE_EINVAL (-1)   /* bad shape, null pointer, misalignment, unsupported dtype */
@@ -149,6 +149,15 @@ int32_t q38moe_gemm_block_m(void);
 #define Q38MOE_TILING_PERSISTENT 1
 #define Q38MOE_TILING_SMALL 2
 int32_t q38moe_gemm_tiling(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int64_t shared_rows);
+
+/* The same for the e4m3 entry points (q38moe_gate_up_fp8, q38moe_down_fp8, q38moe_block_forward_fp8):
+ * small tiles (e4m3 16x16x128 MFMA, K split over the workgroup's waves, the same decomposition as
+ * the bf16 small tiles) when h and I are in {512, 1024, 2048} and T*k + shared_rows <= F * (E +
+ * (shared_rows > 0)), F = 1.25 R (R as above: 25.2 at h = 2048, I = 512, the measured crossover
+ * with the persistent fp8 kernel); Q38MOE_GEMM_TILING overrides it as for bf16. The fp32 entry points have
+ * one tiling (the persistent fp32 kernels) at every T. No counterpart in the reference (it has no
+ * fp8 path). */
+int32_t q38moe_gemm_tiling_fp8(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int64_t shared_rows);
 
 /*
  * Grouped gate/up GEMM with fused SwiGLU, R5-R6 (+R9 first half): replaces _gate_up_kernel

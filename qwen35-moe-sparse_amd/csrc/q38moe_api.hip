@@ -109,6 +109,39 @@ bool small_tiles(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int64_t 
   return (double)(T * k + shared_rows) <= small_rows_per_group(h, I) * (double)(E + (shared_rows > 0 ? 1 : 0));
 }
 
+// The e4m3 path takes its small tiles (q38moe_gemm_small.hip, gemm_small_fp8_kernel) under the same
+// kind of rule with F = 1.25 R rows per group: at configuration 4's shapes (h = 2048, I = 512) the
+// measured block crossover with the persistent fp8 kernel is near T = 280 (26 rows per group: block
+// 119.9 against 132.4 us at T = 200, 134.3 against 132.6 at T = 300; at T = 1, 72 against 95 us).
+double small_rows_per_group_fp8(int32_t h, int32_t I) { return 1.25 * small_rows_per_group(h, I); }
+bool small_tiles_fp8(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int64_t shared_rows) {
+  if (!q38::small_gemm_fp8_supported(h) || !q38::small_gemm_fp8_supported(I)) return false;
+  if (tiling_override() != 0) return tiling_override() == Q38MOE_TILING_SMALL;
+  return (double)(T * k + shared_rows) <= small_rows_per_group_fp8(h, I) * (double)(E + (shared_rows > 0 ? 1 : 0));
+}
+
+hipError_t gate_up_fp8_any(const uint8_t* xq, const float* a_scale, const int32_t* perm, const int4* tiles,
+                           const int32_t* tile_count, int max_tiles, int64_t T, int32_t k, int64_t shared_rows,
+                           const uint8_t* wq, const float* sw, const uint8_t* wq_sg, const float* s_sg,
+                           const uint8_t* wq_su, const float* s_su, uint16_t* H, int32_t I, int32_t h, int32_t E,
+                           hipStream_t st) {
+  if (small_tiles_fp8(T, h, E, k, I, shared_rows))
+    return q38::launch_gate_up_small_fp8(xq, a_scale, perm, tiles, tile_count, max_tiles, (int)(T * k),
+                                         (int)shared_rows, wq, sw, wq_sg, s_sg, wq_su, s_su, H, I, h, E, k, st);
+  return q38::launch_gate_up_fp8(xq, perm, tiles, tile_count, max_tiles, 0, (int)(T * k), a_scale, wq, sw, wq_sg, s_sg,
+                                 wq_su, s_su, H, I, h, E, k, st);
+}
+
+hipError_t down_fp8_any(const uint8_t* Hq, const float* a_scale, const int4* tiles, const int32_t* tile_count,
+                        int max_tiles, int64_t T, int32_t k, int64_t shared_rows, const uint8_t* wq, const float* sw,
+                        const uint8_t* wq_sd, const float* s_sd, uint16_t* Y, int32_t I, int32_t h, int32_t E,
+                        hipStream_t st) {
+  if (small_tiles_fp8(T, h, E, k, I, shared_rows))
+    return q38::launch_down_small_fp8(Hq, a_scale, tiles, tile_count, max_tiles, (int)(T * k), (int)shared_rows, wq,
+                                      sw, wq_sd, s_sd, Y, h, I, E, st);
+  return q38::launch_down_fp8(Hq, tiles, tile_count, max_tiles, 0, a_scale, wq, sw, wq_sd, s_sd, Y, h, I, E, st);
+}
+
 hipError_t gate_up_bf16(const uint16_t* x, const int32_t* perm, const int4* tiles, const int32_t* tile_count,
                         int max_tiles, int64_t T, int32_t k, int64_t shared_rows, const uint16_t* w_gate_up,
                         const uint16_t* sh_gate, const uint16_t* sh_up, uint16_t* H, int32_t I, int32_t h, int32_t E,
@@ -410,6 +443,10 @@ int32_t q38moe_gemm_block_m(void) { return q38::gemm_block_m(); }
 
 int32_t q38moe_gemm_tiling(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int64_t shared_rows) {
   return small_tiles(T, h, E, k, I, shared_rows) ? Q38MOE_TILING_SMALL : Q38MOE_TILING_PERSISTENT;
+}
+
+int32_t q38moe_gemm_tiling_fp8(int64_t T, int32_t h, int32_t E, int32_t k, int32_t I, int64_t shared_rows) {
+  return small_tiles_fp8(T, h, E, k, I, shared_rows) ? Q38MOE_TILING_SMALL : Q38MOE_TILING_PERSISTENT;
 }
 
 int q38moe_route(const void* x, const void* w_router, const void* w_shared_gate,
@@ -973,12 +1010,11 @@ int q38moe_gate_up_fp8(const void* xq, const float* row_scale, const void* wq_ga
     if (s_sh_gate == nullptr || s_sh_up == nullptr) return fail(Q38MOE_EINVAL, "shared-expert scales must not be NULL");
   }
   (void)hipGetLastError();
-  Q38_HIP(q38::launch_gate_up_fp8(static_cast<const uint8_t*>(xq), perm, reinterpret_cast<const int4*>(tiles),
-                                  tile_count, (int)max_tiles_impl(T, E, k, shared_rows), 0, (int)(T * k), row_scale,
-                                  static_cast<const uint8_t*>(wq_gate_up), s_gate_up,
-                                  static_cast<const uint8_t*>(wq_sh_gate), s_sh_gate,
-                                  static_cast<const uint8_t*>(wq_sh_up), s_sh_up, static_cast<uint16_t*>(H), I, h,
-                                  E, k, static_cast<hipStream_t>(stream)),
+  Q38_HIP(gate_up_fp8_any(static_cast<const uint8_t*>(xq), row_scale, perm, reinterpret_cast<const int4*>(tiles),
+                          tile_count, (int)max_tiles_impl(T, E, k, shared_rows), T, k, shared_rows,
+                          static_cast<const uint8_t*>(wq_gate_up), s_gate_up, static_cast<const uint8_t*>(wq_sh_gate),
+                          s_sh_gate, static_cast<const uint8_t*>(wq_sh_up), s_sh_up, static_cast<uint16_t*>(H), I, h,
+                          E, static_cast<hipStream_t>(stream)),
           "gate_up_fp8 launch");
   return Q38MOE_OK;
 }
@@ -1005,10 +1041,10 @@ int q38moe_down_fp8(const void* Hq, const float* row_scale, const void* wq_down,
     if (s_sh_down == nullptr) return fail(Q38MOE_EINVAL, "s_sh_down must not be NULL");
   }
   (void)hipGetLastError();
-  Q38_HIP(q38::launch_down_fp8(static_cast<const uint8_t*>(Hq), reinterpret_cast<const int4*>(tiles), tile_count,
-                               (int)max_tiles_impl(T, E, k, shared_rows), 0, row_scale,
-                               static_cast<const uint8_t*>(wq_down), s_down, static_cast<const uint8_t*>(wq_sh_down),
-                               s_sh_down, static_cast<uint16_t*>(Y), h, I, E, static_cast<hipStream_t>(stream)),
+  Q38_HIP(down_fp8_any(static_cast<const uint8_t*>(Hq), row_scale, reinterpret_cast<const int4*>(tiles), tile_count,
+                       (int)max_tiles_impl(T, E, k, shared_rows), T, k, shared_rows,
+                       static_cast<const uint8_t*>(wq_down), s_down, static_cast<const uint8_t*>(wq_sh_down), s_sh_down,
+                       static_cast<uint16_t*>(Y), I, h, E, static_cast<hipStream_t>(stream)),
           "down_fp8 launch");
   return Q38MOE_OK;
 }
@@ -1074,15 +1110,14 @@ int q38moe_block_forward_fp8(const void* x, const void* w_router, const void* wq
                               perm, inv, tiles, tile_count, q38::gemm_block_m(), (int)X.max_tiles, (int)T, T, E, k, st,
                               sx, sa),
           "permute launch");
-  Q38_HIP(q38::launch_gate_up_fp8(xq, perm, tiles, tile_count, (int)X.max_tiles, 0, (int)P, sa,
-                                  static_cast<const uint8_t*>(wq_gate_up), s_gate_up,
-                                  static_cast<const uint8_t*>(wq_sh_gate), s_sh_gate,
-                                  static_cast<const uint8_t*>(wq_sh_up), s_sh_up, H, I, h, E, k, st),
+  Q38_HIP(gate_up_fp8_any(xq, sa, perm, tiles, tile_count, (int)X.max_tiles, T, k, T,
+                          static_cast<const uint8_t*>(wq_gate_up), s_gate_up, static_cast<const uint8_t*>(wq_sh_gate),
+                          s_sh_gate, static_cast<const uint8_t*>(wq_sh_up), s_sh_up, H, I, h, E, st),
           "gate_up_fp8 launch");
   // SwiGLU rows to e4m3, one scale per row (routed pairs in sorted order, then the shared rows).
   Q38_HIP(q38::launch_quant_rows(H, Hq, sH, P + T, I, st), "quantize H launch");
-  Q38_HIP(q38::launch_down_fp8(Hq, tiles, tile_count, (int)X.max_tiles, 0, sH, static_cast<const uint8_t*>(wq_down),
-                               s_down, static_cast<const uint8_t*>(wq_sh_down), s_sh_down, Y, h, I, E, st),
+  Q38_HIP(down_fp8_any(Hq, sH, tiles, tile_count, (int)X.max_tiles, T, k, T, static_cast<const uint8_t*>(wq_down),
+                       s_down, static_cast<const uint8_t*>(wq_sh_down), s_sh_down, Y, I, h, E, st),
           "down_fp8 launch");
   Q38_HIP(q38::launch_combine(Y, inv, idx, false, w, Y + P * h, gate, static_cast<uint16_t*>(out), T, h, E, k, st),
           "combine launch");

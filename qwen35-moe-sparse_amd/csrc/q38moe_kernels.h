@@ -98,6 +98,18 @@ hipError_t launch_down_kn(const uint16_t* A, const int4* tiles, const int32_t* n
 // up to 64 activation rows per workgroup, K split over its waves (q38moe_gemm_small.hip), for K in
 // {128, 256, 512, 1024, 2048} (small_gemm_supported); P = T * k routed rows, shared_rows after them.
 bool small_gemm_supported(int K);
+// e4m3 small tiles (q38moe_gemm_small.hip): K in {512, 1024, 2048}; scales as launch_gate_up_fp8 /
+// launch_down_fp8 take them.
+bool small_gemm_fp8_supported(int K);
+hipError_t launch_gate_up_small_fp8(const uint8_t* xq, const float* a_scale, const int32_t* perm, const int4* tiles,
+                                    const int32_t* ntiles_dev, int max_mtiles, int P, int shared_rows,
+                                    const uint8_t* wq_gate_up, const float* s_gate_up, const uint8_t* wq_sh_gate,
+                                    const float* s_sh_gate, const uint8_t* wq_sh_up, const float* s_sh_up,
+                                    uint16_t* H, int N, int K, int E, int topk, hipStream_t stream);
+hipError_t launch_down_small_fp8(const uint8_t* Hq, const float* a_scale, const int4* tiles, const int32_t* ntiles_dev,
+                                 int max_mtiles, int P, int shared_rows, const uint8_t* wq_down, const float* s_down,
+                                 const uint8_t* wq_sh_down, const float* s_sh_down, uint16_t* Y, int N, int K, int E,
+                                 hipStream_t stream);
 hipError_t launch_gate_up_small(const uint16_t* x, const int32_t* perm, const int4* tiles, const int32_t* ntiles_dev,
                                 int max_mtiles, int P, int shared_rows, const uint16_t* w_gate_up,
                                 const uint16_t* ws_gate, const uint16_t* ws_up, uint16_t* H, int N, int K, int E,

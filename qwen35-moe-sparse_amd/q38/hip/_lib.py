@@ -12,7 +12,7 @@ import torch  # noqa: F401  (loads the HIP runtime first)
 
 LIB_PATH = Path(os.environ.get("Q38MOE_LIB", Path(__file__).resolve().parent / "libq38moe.so"))
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 BF16 = 1
 FP32 = 2
 TILING_PERSISTENT = 1
@@ -33,6 +33,7 @@ SIGNATURES = {
     "q38moe_max_tiles": (_c_i64, [_c_i64, _c_i32, _c_i32, _c_i64]),
     "q38moe_gemm_block_m": (_c_i32, []),
     "q38moe_gemm_tiling": (_c_i32, [_c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64]),
+    "q38moe_gemm_tiling_fp8": (_c_i32, [_c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64]),
     "q38moe_gate_up": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i64, _c_i32, _c_i32, _c_i32,
                                 _c_i32, _c_i32, _vp]),
     "q38moe_down": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,

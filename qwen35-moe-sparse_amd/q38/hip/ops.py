@@ -64,9 +64,11 @@ def max_tiles(T, E, k, shared_rows=0):
     return int(lib.q38moe_max_tiles(T, E, k, shared_rows))
 
 
-def gemm_tiling(T, h, E, k, I, shared_rows=0):
-    """"small" or "persistent": the grouped-GEMM kernels bf16 calls of this shape run."""
-    v = int(lib.q38moe_gemm_tiling(T, h, E, k, I, shared_rows))
+def gemm_tiling(T, h, E, k, I, shared_rows=0, fp8=False):
+    """"small" or "persistent": the grouped-GEMM kernels bf16 (or, with fp8, e4m3) calls of this
+    shape run."""
+    f = lib.q38moe_gemm_tiling_fp8 if fp8 else lib.q38moe_gemm_tiling
+    v = int(f(T, h, E, k, I, shared_rows))
     return {TILING_SMALL: "small", TILING_PERSISTENT: "persistent"}[v]
 
 

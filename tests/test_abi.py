@@ -35,7 +35,7 @@ def test_header_symbols_exported():
 
 def test_abi_version():
     m = _lib()
-    assert m.lib.q38moe_abi_version() == m.ABI_VERSION == 12
+    assert m.lib.q38moe_abi_version() == m.ABI_VERSION == 13
 
 
 def test_max_tiles_and_block_m():
@@ -68,6 +68,10 @@ def test_gemm_tiling_rule():
     assert tiling(219, 219, h=2048, I=512) == m.TILING_PERSISTENT
     assert tiling(550, 550, h=512, I=128) == m.TILING_SMALL         # R = 50.8 at h I = 2^16
     assert tiling(551, 551, h=512, I=128) == m.TILING_PERSISTENT
+    fp8 = lambda T, sh, h=2048, E=64, k=5, I=512: m.lib.q38moe_gemm_tiling_fp8(T, h, E, k, I, sh)  # noqa: E731
+    assert fp8(272, 272) == m.TILING_SMALL       # F = 1.25 R = 25.2: 272 * 6 = 1632 <= 25.2 * 65
+    assert fp8(273, 273) == m.TILING_PERSISTENT
+    assert fp8(1, 1, h=256, I=64) == m.TILING_PERSISTENT   # e4m3 small tiles need K in {512, 1024, 2048}
     assert tiling(40, 40, E=8, k=2) == m.TILING_SMALL    # 120 <= 32 * 9
     assert tiling(100, 100, E=8, k=2) == m.TILING_PERSISTENT
     kinds = [tiling(T, T) for T in range(1, 5000, 7)]

@@ -72,12 +72,16 @@ def _setup(name, T, scale_x=1.0):
     return wl, x, params, bias
 
 
-@pytest.mark.parametrize("name,T", [("c1", 1024), ("c4", 2048)])
-def test_fp8_gemm_stages(gpu, name, T):
-    """gate/up and down on e4m3 vs the fake-quant oracle, stage by stage on identical inputs."""
+@pytest.mark.parametrize("name,T,kind", [("c1", 1024, "persistent"), ("c4", 2048, "persistent"),
+                                         ("c4", 1, "small"), ("c4", 16, "small"), ("c4", 272, "small"),
+                                         ("c4", 273, "persistent")])
+def test_fp8_gemm_stages(gpu, name, T, kind):
+    """gate/up and down on e4m3 vs the fake-quant oracle, stage by stage on identical inputs, on both
+    tilings (small e4m3 tiles up to configuration 4's threshold, T = 272; h = 256 has none)."""
     ops = _ops()
     wl, x, params, _ = _setup(name, T)
     k, E = wl.topk, wl.experts
+    assert ops.gemm_tiling(T, wl.hidden, E, k, wl.inter, T, fp8=True) == kind
     d = {n: p.to(gpu) for n, p in params.items()}
     _, _, ridx, rw = orc.router(x, params["gate.weight"], k)
     gate_logit = orc.bf16(orc._f(x) @ orc._f(params["shared_expert_gate.weight"]).reshape(-1))
@@ -140,7 +144,7 @@ def test_block_fp8_equals_staged_pipeline(gpu, T):
     assert torch.equal(out.cpu(), out2.cpu())
 
 
-@pytest.mark.parametrize("name,T", [("c1", 2048), ("c4", 2048), ("c4", 999)])
+@pytest.mark.parametrize("name,T", [("c1", 2048), ("c4", 2048), ("c4", 999), ("c4", 1), ("c4", 100)])
 def test_block_forward_fp8(gpu, name, T):
     """Whole fp8 block vs the fake-quant oracle on the GPU's own routing (bit-exact routing)."""
     ops = _ops()
