@@ -9,6 +9,9 @@ amplifies rounding noise by about 1.3x per layer: the reference's own bf16 forwa
 L2 away from its fp32 forward at the logits (argmax agreement ~49 %), so bf16 results are judged
 against that spread: ours must be no further from the fp32 reference than 1.25x the reference's bf16
 run is (logsumexp within 1.5x), and closer to the reference's bf16 run than that run is to fp32.
+That spread cannot see a MoE-block error well under 10 %, so the bf16 checks also hold every one of
+the twelve HIP blocks, on the inputs the trunk gave it in this very forward, to the block bar of the
+bf16 path (2e-2 max-abs, 1e-2 relative L2 against the CPU oracle's block on sampled tokens).
 """
 from pathlib import Path
 
@@ -16,6 +19,7 @@ import numpy as np
 import pytest
 import torch
 
+from _util import assert_bf16_close
 from oracle import moe_oracle as O
 from q38 import prefill as P
 
@@ -42,13 +46,13 @@ def _bf16_rows(bits):
 
 
 def _record_blocks(model):
-    """Keep every MoE call's input and output: the list gets one (x, y) per layer and forward."""
+    """Keep every MoE call's input and output: the list gets one (x, y, block) per layer and forward."""
     calls = []
     inner = model._moe
 
     def moe(block, x, with_router):
         res = inner(block, x, with_router)
-        calls.append((x.clone(), (res[0] if with_router else res).clone()))
+        calls.append((x.clone(), (res[0] if with_router else res).clone(), block))
         return res
 
     model._moe = moe
@@ -66,7 +70,7 @@ def _assert_deterministic(logits, again, first, second):
     diff = (logits != again).any(-1)  # [B, S]
     first_pos = [int(torch.nonzero(r)[0]) if r.any() else -1 for r in diff]
     where = "every block's input and output identical: after the last block (final norm, head)"
-    for i, ((x1, y1), (x2, y2)) in enumerate(zip(first, second)):
+    for i, ((x1, y1, _), (x2, y2, _)) in enumerate(zip(first, second)):
         if not torch.equal(x1, x2):
             n = int((x1 != x2).any(-1).sum())
             where = f"layer {i}: the MoE block's input differs at {n} tokens (the trunk diverged before it)"
@@ -81,6 +85,21 @@ def _assert_deterministic(logits, again, first, second):
 
 def _rel(a, b):
     return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+def _assert_blocks_within_bar(calls, k, samples):
+    """Every recorded HIP MoE block against the CPU oracle's block (oracle.block: the reference's
+    roundings, its own router) on the same bf16 inputs, at `samples` tokens spread over the packed
+    sequence: the bf16 block bar (max-abs 2e-2, relative L2 1e-2), as for the standalone block."""
+    assert len(calls) == 12
+    for i, (x, y, block) in enumerate(calls):
+        h = x.shape[-1]
+        xs, ys = x.reshape(-1, h), y.reshape(-1, h)
+        sel = torch.linspace(0, xs.shape[0] - 1, samples).long().to(xs.device)
+        params = {n: p.detach().cpu() for n, p in block.named_parameters()}
+        ref, _ = O.block(xs[sel].cpu(), params, k)
+        mx, r = assert_bf16_close(ys[sel].cpu(), ref, what=f"layer {i} MoE block in the prefill")
+        print(f"layer {i:2d}: block max-abs {mx:.2e} rel {r:.2e}")
 
 
 def test_prefill_fp32_trunk_on_gpu(gpu, golden, params):
@@ -118,6 +137,7 @@ def test_prefill_bf16_hip_within_reference_bf16_spread(gpu, golden, params):
     print(f"aux loss {float(out.aux_loss):.7f} vs reference fp32 {aux_ref:.7f} (bf16 {float(golden['aux_loss_bf16']):.7f})")
     assert abs(float(out.aux_loss) - aux_ref) <= max(2 * spread_aux, 0.1 * abs(aux_ref - k))
     _assert_deterministic(logits, again, first, calls)
+    _assert_blocks_within_bar(first, k, 256)
     ref32, ref16 = golden["logits_fp32"], _bf16_rows(golden["logits_bf16"])
     spread = _rel(ref16, ref32)
     spread_lse = np.abs(golden["lse_bf16"] - golden["lse_fp32"]).max()
@@ -193,6 +213,7 @@ def test_prefill_full_config5_bf16_hip(gpu, golden_full, params):
     assert torch.isfinite(logits).all()
     _assert_deterministic(logits, again, first, calls)
     k = cfg.topk
+    _assert_blocks_within_bar(first, k, 512)
     spread_aux = abs(float(g["aux_loss_bf16"]) - float(g["aux_loss_fp32"]))
     aux_ref = float(g["aux_loss_fp32"])
     assert abs(float(out.aux_loss) - aux_ref) <= max(2 * spread_aux, 0.1 * abs(aux_ref - k))
