@@ -38,7 +38,9 @@ def time_stream(fn, iters, stream):
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
-        torch.cuda._sleep(4_000_000)  # about 2 ms of spinning at the MI355X clock
+        # about 2 ms of spinning at the MI355X clock, and 125 us more per launch beyond 16 (the
+        # slowest host call, the route's, takes well under that)
+        torch.cuda._sleep(4_000_000 + 250_000 * max(0, iters - 16))
     start.record(stream)
     for _ in range(iters):
         fn()
@@ -132,6 +134,16 @@ def kernel_breakdown_fp8(wl, x, d, wq, bias, iters, stream):
     Y = ops.down_fp8(Hq, sH, wq, tiles, tcount, T, k, shared_rows=T)
     torch.cuda.synchronize()
     fl = wl.flops()
+    # The e4m3 small tiles (few rows per expert) stream each routed expert's codes and scales once:
+    # their bound is HBM, the algorithmic bytes those weights (shared expert included) plus the rows
+    # (codes and row scale in, bf16 out).
+    small = ops.gemm_tiling(T, h, E, k, I, T, fp8=True) == "small"
+    used = int((counts > 0).sum()) + 1
+    rows = P + T
+    gu_bound, gu_work = ("hbm", used * 2 * I * (h + 4) + rows * (h + 4 + I * 2)) if small else \
+        ("mfma", fl["gate_up"] + fl["shared"] * 2 // 3)
+    dn_bound, dn_work = ("hbm", used * h * (I + 4) + rows * (I + 4 + h * 2)) if small else \
+        ("mfma", fl["down"] + fl["shared"] // 3)
     stages = {
         "route": (lambda: ops.route(x, d["gate.weight"], k, w_shared_gate=d["shared_expert_gate.weight"],
                                     logit_bias=bias, want_hist=True), "hbm",
@@ -139,11 +151,10 @@ def kernel_breakdown_fp8(wl, x, d, wq, bias, iters, stream):
         # x read (bf16) + e4m3 codes and scales written
         "quant_x": (lambda: ops.quantize_rows(x), "hbm", T * h * 3 + T * 4),
         "permute": (lambda: ops.permute(idx, hist, E, shared_rows=T), "hbm", P * 4 * 3),
-        "gate_up": (lambda: ops.gate_up_fp8(xq, row_scale, wq, perm, tiles, tcount, k, shared_rows=T), "mfma",
-                    fl["gate_up"] + fl["shared"] * 2 // 3),
+        "gate_up": (lambda: ops.gate_up_fp8(xq, row_scale, wq, perm, tiles, tcount, k, shared_rows=T), gu_bound,
+                    gu_work),
         "quant_h": (lambda: ops.quantize_rows(H), "hbm", (P + T) * I * 3 + (P + T) * 4),
-        "down": (lambda: ops.down_fp8(Hq, sH, wq, tiles, tcount, T, k, shared_rows=T), "mfma",
-                 fl["down"] + fl["shared"] // 3),
+        "down": (lambda: ops.down_fp8(Hq, sH, wq, tiles, tcount, T, k, shared_rows=T), dn_bound, dn_work),
         "combine": (lambda: ops.combine(Y, inv, w, E, shared_out=Y[P:], shared_gate_logit=gate), "hbm",
                     T * h * 2 * (k + 2)),
     }
@@ -157,6 +168,8 @@ def kernel_breakdown_fp8(wl, x, d, wq, bias, iters, stream):
             achieved, peak, unit = work / dt / 1e9, PEAK_HBM / 1e9, "GB/s"
         out[name] = dict(us=round(dt * 1e6, 2), bound=bound, work=work, achieved=round(achieved, 2),
                          peak=peak, unit=unit, frac=round(achieved / peak, 4))
+    for name in ("gate_up", "down"):
+        out[name]["tiling"] = "small" if small else "persistent"
     return out
 
 

@@ -246,9 +246,14 @@ hipError_t launch_permute(const void* idx, bool idx64, const int32_t* hist, int3
                           int32_t* tile_count, int block_m, int max_tiles, int shared_rows,
                           int64_t T, int E, int k, hipStream_t stream, const float* row_scale_in,
                           float* row_scale_out) {
-  // At least one block, so T == 0 still writes zero counts and an empty tile table.
+  // At least one block, so T == 0 still writes zero counts and an empty tile table; with a tile
+  // table at least E + 1 blocks, one per group's entries (blocks past the pairs' own only write
+  // those): fewer would walk several groups each, one after another (at T <= 64, a single block
+  // wrote all 65 groups' entries in about 25 us).
   const int64_t nblk = (T + PERM_TOKENS - 1) / PERM_TOKENS;
-  const unsigned grid = (unsigned)(nblk > 0 ? nblk : 1);
+  int64_t g = nblk > 0 ? nblk : 1;
+  if (tiles != nullptr && g < E + 1) g = E + 1;
+  const unsigned grid = (unsigned)g;
   if (idx64)
     hipLaunchKernelGGL(permute_kernel<int64_t>, dim3(grid), dim3(256), 0, stream,
                        (const int64_t*)idx, hist, T, E, k, (int)nblk, counts, starts, perm, inv,
