@@ -543,7 +543,9 @@ constexpr int ROUTE_THREADS = 512;  // 8 waves: 0-3 multiply, all select and rep
 // F32IO: the fp32 path (fp32 models): logits come in as fp32 (logits_in, computed by the fp32
 // router GEMM) and the renormalised weights leave as fp32 (no bf16 rounding, modeling:812 with
 // the fp32 logits dtype); x is unused.
-template <int KT, bool F32IO, int TOK = ROUTE_TOKENS>
+// SPLITK (T <= 16, one 64-token block; bf16, logits computed here): phase 1 is a split-K product
+// instead of the staged one, see below.
+template <int KT, bool F32IO, int TOK = ROUTE_TOKENS, bool SPLITK = false>
 __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
     const uint16_t* __restrict__ wsg, const void* __restrict__ logits_in,
@@ -551,6 +553,7 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     int32_t* __restrict__ idx_out, void* __restrict__ w_out,
     uint16_t* __restrict__ gate_out, int32_t* __restrict__ hist, int64_t T, int h, int E, int k) {
   static_assert(TOK == 64 || TOK == 128, "64 or 128 tokens per block");
+  static_assert(!SPLITK || (TOK == 64 && !F32IO), "split-K logits: one 64-token block, bf16");
   // Staged router weights (phase 1) and logits (from phase 2 on). With 128 tokens both do not fit
   // side by side: they share one LDS area, and the logits are written once every wave has finished
   // its MFMAs.
@@ -575,7 +578,57 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
   if (tid < 64) s_bias[tid] = (bias != nullptr && tid < E) ? bias[tid] : 0.0f;
   if (tid == 0) s_nties = 0;
 
-  if (!F32IO && logits_in == nullptr) {
+  if constexpr (SPLITK) {
+    // At most 16 tokens (decode, short chunks): staging the 133 KB of router weights in LDS for one
+    // 16-token MFMA wave would serialise the copy and the multiply in one workgroup. Instead every
+    // wave multiplies the 16 token rows by all 64 + 1 weight rows over its eighth of K, both operands
+    // loaded from global memory straight into MFMA registers (all its loads in flight at once),
+    // and the eight partial sums are added in wave order through LDS, then rounded to bf16 as the
+    // staged product's logits are. Same products, another fp32 summation order.
+    const int kw = h / (ROUTE_THREADS / 64);  // multiple of 32 (h % 256 == 0)
+    const int64_t trow = (lane & 15) < T ? (lane & 15) : T - 1;
+    const uint16_t* const xa = x + trow * (int64_t)h + 8 * (lane >> 4);
+    const uint16_t* wrow[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = 16 * j + (lane & 15);
+      wrow[j] = wr + (int64_t)(n < E ? n : 0) * h + 8 * (lane >> 4);
+    }
+    const uint16_t* const grow = wsg != nullptr ? wsg + 8 * (lane >> 4) : nullptr;
+    f32x4_t acc[5];
+#pragma unroll
+    for (int j = 0; j < 5; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int kbeg = wave_u * kw;
+#pragma unroll 4
+    for (int kk = 0; kk < kw; kk += 32) {
+      const int kq = kbeg + kk;
+      const u32x4_t a = ld16(xa + kq);
+      u32x4_t b[5];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = ld16(wrow[j] + kq);
+      b[4] = grow != nullptr ? ld16(grow + kq) : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int j = 0; j < 5; ++j) acc[j] = mfma16x16x32(a, b[j], acc[j]);
+    }
+    f32x4_t* const part = reinterpret_cast<f32x4_t*>(s_wl);  // [wave][tile][lane], 40 KB
+#pragma unroll
+    for (int j = 0; j < 5; ++j) part[(wave * 5 + j) * 64 + lane] = acc[j];
+    __syncthreads();
+    if (tid < 5 * 64) {
+      const int j = tid >> 6, l = tid & 63;
+      f32x4_t sum = part[j * 64 + l];
+      for (int w = 1; w < ROUTE_THREADS / 64; ++w) sum += part[(w * 5 + j) * 64 + l];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tok = 4 * (l >> 4) + i, col = 16 * j + (l & 15);
+        if (j < 4) {
+          if (col < E) s_logit[tok][col] = round_bf16(sum[i]);
+        } else if ((l & 15) == 0 && wsg != nullptr) {
+          s_logit[tok][64] = round_bf16(sum[i]);
+        }
+      }
+    }
+  } else if (!F32IO && logits_in == nullptr) {
     const int ntile = (E + 15) >> 4;
     const bool gate_tile = wsg != nullptr;
     const int nrows_w = gate_tile ? ROUTE_WROWS : 64;
@@ -803,9 +856,14 @@ hipError_t launch_route(const uint16_t* x, const uint16_t* wr, const uint16_t* w
   // weights once for twice the tokens (configuration 4, T = 32768: 71 -> 54 us).
   const bool wide = nblk64 > device_cus();
   const int64_t nblk = wide ? (T + 127) / 128 : nblk64;
+  // Up to 16 tokens: the split-K logits (one workgroup either way).
+  const bool splitk = logits_in == nullptr && T <= 16 && h % 256 == 0;
 #define Q38_ROUTE(KT)                                                                                         \
   case KT:                                                                                                    \
-    if (wide)                                                                                                 \
+    if (splitk)                                                                                               \
+      hipLaunchKernelGGL((route_kernel<KT, false, 64, true>), dim3(1), dim3(ROUTE_THREADS), 0, stream, x, wr,  \
+                         wsg, logits_in, bias, logits_out, idx_out, w_out, gate_out, hist, T, h, E, k);       \
+    else if (wide)                                                                                            \
       hipLaunchKernelGGL((route_kernel<KT, false, 128>), dim3((unsigned)nblk), dim3(ROUTE_THREADS), 0, stream, \
                          x, wr, wsg, logits_in, bias, logits_out, idx_out, w_out, gate_out, hist, T, h, E, k); \
     else                                                                                                      \
