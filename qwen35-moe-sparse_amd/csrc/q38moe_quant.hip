@@ -10,7 +10,8 @@
 // The same routine quantises expert weights (rows = output channels, at load time), the tokens
 // entering the gate/up GEMM and the SwiGLU rows entering the down GEMM.
 //
-// HBM-bound: one wave per row; each lane loads 16-byte runs (8 bf16) and stores 8-byte runs.
+// HBM-bound: a wave quantises RPW rows (4 of 512 columns, 2 of 1024, else 1), so that every lane
+// has four 16-byte loads (8 bf16 each) in flight whatever the row length; it stores 8-byte runs.
 #include "q38moe_common.h"
 #include "q38moe_kernels.h"
 
@@ -41,49 +42,66 @@ __device__ __forceinline__ uint32_t e4m3x2(float a, float b) {
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
 }
 
-template <int NCH>  // 16-byte chunks per lane, compile-time for C = 512 * NCH
+template <int NCH, int RPW>  // 16-byte chunks per lane and row (C = 512 * NCH; 0: any C), rows per wave
 __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restrict__ x,
                                                          uint8_t* __restrict__ q,
                                                          float* __restrict__ scale, int64_t R,
                                                          int C) {
+  constexpr int NV = NCH > 0 ? NCH : 8;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * QUANT_WAVES + wave;
-  if (r >= R) return;
-  const uint16_t* xr = x + r * C;
+  const int64_t r0 = ((int64_t)blockIdx.x * QUANT_WAVES + wave) * RPW;
+  if (r0 >= R) return;
   const int nch = NCH > 0 ? NCH : (C / 8 + 63) / 64;
-  u32x4_t v[NCH > 0 ? NCH : 8];
-  float m = 0.0f;
+  u32x4_t v[RPW][NV];
+  float m[RPW];
 #pragma unroll
-  for (int j = 0; j < (NCH > 0 ? NCH : 8); ++j) {
-    if (NCH == 0 && j >= nch) break;
-    const int c = 8 * (lane + 64 * j);
-    v[j] = c < C ? ld16_stream(xr + c) : u32x4_t{0, 0, 0, 0};
+  for (int u = 0; u < RPW; ++u) {
+    m[u] = 0.0f;
+    const bool row_in = r0 + u < R;  // wave-uniform
+    const uint16_t* xr = x + (r0 + u) * C;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float a, b;
-      unpack_bf16x2(v[j][i], a, b);
-      m = nan_max(m, nan_max(fabsf(a), fabsf(b)));
+    for (int j = 0; j < NV; ++j) {
+      if (NCH == 0 && j >= nch) break;
+      const int c = 8 * (lane + 64 * j);
+      v[u][j] = row_in && c < C ? ld16_stream(xr + c) : u32x4_t{0, 0, 0, 0};
     }
   }
-  const float amax = wave_amax(m);
-  const float inv = amax > 0.0f ? 448.0f / amax : (__builtin_isnan(amax) ? amax : 0.0f);
-  if (lane == 0) scale[r] = amax / 448.0f;
-  uint8_t* qr = q + r * C;
 #pragma unroll
-  for (int j = 0; j < (NCH > 0 ? NCH : 8); ++j) {
-    if (NCH == 0 && j >= nch) break;
-    const int c = 8 * (lane + 64 * j);
-    if (c < C) {
-      uint32_t w[2];
+  for (int u = 0; u < RPW; ++u) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        float a0, b0, a1, b1;
-        unpack_bf16x2(v[j][2 * i], a0, b0);
-        unpack_bf16x2(v[j][2 * i + 1], a1, b1);
-        w[i] = e4m3x2(a0 * inv, b0 * inv) | (e4m3x2(a1 * inv, b1 * inv) << 16);
+    for (int j = 0; j < NV; ++j) {
+      if (NCH == 0 && j >= nch) break;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float a, b;
+        unpack_bf16x2(v[u][j][i], a, b);
+        m[u] = nan_max(m[u], nan_max(fabsf(a), fabsf(b)));
       }
-      *reinterpret_cast<uint2*>(qr + c) = make_uint2(w[0], w[1]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < RPW; ++u) {
+    if (r0 + u >= R) break;  // wave-uniform
+    const float amax = wave_amax(m[u]);
+    const float inv = amax > 0.0f ? 448.0f / amax : (__builtin_isnan(amax) ? amax : 0.0f);
+    if (lane == 0) scale[r0 + u] = amax / 448.0f;
+    uint8_t* qr = q + (r0 + u) * C;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      if (NCH == 0 && j >= nch) break;
+      const int c = 8 * (lane + 64 * j);
+      if (c < C) {
+        uint32_t w[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          float a0, b0, a1, b1;
+          unpack_bf16x2(v[u][j][2 * i], a0, b0);
+          unpack_bf16x2(v[u][j][2 * i + 1], a1, b1);
+          w[i] = e4m3x2(a0 * inv, b0 * inv) | (e4m3x2(a1 * inv, b1 * inv) << 16);
+        }
+        *reinterpret_cast<uint2*>(qr + c) = make_uint2(w[0], w[1]);
+      }
     }
   }
 }
@@ -92,19 +110,19 @@ hipError_t launch_quant_rows(const uint16_t* x, uint8_t* q, float* scale, int64_
                              hipStream_t stream) {
   if (R == 0) return hipSuccess;
   if (C % 64 != 0 || C > 8 * 64 * 8) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((R + QUANT_WAVES - 1) / QUANT_WAVES));
+  auto grid = [&](int rpw) { return dim3((unsigned)((R + QUANT_WAVES * rpw - 1) / (QUANT_WAVES * rpw))); };
   switch (C) {
     case 512:
-      hipLaunchKernelGGL(quant_rows_kernel<1>, grid, dim3(256), 0, stream, x, q, scale, R, C);
+      hipLaunchKernelGGL((quant_rows_kernel<1, 4>), grid(4), dim3(256), 0, stream, x, q, scale, R, C);
       break;
     case 1024:
-      hipLaunchKernelGGL(quant_rows_kernel<2>, grid, dim3(256), 0, stream, x, q, scale, R, C);
+      hipLaunchKernelGGL((quant_rows_kernel<2, 2>), grid(2), dim3(256), 0, stream, x, q, scale, R, C);
       break;
     case 2048:
-      hipLaunchKernelGGL(quant_rows_kernel<4>, grid, dim3(256), 0, stream, x, q, scale, R, C);
+      hipLaunchKernelGGL((quant_rows_kernel<4, 1>), grid(1), dim3(256), 0, stream, x, q, scale, R, C);
       break;
     default:
-      hipLaunchKernelGGL(quant_rows_kernel<0>, grid, dim3(256), 0, stream, x, q, scale, R, C);
+      hipLaunchKernelGGL((quant_rows_kernel<0, 1>), grid(1), dim3(256), 0, stream, x, q, scale, R, C);
       break;
   }
   return hipGetLastError();
