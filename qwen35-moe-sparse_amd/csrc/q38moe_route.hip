@@ -530,13 +530,15 @@ __device__ __forceinline__ int group_select(float* row, const float* bias, int E
 
 
 // One block = TOK tokens (64, or 128 when a launch would need more than one round of 64-token
-// blocks), 8 waves. Phase 1: logits on 16x16x32 MFMA (TOK / 16 waves, 16 tokens each),
-// router weights (+ the shared-expert gate row as column 64) staged in LDS per 1024-wide K chunk
-// by all waves, each multiplying wave's 16 x rows loaded straight into registers with the whole
-// chunk in flight. Phase 2: bf16-rounded logits to LDS.
+// blocks), 16 waves. Phase 1: logits on 16x16x32 MFMA, router weights (+ the shared-expert gate row
+// as column 64) staged in LDS per 1024-wide K chunk by all waves; every wave multiplies one
+// 16-token group over one K part of the chunk (4 parts with 64 tokens, 2 with 128), its x rows
+// loaded straight into registers with the whole part in flight, and the parts' partial sums are
+// added in K-part order through LDS. Phase 2: bf16-rounded logits to LDS.
 // Phase 3: eight lanes per token select top-k (unique answer when the k+1 largest values are
-// distinct). Phase 4: tokens with ties are replayed wave-parallel through libstdc++'s algorithm.
-constexpr int ROUTE_THREADS = 512;  // 8 waves: 0-3 multiply, all select and replay ties
+// distinct). Phase 4: tokens with ties are replayed wave-parallel through libstdc++'s algorithm,
+// one per wave: sixteen at a time.
+constexpr int ROUTE_THREADS = 1024;  // 16 waves: all multiply (K split), select and replay ties
 
 // KT = k (1..KMAX) as a template parameter: each instantiation carries only its own selection
 // network, which keeps the kernel's code within the instruction cache.
@@ -585,7 +587,7 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     // loaded from global memory straight into MFMA registers (all its loads in flight at once),
     // and the eight partial sums are added in wave order through LDS, then rounded to bf16 as the
     // staged product's logits are. Same products, another fp32 summation order.
-    const int kw = h / (ROUTE_THREADS / 64);  // multiple of 32 (h % 256 == 0)
+    const int kw = h / (ROUTE_THREADS / 64);  // multiple of 32 (h % 512 == 0)
     const int64_t trow = (lane & 15) < T ? (lane & 15) : T - 1;
     const uint16_t* const xa = x + trow * (int64_t)h + 8 * (lane >> 4);
     const uint16_t* wrow[4];
@@ -635,8 +637,11 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     f32x4_t acc[5];
 #pragma unroll
     for (int j = 0; j < 5; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const bool mma = wave < TOK / 16;
-    const int64_t trow = tb + (wave & (TOK / 16 - 1)) * 16 + (lane & 15);
+    // Every wave multiplies: token group g (16 tokens) over K part kp of each chunk (SPW of its 32
+    // steps); the NKP partial sums of a token group are added in K-part order below.
+    constexpr int G = TOK / 16, NKP = (ROUTE_THREADS / 64) / G, SPW = 32 / NKP;
+    const int g = wave & (G - 1), kp = wave / G;
+    const int64_t trow = tb + g * 16 + (lane & 15);
     const uint16_t* xa = x + (trow < T ? trow : T - 1) * (int64_t)h + 8 * (lane >> 4);
     // Tiles of experts >= E (and the gate tile without wsg) multiply LDS rows that are never
     // filled; their columns are never stored. Computing them keeps the MFMA loop branch-free.
@@ -661,14 +666,14 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
         slot = n * (ROUTE_KCHUNK / 8) + part * 64 + lane;
         return src == nullptr ? nullptr : src + k0 + (c < kc / 8 ? c : 0) * 8;
       };
-      u32x4_t a[32];  // this wave's x rows for a full chunk
+      u32x4_t a[SPW];  // this wave's x rows over its K part of a full chunk
       if constexpr (!ALIAS) {
-        // 64-token blocks: waves 0-3 multiply. Their x loads go first; then all eight waves copy
-        // the weights (asynchronous copies; spread over every wave they arrive sooner than from
-        // four). The multiply starts once both are in.
-        if (mma && full) {
+        // 64-token blocks: the x loads go first; then every wave copies weight segments
+        // (asynchronous copies; spread over every wave they arrive sooner). The multiply starts
+        // once both are in.
+        if (full) {
 #pragma unroll
-          for (int s = 0; s < 32; ++s) a[s] = ld16(xa + k0 + s * 32);
+          for (int s = 0; s < SPW; ++s) a[s] = ld16(xa + k0 + (kp * SPW + s) * 32);
         }
         for (int q = wave_u; q < nseg; q += ROUTE_THREADS / 64) {
           int slot;
@@ -685,14 +690,14 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
           const uint16_t* src = seg_src(q, slot);
           if (src != nullptr) load_lds16(src, &s_w[slot - lane]);
         }
-        if (full && mma) {
+        if (full) {
 #pragma unroll
-          for (int s = 0; s < 32; ++s) a[s] = ld16(xa + k0 + s * 32);
+          for (int s = 0; s < SPW; ++s) a[s] = ld16(xa + k0 + (kp * SPW + s) * 32);
         }
         wait_vmcnt0();
         __syncthreads();
       }
-      if (full && mma) {
+      if (full) {
         // Weight fragments of step s + 1 are read from LDS while step s multiplies. Fragment (j, s)
         // of this lane is wr_slot(16 j + lr, 4 s + lq): with s = 4 m + r its byte offset is
         // 32768 j + 256 m + (2048 lr + 64 (r ^ (lr >> 2)) + 16 (lq ^ (lr & 3))), so four per-lane
@@ -702,34 +707,44 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
         const uint32_t lr = lane & 15, lq = lane >> 4;
         // (The empty asm keeps each base in one register: folded into the constants, every step's
         // address would be a register of its own.)
+        // This wave's steps start at kp * SPW (a multiple of 4): its part's offset joins the bases.
         const uint8_t* fb[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          uint32_t off = 2048u * lr + 64u * ((uint32_t)r ^ (lr >> 2)) + 16u * (lq ^ (lr & 3u));
+          uint32_t off = 2048u * lr + 64u * ((uint32_t)r ^ (lr >> 2)) + 16u * (lq ^ (lr & 3u)) +
+                         64u * (uint32_t)(kp * SPW);
           asm volatile("" : "+v"(off));
           fb[r] = sb + off;
         }
-        uint32_t goff = (uint32_t)wr_slot(64, 0) * 16u + 16u * lq;
+        uint32_t goff = (uint32_t)wr_slot(64, 0) * 16u + 16u * lq + 64u * (uint32_t)(kp * SPW);
         asm volatile("" : "+v"(goff));
         const uint8_t* const gb = sb + goff;
-        u32x4_t bf[2][5];
+        // Fragment reads one step ahead (two buffers); with 128-token blocks a wave's 16 steps of x
+        // already take 64 registers, so its reads run in the step itself.
+        constexpr int NB = SPW > 8 ? 1 : 2;
+        u32x4_t bf[NB][5];
         auto bload = [&](int s, u32x4_t(&d)[5]) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) d[j] = *reinterpret_cast<const u32x4_t*>(fb[s & 3] + (32768 * j + 256 * (s >> 2)));
           d[4] = *reinterpret_cast<const u32x4_t*>(gb + 64 * s);
         };
-        bload(0, bf[0]);
+        if constexpr (NB == 2) bload(0, bf[0]);
 #pragma unroll
-        for (int s = 0; s < 32; ++s) {
-          if (s + 1 < 32) bload(s + 1, bf[(s + 1) & 1]);
+        for (int s = 0; s < SPW; ++s) {
+          if constexpr (NB == 2) {
+            if (s + 1 < SPW) bload(s + 1, bf[(s + 1) & 1]);
+          } else {
+            bload(s, bf[0]);
+          }
           __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of this step's MFMAs
 #pragma unroll
-          for (int j = 0; j < 5; ++j) acc[j] = mfma16x16x32(a[s], bf[s & 1][j], acc[j]);
+          for (int j = 0; j < 5; ++j) acc[j] = mfma16x16x32(a[s], bf[NB == 2 ? (s & 1) : 0][j], acc[j]);
           __builtin_amdgcn_sched_barrier(0);
         }
-      } else if (mma) {
-        // Narrow last chunk (h not a multiple of the chunk): one 32-wide slice at a time.
-        for (int s = 0; s < kc / 32; ++s) {
+      } else {
+        // Narrow last chunk (h not a multiple of the chunk): one 32-wide slice at a time, slice s
+        // to K part s % NKP.
+        for (int s = kp; s < kc / 32; s += NKP) {
           const u32x4_t as = ld16(xa + k0 + s * 32);
           const int c = 4 * s + (lane >> 4);
 #pragma unroll
@@ -738,20 +753,42 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
         }
       }
     }
-    if (ALIAS) __syncthreads();  // every wave's MFMAs have read the staged weights
+    // Partial sums through the staged-weight area (every wave's MFMAs have read it), added in K-part
+    // order; with 128-token blocks the logits share that area, so the sums are formed in registers
+    // before any logit is written.
+    __syncthreads();
+    f32x4_t* const part = reinterpret_cast<f32x4_t*>(s_wl);  // [wave][tile][lane]
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (mma && j < ntile) {
+    for (int j = 0; j < 5; ++j) part[(wave * 5 + j) * 64 + lane] = acc[j];
+    __syncthreads();
+    constexpr int NENT = G * 5 * 64, NPT = (NENT + ROUTE_THREADS - 1) / ROUTE_THREADS;
+    f32x4_t sum[NPT];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int col = 16 * j + (lane & 15);
-          if (col < E) s_logit[wave * 16 + 4 * (lane >> 4) + i][col] = round_bf16(acc[j][i]);
-        }
+    for (int u = 0; u < NPT; ++u) {
+      const int e_ = tid + u * ROUTE_THREADS;
+      if (e_ < NENT) {
+        const int gg = e_ / 320, j = (e_ / 64) % 5, l = e_ & 63;
+        sum[u] = part[(gg * 5 + j) * 64 + l];
+#pragma unroll
+        for (int q = 1; q < NKP; ++q) sum[u] += part[((q * G + gg) * 5 + j) * 64 + l];
       }
     }
-    if (mma && gate_tile && (lane & 15) == 0) {
+    if (ALIAS) __syncthreads();
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s_logit[wave * 16 + 4 * (lane >> 4) + i][64] = round_bf16(acc[4][i]);
+    for (int u = 0; u < NPT; ++u) {
+      const int e_ = tid + u * ROUTE_THREADS;
+      if (e_ < NENT) {
+        const int gg = e_ / 320, j = (e_ / 64) % 5, l = e_ & 63;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tok = gg * 16 + 4 * (l >> 4) + i, col = 16 * j + (l & 15);
+          if (j < 4) {
+            if (j < ntile && col < E) s_logit[tok][col] = round_bf16(sum[u][i]);
+          } else if (gate_tile && (l & 15) == 0) {
+            s_logit[tok][64] = round_bf16(sum[u][i]);
+          }
+        }
+      }
     }
   } else {
     for (int i = tid; i < TOK * E; i += ROUTE_THREADS) {
@@ -780,11 +817,11 @@ __global__ __launch_bounds__(ROUTE_THREADS) void route_kernel(
     if (t < T) gate_out[t] = (uint16_t)f32_to_bf16_rne(s_logit[tid][64]);
   }
 
-  // Phase 3: SEL_LANES lanes per token (token 64 pass + wave * 64 / SEL_LANES + lane / SEL_LANES).
-  for (int pass = 0; pass < TOK / 64; ++pass) {
-    const int tl = 64 * pass + wave * (64 / SEL_LANES) + lane / SEL_LANES;
+  // Phase 3: SEL_LANES lanes per token (token tl0 + wave * 64 / SEL_LANES + lane / SEL_LANES).
+  for (int tl0 = 0; tl0 < TOK; tl0 += ROUTE_THREADS / SEL_LANES) {
+    const int tl = tl0 + wave * (64 / SEL_LANES) + lane / SEL_LANES;
     const int64_t t = tb + tl;
-    if (t < T) {  // uniform over the token's lanes
+    if (tl < TOK && t < T) {  // uniform over the token's lanes
       int oi[KMAX];
       float ow[KMAX];
       const int sel = group_select<KT + 1>(s_logit[tl], bias != nullptr ? s_bias : nullptr, E,
@@ -857,7 +894,7 @@ hipError_t launch_route(const uint16_t* x, const uint16_t* wr, const uint16_t* w
   const bool wide = nblk64 > device_cus();
   const int64_t nblk = wide ? (T + 127) / 128 : nblk64;
   // Up to 16 tokens: the split-K logits (one workgroup either way).
-  const bool splitk = logits_in == nullptr && T <= 16 && h % 256 == 0;
+  const bool splitk = logits_in == nullptr && T <= 16 && h % 512 == 0;
 #define Q38_ROUTE(KT)                                                                                         \
   case KT:                                                                                                    \
     if (splitk)                                                                                               \
