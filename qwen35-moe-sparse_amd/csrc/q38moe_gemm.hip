@@ -824,9 +824,9 @@ hipError_t launch_gather_gemm(const uint16_t* A, const int32_t* perm, const int4
   return hipGetLastError();
 }
 
-// Q38MOE_GEMM_WAVES=8 (read once) keeps the bf16 gate/up launch on the eight-wave kernel where the
-// four-wave one (q38moe_gemm4w.hip) would run: for A/B timing. Results differ only in fp32 summation
-// order.
+// Q38MOE_GEMM_WAVES=8 (read once) keeps the gate/up launches (bf16 and e4m3) on the eight-wave kernel
+// where the four-wave one (q38moe_gemm4w.hip) would run: for A/B timing. Results differ only in fp32
+// summation order.
 static bool use_gemm4w(int N, int K, int64_t a_rows) {
   static const bool off = [] {
     const char* e = std::getenv("Q38MOE_GEMM_WAVES");
@@ -863,6 +863,10 @@ hipError_t launch_gate_up_fp8(const uint8_t* xq, const int32_t* perm, const int4
                               const uint8_t* wq_sh_gate, const float* s_sh_gate,
                               const uint8_t* wq_sh_up, const float* s_sh_up, uint16_t* H, int N,
                               int K, int E, int topk, hipStream_t stream) {
+  const int64_t x_rows = tiles != nullptr ? (int64_t)P / (topk > 0 ? topk : 1) : M_dense;
+  if (K % 2 == 0 && use_gemm4w(N, K / 2, x_rows))
+    return launch_gate_up_4w_fp8(xq, x_rows, perm, tiles, ntiles_dev, max_mtiles, M_dense, P, a_scale, wq_gate_up,
+                                 s_gate_up, wq_sh_gate, s_sh_gate, wq_sh_up, s_sh_up, H, N, K, E, topk, stream);
   return gate_up_impl(xq, perm, tiles, ntiles_dev, max_mtiles, M_dense, P, wq_gate_up, wq_sh_gate, wq_sh_up, H,
                       N, K, E, topk, true, a_scale, s_gate_up, s_sh_gate, s_sh_up, stream);
 }

@@ -1,7 +1,7 @@
-// Four-wave grouped gate/up GEMM + SwiGLU on bf16 MFMA (R5, R6, R9): the bf16 gate/up launch of the
-// block when K (= h) is a multiple of 256 (>= 512) and the H columns fill whole tiles. Same products,
-// roundings, tile table and unit order as grouped_gemm_kernel<MODE_GATE_UP> (q38moe_gemm.hip), a
-// different data path:
+// Four-wave grouped gate/up GEMM + SwiGLU on bf16 or e4m3 MFMA (R5, R6, R9, R14): the gate/up launch
+// of the block when K (= h; e4m3: h / 2) is a multiple of 256 (>= 512) and the H columns fill whole
+// tiles. Same products, roundings, tile table and unit order as grouped_gemm_kernel<MODE_GATE_UP>
+// (q38moe_gemm.hip), a different data path:
 //
 //   H[r, n] = bf16(bf16(silu(bf16(a_r.Wg[n]))) * bf16(a_r.Wu[n])), a_r = x[perm[r] / k] for routed
 //   rows (inference.py:74, 83-96) or x[r - P] for shared-expert rows (x[r] for a dense launch).
@@ -28,6 +28,13 @@
 // runs as two column halves (64 H columns: 64 gate + 64 up weight rows, 8 fragments per K step) on
 // two workgroups, so the round ends in about half the time and no workgroup idles through it. Every
 // output element keeps its products and K order, so the bits do not change.
+//
+// e4m3 operands (gemm4w_gate_up_kernel<true>, the fp8 path's gate/up): the same units, ring, staging
+// and activation loads, which move the same bytes (a row of K e4m3 values is K / 2 16-bit units).
+// Each mfma_f32_16x16x128_f8f6f4 takes a whole 128-byte slice of both operands, so a slice runs its
+// MFMAs once on the activation bytes of both bf16 steps. The epilogue dequantises first:
+// acc * (s_w * s_a), weight-row and activation-row scales staged in LDS per unit (as the eight-wave
+// kernel's e4m3 epilogue).
 //
 // The MFMAs are inline asm (see g4_mfma); every global and LDS access is an ordinary
 // compiler-visible load or store, so the compiler's own waits track all of them, and the only
@@ -59,9 +66,14 @@ struct G4Params {
   const uint16_t* Ws_b;       // shared expert: up [N, K]
   uint16_t* C;                // output rows H [*, N]
   int P;                      // first shared-expert row of the row space
-  int N, K, E, topk;
+  int N, K, E, topk;          // K: 16-bit units per row (bf16 elements, or pairs of e4m3 values)
   int ntiles_n;               // output-column tiles per row tile (N / 128)
   uint32_t a_bytes;           // bytes of A (rows x K x 2 < 2^32)
+  // e4m3 operands only: dequantisation scales.
+  const float* a_scale;       // per row of the row space (the H rows)
+  const float* w_scale;       // routed weight rows [E, 2N]
+  const float* ws_scale_a;    // shared expert gate rows [N]
+  const float* ws_scale_b;    // shared expert up rows [N]
 };
 
 __device__ __forceinline__ int4 g4_tile_entry(const G4Params& p, int mt) {
@@ -207,7 +219,21 @@ __device__ __forceinline__ void g4_mfma_nop(f32x4_t& acc, const u32x4_t& a, cons
 __device__ __forceinline__ void g4_mfma_first_nop(f32x4_t& acc, const u32x4_t& a, const u32x4_t& b) {
   asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(acc) : "v"(a), "v"(b));
 }
-// Wait states between the last MFMA and VALU reads of its result (ample for the 8-pass XDL op).
+// e4m3 x e4m3 (the f8f6f4 form with both formats e4m3, no block scales), 128 K per instruction:
+// lane l holds 32 bytes of row l % 16 of each operand. The kernel fills them with bytes
+// 16 (l / 16) .. + 16 and 64 + 16 (l / 16) .. + 16 of a 128-byte slice, in both operands, so each
+// output is the dot product over the slice's 128 K in another order than the instruction's own.
+__device__ __forceinline__ void g4_mfma8(f32x4_t& acc, const i32x8_t& a, const i32x8_t& b) {
+  asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void g4_mfma8_nop(f32x4_t& acc, const i32x8_t& a, const i32x8_t& b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void g4_mfma8_first_nop(f32x4_t& acc, const i32x8_t& a, const i32x8_t& b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, 0" : "=a"(acc) : "v"(a), "v"(b));
+}
+// Wait states between the last MFMA and VALU reads of its result (ample for the 8-pass bf16 and the
+// 16-pass e4m3 XDL ops).
 __device__ __forceinline__ void g4_mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
 
 // Lane id computed in place (volatile: not hoisted or shared), so the epilogue's lane-derived
@@ -223,23 +249,49 @@ __device__ __forceinline__ int g4_lane() {
 // start 4 banks apart: conflict-free writes and reads, and per-block offsets that are immediates) to
 // whole-line stores (4 rows x 256 B per instruction).
 // NW: weight fragments per K step (16; 8 for a column half: 64 columns, 2 rows x 128 B per store).
-template <int NF, int NW>
+// FP8: the accumulators are dequantised first, acc * (s_w * s_a) with the weight row's and the
+// activation row's scales (sc: 256 activation-row scales, then the unit's weight-row scales).
+template <int NF, int NW, bool FP8>
 __device__ __forceinline__ void g4_epilogue_frag(const G4Params& p, const f32x4_t (&acc)[NW][NF], const G4Unit& u,
-                                                 int f, int wave, uint8_t* stage) {
+                                                 int f, int wave, uint8_t* stage, const float* sc) {
   constexpr int NG = NW / 2;  // gate fragments (the up fragments follow)
   const int lane = g4_lane();
   const int lr = lane & 15, lq = lane >> 4;
   const int rbase = 16 * (4 * f + wave);
   uint8_t* const wr = stage + lr * G4_PITCH + 8 * lq;
+  // Lane l holds weight rows 16 t + 4 (l / 16) + i (i = 0..3) of activation row rbase + l % 16. The
+  // scales of fragment t + 1 are read before fragment t's arithmetic, so their LDS latency is hidden.
+  const float sa = FP8 ? sc[rbase + lr] : 1.0f;
+  const f32x4_t* const swp = reinterpret_cast<const f32x4_t*>(sc + 256 + 4 * lq);
+  f32x4_t swg_n = {1.0f, 1.0f, 1.0f, 1.0f}, swu_n = swg_n;
+  if constexpr (FP8) {
+    swg_n = swp[0];
+    swu_n = swp[4 * NG];
+  }
 #pragma unroll
   for (int t = 0; t < NG; ++t) {
+    f32x4_t swg = swg_n, swu = swu_n;
+    if constexpr (FP8) {
+      swg *= sa;
+      swu *= sa;
+      if (t + 1 < NG) {
+        swg_n = swp[4 * (t + 1)];
+        swu_n = swp[4 * (t + 1 + NG)];
+      }
+    }
     uint32_t v[2];
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
       // Reference rounding (inference.py:90-96): bf16 gate and up, bf16 silu(gate), bf16 product.
       float g0, g1, u0, u1, s0, s1;
-      unpack_bf16x2(pack_bf16x2(acc[t][f][2 * h2], acc[t][f][2 * h2 + 1]), g0, g1);
-      unpack_bf16x2(pack_bf16x2(acc[t + NG][f][2 * h2], acc[t + NG][f][2 * h2 + 1]), u0, u1);
+      if constexpr (FP8) {
+        unpack_bf16x2(pack_bf16x2(acc[t][f][2 * h2] * swg[2 * h2], acc[t][f][2 * h2 + 1] * swg[2 * h2 + 1]), g0, g1);
+        unpack_bf16x2(pack_bf16x2(acc[t + NG][f][2 * h2] * swu[2 * h2], acc[t + NG][f][2 * h2 + 1] * swu[2 * h2 + 1]),
+                      u0, u1);
+      } else {
+        unpack_bf16x2(pack_bf16x2(acc[t][f][2 * h2], acc[t][f][2 * h2 + 1]), g0, g1);
+        unpack_bf16x2(pack_bf16x2(acc[t + NG][f][2 * h2], acc[t + NG][f][2 * h2 + 1]), u0, u1);
+      }
       unpack_bf16x2(pack_bf16x2(g0 * __builtin_amdgcn_rcpf(1.0f + __expf(-g0)),
                                 g1 * __builtin_amdgcn_rcpf(1.0f + __expf(-g1))), s0, s1);
       v[h2] = pack_bf16x2(s0 * u0, s1 * u1);
@@ -270,6 +322,7 @@ __device__ __forceinline__ void g4_epilogue_frag(const G4Params& p, const f32x4_
 struct G4State {
   uint8_t* ring;          // LDS ring base
   uint8_t* stage;         // this wave's staging area
+  float* sc;              // e4m3: the unit's dequantisation scales (256 activation rows, then weight rows)
   uint32_t rd_off[2];     // this lane's fragment-read offset within a slot, for step half s = 0, 1
   uint32_t wl[2];         // this lane's staging-load source offsets (even, odd loads)
   uint32_t ws_lane;       // this lane's staging-store offset within the wave's block (16 lane)
@@ -402,7 +455,7 @@ __device__ __forceinline__ void g4_unit(const G4Params& p, G4State& st, u32x4_t 
   const int nf = g4_nfrag(cur.ti.z, wave);
 #pragma unroll
   for (int f = 0; f < NF; ++f)
-    if (f < nf) g4_epilogue_frag<NF, NW>(p, acc, cur, f, wave, st.stage);
+    if (f < nf) g4_epilogue_frag<NF, NW, false>(p, acc, cur, f, wave, st.stage, st.sc);
   // The next unit's first fragments (its slice 0 was published by the last barrier).
   {
     const uint8_t* const rb = g4_frag_base(st, g4_slot(st.gslice), 0);
@@ -411,9 +464,134 @@ __device__ __forceinline__ void g4_unit(const G4Params& p, G4State& st, u32x4_t 
   }
 }
 
+// ---- e4m3 operands -------------------------------------------------------------------------------
+// The same units, ring, staging and activation loads (a row of K e4m3 values is K / 2 16-bit units,
+// so every byte offset above holds); an MFMA takes a whole 128-byte slice of its two operands, the
+// bytes the two 32-K steps of the bf16 kernel load, so the MFMAs of a slice run once per slice on
+// both halves together. Activation buffers hold whole slices (two: slice j multiplies one while
+// slice j + 1 loads into the other), the weight window whole-slice fragment pairs.
+constexpr int G4_WIN8 = 4;  // weight-fragment pairs read ahead (MFMA groups)
+
+__device__ __forceinline__ i32x8_t g4_cat(const u32x4_t& lo, const u32x4_t& hi) {
+  return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+// Fragment t of a slice: its two step halves (bases of g4_frag_base with s = 0, 1).
+__device__ __forceinline__ i32x8_t g4_frag8(const uint8_t* b0, const uint8_t* b1, int t) {
+  return g4_cat(g4_frag(b0, t), g4_frag(b1, t));
+}
+// This lane's activation bytes of a slice: the two step halves at kb0, kb1 (g4_kbyte of steps 2j, 2j+1).
+__device__ __forceinline__ i32x8_t g4_bload8(__amdgpu_buffer_rsrc_t r, uint32_t xo, uint32_t kb0, uint32_t kb1) {
+  return g4_cat(g4_bload(r, xo, kb0), g4_bload(r, xo, kb1));
+}
+
+// One 128-K slice: for each of the NW weight fragments t, the NF MFMAs with activation buffer XB,
+// then the read of pair t + G4_WIN8 (this slice's, from rc0/rc1; past NW - 1 the next slice's, from
+// rn0/rn1, unless !RNEXT). After groups 0-3 the loads of the next slice's activation fragment t (XNF
+// fragments into buffer XB ^ 1, offsets xo at kb0, kb1): every MFMA of a slice reads all four, so
+// they go first (all eight after groups 0 and 1 measured 5 us slower at configuration 4: bursts of
+// memory instructions stall the issuing waves). After groups 4 .. 3 + NW/2 staging store i and
+// staging load i (as g4_step with WS). FIRST, RT: as g4_step.
+template <int NF, int XNF, int XB, bool RNEXT, bool FIRST, int NW, bool RT>
+__device__ __forceinline__ void g4_slice8(f32x4_t (&acc)[NW][NF], i32x8_t (&wp)[G4_WIN8], i32x8_t (&xb)[2][4],
+                                          u32x4_t (&wst)[8], const G4State& st, const uint32_t (&xo)[4],
+                                          uint32_t kb0, uint32_t kb1, const uint8_t* rc0, const uint8_t* rc1,
+                                          const uint8_t* rn0, const uint8_t* rn1, uint8_t* wdst, const G4Unit& wu,
+                                          int wj, int nst, int nld) {
+#pragma unroll
+  for (int t = 0; t < NW; ++t) {
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      if (FIRST) g4_mfma8_first_nop(acc[t][f], wp[t % G4_WIN8], xb[XB][f]);
+      else if constexpr (NW == 8) g4_mfma8_nop(acc[t][f], wp[t % G4_WIN8], xb[XB][f]);
+      else g4_mfma8(acc[t][f], wp[t % G4_WIN8], xb[XB][f]);
+    }
+    if (t + G4_WIN8 < NW) wp[t % G4_WIN8] = g4_frag8(rc0, rc1, t + G4_WIN8);
+    else if (RNEXT) wp[t % G4_WIN8] = g4_frag8(rn0, rn1, t + G4_WIN8 - NW);
+    if (t < 4 && t < XNF) xb[XB ^ 1][t] = g4_bload8(st.xrs, xo[t], kb0, kb1);
+    if (t >= 4 && t - 4 < NW / 2) {
+      const int i = t - 4;
+      if (!RT || i < nst) *reinterpret_cast<u32x4_t*>(wdst + 1024 * i) = wst[i];
+      if (!RT || i < nld) wst[i] = g4_wload(wu, wj, st.nk, st.K2, st.wl, i);
+    }
+  }
+}
+
+// Dequantisation scale of weight row r (0 .. 16 NW - 1) of unit u (the staging rows' mapping).
+__device__ __forceinline__ float g4_weight_scale(const G4Params& p, const G4Unit& u, int r) {
+  const int nwr = u.half < 0 ? 256 : 128;
+  const bool up = r >= nwr / 2;
+  const int col = u.nt * 128 + (u.half < 0 ? 0 : 64 * u.half) + (up ? r - nwr / 2 : r);
+  if (u.ti.x >= p.E) return (up ? p.ws_scale_b : p.ws_scale_a)[col];
+  return p.w_scale[(int64_t)u.ti.x * 2 * p.N + (up ? p.N : 0) + col];
+}
+
+// One unit on e4m3 operands (as g4_unit): nk slices in iterations of four, then the epilogue. On
+// entry wp holds slice 0's first G4_WIN8 pairs, xb[0] slice 0's activation loads, the ring slices 0
+// and 1 and wst slice 2 (loads issued). The unit's scales are loaded at its start and stored to LDS
+// after its first iteration, whose barriers have retired every read of the previous unit's.
+template <int NF, int NW>
+__device__ __forceinline__ void g4_unit8(const G4Params& p, G4State& st, i32x8_t (&wp)[G4_WIN8],
+                                         i32x8_t (&xb)[2][4], u32x4_t (&wst)[8], const G4Unit& cur,
+                                         const G4Unit& nxt, int wave) {
+  f32x4_t acc[NW][NF];
+  const int nk = st.nk;
+  const bool nxt_half = nxt.half >= 0;
+  const int nxt_n = nxt_half ? 4 : 8;
+  const int tid = 64 * wave + g4_lane();
+  const float s_a = p.a_scale[cur.ti.y + (tid < cur.ti.z ? tid : 0)];
+  const float s_w = tid < 16 * NW ? g4_weight_scale(p, cur, tid) : 0.0f;
+#define Q38_G8_SLICE(J, S_, FIRST_, LAST_)                                                               \
+  do {                                                                                                  \
+    const int j_ = (J) + (S_);                                                                          \
+    const uint8_t* rc0_ = g4_frag_base(st, g4_slot(st.gslice), 0);                                      \
+    const uint8_t* rc1_ = g4_frag_base(st, g4_slot(st.gslice), 1);                                      \
+    const uint8_t* rn0_ = g4_frag_base(st, g4_slot(st.gslice + 1), 0);                                  \
+    const uint8_t* rn1_ = g4_frag_base(st, g4_slot(st.gslice + 1), 1);                                  \
+    const bool sc_ = j_ + 2 < nk, wc_ = j_ + 3 < nk; /* slices j + 2, j + 3 this unit's */              \
+    g4_barrier();                                                                                       \
+    uint8_t* ws_ = g4_store_base(st, g4_slot(st.gslice + 2), (LAST_) && !sc_ ? nxt_half : NW == 8);     \
+    const int nst_ = (LAST_) && !sc_ ? nxt_n : NW / 2, nld_ = (LAST_) && !wc_ ? nxt_n : NW / 2;         \
+    if (!(LAST_) || (S_) < 3)                                                                           \
+      g4_slice8<NF, NF, (S_) & 1, true, FIRST_ && (S_) == 0, NW, LAST_>(                                \
+          acc, wp, xb, wst, st, cur.xo, g4_kbyte(2 * j_ + 2, cur.rot, nk), g4_kbyte(2 * j_ + 3, cur.rot, nk), \
+          rc0_, rc1_, rn0_, rn1_, ws_, wc_ ? cur : nxt, wc_ ? j_ + 3 : j_ + 3 - nk, nst_, nld_);         \
+    else                                                                                                \
+      g4_slice8<NF, 4, (S_) & 1, false, false, NW, LAST_>(                                              \
+          acc, wp, xb, wst, st, nxt.xo, g4_kbyte(0, nxt.rot, nk), g4_kbyte(1, nxt.rot, nk), rc0_, rc1_, \
+          rn0_, rn1_, ws_, wc_ ? cur : nxt, wc_ ? j_ + 3 : j_ + 3 - nk, nst_, nld_);                     \
+    ++st.gslice;                                                                                        \
+  } while (0)
+#define Q38_G8_ITER(J, FIRST_, LAST_)                                                                   \
+  do {                                                                                                  \
+    Q38_G8_SLICE(J, 0, FIRST_, LAST_); Q38_G8_SLICE(J, 1, FIRST_, LAST_);                               \
+    Q38_G8_SLICE(J, 2, FIRST_, LAST_); Q38_G8_SLICE(J, 3, FIRST_, LAST_);                               \
+  } while (0)
+  Q38_G8_ITER(0, true, false);
+  st.sc[tid] = s_a;
+  if (tid < 16 * NW) st.sc[256 + tid] = s_w;
+  for (int j = 4; j < nk - 4; j += 4) Q38_G8_ITER(j, false, false);
+  Q38_G8_ITER(nk - 4, false, true);
+#undef Q38_G8_ITER
+#undef Q38_G8_SLICE
+  g4_mfma_drain();
+  const int nf = g4_nfrag(cur.ti.z, wave);
+#pragma unroll
+  for (int f = 0; f < NF; ++f)
+    if (f < nf) g4_epilogue_frag<NF, NW, true>(p, acc, cur, f, wave, st.stage, st.sc);
+  {
+    const uint8_t* const b0 = g4_frag_base(st, g4_slot(st.gslice), 0);
+    const uint8_t* const b1 = g4_frag_base(st, g4_slot(st.gslice), 1);
+#pragma unroll
+    for (int t = 0; t < G4_WIN8; ++t) wp[t] = g4_frag8(b0, b1, t);
+  }
+}
+
+// FP8: e4m3 activations and weights (g4_unit8) with per-row dequantisation scales.
+template <bool FP8>
 __global__ __launch_bounds__(G4_THREADS, 1) void gemm4w_gate_up_kernel(G4Params p) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[G4_NSLOT * G4_SLOT];
   __shared__ __attribute__((aligned(16))) uint8_t stage[4 * G4_STAGE];
+  __shared__ __attribute__((aligned(16))) float scales[FP8 ? 512 : 4];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = (int)gridDim.x, b = (int)blockIdx.x;
@@ -432,6 +610,7 @@ __global__ __launch_bounds__(G4_THREADS, 1) void gemm4w_gate_up_kernel(G4Params 
   G4State st;
   st.ring = ring;
   st.stage = stage + wave * G4_STAGE;
+  st.sc = scales;
   st.gslice = 0;
   st.nk = nk;
   st.K2 = 2u * (uint32_t)p.K;
@@ -465,9 +644,9 @@ __global__ __launch_bounds__(G4_THREADS, 1) void gemm4w_gate_up_kernel(G4Params 
   int4 tinn = g4_tile_entry(p, g4_tile_index(p, Lnn, U0, split));
   g4_row_sources(p, tinn, wave, lane, src2);
 
-  // Prologue: slices 0 and 1 into the ring, slice 2 in wst; activation steps 0-2 in flight; step 0's
-  // fragments.
-  u32x4_t wf[G4_WIN], xb[G4_XBUF][4], wst[8];
+  // Prologue: slices 0 and 1 into the ring, slice 2 in wst; activation steps 0-2 in flight (e4m3:
+  // slice 0); step 0's fragments (e4m3: slice 0's first pairs).
+  u32x4_t wst[8];
   const bool half0 = cur.half >= 0;
   const int n0 = half0 ? 4 : 8;
 #pragma unroll
@@ -484,34 +663,63 @@ __global__ __launch_bounds__(G4_THREADS, 1) void gemm4w_gate_up_kernel(G4Params 
   for (int i = 0; i < 8; ++i)
     if (i < n0) wst[i] = g4_wload(cur, 2, nk, st.K2, st.wl, i);
   const int nf0 = cur.ti.z > 128 ? 4 : 2;
-#pragma unroll
-  for (int q = 0; q < G4_XBUF - 1; ++q)
+  // After a unit (Ln != L): on to the next one.
+#define Q38_G4_NEXT()                                                                                    \
+  L = Ln;                                                                                               \
+  cur = nxt;                                                                                            \
+  Ln = Lnn;                                                                                             \
+  g4_unit_head(p, Ln, nk, wave, U0, split, nxt);                                                        \
+  g4_unit_rows(p, nxt.ti, lane, src2, nxt);                                                             \
+  Lnn = Ln + G < used ? Ln + G : Ln;                                                                    \
+  tinn = g4_tile_entry(p, g4_tile_index(p, Lnn, U0, split));                                            \
+  g4_row_sources(p, tinn, wave, lane, src2)
+  // Units of at most 128 rows: every wave has at most two active fragments.
+  if constexpr (FP8) {
+    i32x8_t wp[G4_WIN8], xb[2][4];
 #pragma unroll
     for (int f = 0; f < 4; ++f)
-      if (f < nf0) xb[q][f] = g4_bload(st.xrs, cur.xo[f], g4_kbyte(q, cur.rot, nk));
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (f < nf0) xb[0][f] = g4_bload8(st.xrs, cur.xo[f], g4_kbyte(0, cur.rot, nk), g4_kbyte(1, cur.rot, nk));
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
-  for (int t = 0; t < G4_WIN; ++t) wf[t] = g4_frag(g4_frag_base(st, 0, 0), t);
-
-  for (;;) {
-    // Units of at most 128 rows: every wave has at most two active fragments.
-    if (cur.half < 0) {
-      if (cur.ti.z > 128) g4_unit<4, 16>(p, st, wf, xb, wst, cur, nxt, wave);
-      else g4_unit<2, 16>(p, st, wf, xb, wst, cur, nxt, wave);
-    } else {
-      if (cur.ti.z > 128) g4_unit<4, 8>(p, st, wf, xb, wst, cur, nxt, wave);
-      else g4_unit<2, 8>(p, st, wf, xb, wst, cur, nxt, wave);
+    for (int t = 0; t < G4_WIN8; ++t) wp[t] = g4_frag8(g4_frag_base(st, 0, 0), g4_frag_base(st, 0, 1), t);
+    // (A loop of the same form as the bf16 one below left the register allocator 30 VGPRs short.)
+    auto advance = [&]() -> bool {
+      if (Ln == L) return false;
+      Q38_G4_NEXT();
+      return true;
+    };
+    do {
+      if (cur.half < 0) {
+        if (cur.ti.z > 128) g4_unit8<4, 16>(p, st, wp, xb, wst, cur, nxt, wave);
+        else g4_unit8<2, 16>(p, st, wp, xb, wst, cur, nxt, wave);
+      } else {
+        if (cur.ti.z > 128) g4_unit8<4, 8>(p, st, wp, xb, wst, cur, nxt, wave);
+        else g4_unit8<2, 8>(p, st, wp, xb, wst, cur, nxt, wave);
+      }
+    } while (advance());
+  } else {
+    u32x4_t wf[G4_WIN], xb[G4_XBUF][4];
+#pragma unroll
+    for (int q = 0; q < G4_XBUF - 1; ++q)
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+        if (f < nf0) xb[q][f] = g4_bload(st.xrs, cur.xo[f], g4_kbyte(q, cur.rot, nk));
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int t = 0; t < G4_WIN; ++t) wf[t] = g4_frag(g4_frag_base(st, 0, 0), t);
+    for (;;) {
+      if (cur.half < 0) {
+        if (cur.ti.z > 128) g4_unit<4, 16>(p, st, wf, xb, wst, cur, nxt, wave);
+        else g4_unit<2, 16>(p, st, wf, xb, wst, cur, nxt, wave);
+      } else {
+        if (cur.ti.z > 128) g4_unit<4, 8>(p, st, wf, xb, wst, cur, nxt, wave);
+        else g4_unit<2, 8>(p, st, wf, xb, wst, cur, nxt, wave);
+      }
+      if (Ln == L) break;
+      Q38_G4_NEXT();
     }
-    if (Ln == L) break;
-    L = Ln;
-    cur = nxt;
-    Ln = Lnn;
-    g4_unit_head(p, Ln, nk, wave, U0, split, nxt);
-    g4_unit_rows(p, nxt.ti, lane, src2, nxt);
-    Lnn = Ln + G < used ? Ln + G : Ln;
-    tinn = g4_tile_entry(p, g4_tile_index(p, Lnn, U0, split));
-    g4_row_sources(p, tinn, wave, lane, src2);
   }
+#undef Q38_G4_NEXT
   // Retire the lookahead loads of the (absent) next unit before the wave ends.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
@@ -528,21 +736,24 @@ bool gemm4w_supported(int N, int K, int64_t a_rows) {
   return a_rows * 2 * (int64_t)K < ((int64_t)1 << 32);
 }
 
-hipError_t launch_gate_up_4w(const uint16_t* x, int64_t x_rows, const int32_t* perm, const int4* tiles,
-                             const int32_t* ntiles_dev, int max_mtiles, int64_t M_dense, int P,
-                             const uint16_t* w_gate_up, const uint16_t* ws_gate, const uint16_t* ws_up, uint16_t* H,
-                             int N, int K, int E, int topk, hipStream_t stream) {
+// K in 16-bit units (e4m3: K / 2 of the elements); scales only with fp8.
+static hipError_t gate_up_4w_impl(const void* x, int64_t x_rows, const int32_t* perm, const int4* tiles,
+                                  const int32_t* ntiles_dev, int max_mtiles, int64_t M_dense, int P,
+                                  const void* w_gate_up, const void* ws_gate, const void* ws_up, uint16_t* H,
+                                  int N, int K, int E, int topk, bool fp8, const float* a_scale,
+                                  const float* w_scale, const float* ws_scale_gate, const float* ws_scale_up,
+                                  hipStream_t stream) {
   if (!gemm4w_supported(N, K, x_rows)) return hipErrorInvalidValue;
   G4Params p;
-  p.A = x;
+  p.A = static_cast<const uint16_t*>(x);
   p.perm = perm;
   p.tiles = tiles;
   p.ntiles_dev = ntiles_dev;
   p.ntiles_host = tiles != nullptr ? 0 : (int)((M_dense + G4_BM - 1) / G4_BM);
   p.M = M_dense;
-  p.W = w_gate_up;
-  p.Ws_a = ws_gate;
-  p.Ws_b = ws_up;
+  p.W = static_cast<const uint16_t*>(w_gate_up);
+  p.Ws_a = static_cast<const uint16_t*>(ws_gate);
+  p.Ws_b = static_cast<const uint16_t*>(ws_up);
   p.C = H;
   p.P = P;
   p.N = N;
@@ -551,13 +762,37 @@ hipError_t launch_gate_up_4w(const uint16_t* x, int64_t x_rows, const int32_t* p
   p.topk = topk;
   p.ntiles_n = N / 128;
   p.a_bytes = (uint32_t)(x_rows * 2 * (int64_t)K);
+  p.a_scale = a_scale;
+  p.w_scale = w_scale;
+  p.ws_scale_a = ws_scale_gate;
+  p.ws_scale_b = ws_scale_up;
   const int mt = tiles != nullptr ? max_mtiles : p.ntiles_host;
   if (mt == 0) return hipSuccess;
   const int cus = device_cus();
   const int64_t units = (int64_t)mt * p.ntiles_n;
   const dim3 grid((unsigned)(units < cus ? units : cus));
-  hipLaunchKernelGGL(gemm4w_gate_up_kernel, grid, dim3(G4_THREADS), 0, stream, p);
+  if (fp8) hipLaunchKernelGGL(gemm4w_gate_up_kernel<true>, grid, dim3(G4_THREADS), 0, stream, p);
+  else hipLaunchKernelGGL(gemm4w_gate_up_kernel<false>, grid, dim3(G4_THREADS), 0, stream, p);
   return hipGetLastError();
+}
+
+hipError_t launch_gate_up_4w(const uint16_t* x, int64_t x_rows, const int32_t* perm, const int4* tiles,
+                             const int32_t* ntiles_dev, int max_mtiles, int64_t M_dense, int P,
+                             const uint16_t* w_gate_up, const uint16_t* ws_gate, const uint16_t* ws_up, uint16_t* H,
+                             int N, int K, int E, int topk, hipStream_t stream) {
+  return gate_up_4w_impl(x, x_rows, perm, tiles, ntiles_dev, max_mtiles, M_dense, P, w_gate_up, ws_gate, ws_up, H, N,
+                         K, E, topk, false, nullptr, nullptr, nullptr, nullptr, stream);
+}
+
+hipError_t launch_gate_up_4w_fp8(const uint8_t* xq, int64_t x_rows, const int32_t* perm, const int4* tiles,
+                                 const int32_t* ntiles_dev, int max_mtiles, int64_t M_dense, int P,
+                                 const float* a_scale, const uint8_t* wq_gate_up, const float* s_gate_up,
+                                 const uint8_t* wq_sh_gate, const float* s_sh_gate, const uint8_t* wq_sh_up,
+                                 const float* s_sh_up, uint16_t* H, int N, int K, int E, int topk,
+                                 hipStream_t stream) {
+  if (K % 2 != 0) return hipErrorInvalidValue;
+  return gate_up_4w_impl(xq, x_rows, perm, tiles, ntiles_dev, max_mtiles, M_dense, P, wq_gate_up, wq_sh_gate,
+                         wq_sh_up, H, N, K / 2, E, topk, true, a_scale, s_gate_up, s_sh_gate, s_sh_up, stream);
 }
 
 }  // namespace q38

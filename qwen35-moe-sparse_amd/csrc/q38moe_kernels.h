@@ -82,6 +82,14 @@ hipError_t launch_gate_up_4w(const uint16_t* x, int64_t x_rows, const int32_t* p
                              const int32_t* ntiles_dev, int max_mtiles, int64_t M_dense, int P,
                              const uint16_t* w_gate_up, const uint16_t* ws_gate, const uint16_t* ws_up, uint16_t* H,
                              int N, int K, int E, int topk, hipStream_t stream);
+// The same kernel on e4m3 operands (K in elements; runs when gemm4w_supported(N, K / 2, x_rows)): same
+// arguments and results (up to fp32 summation order) as launch_gate_up_fp8, which calls it.
+hipError_t launch_gate_up_4w_fp8(const uint8_t* xq, int64_t x_rows, const int32_t* perm, const int4* tiles,
+                                 const int32_t* ntiles_dev, int max_mtiles, int64_t M_dense, int P,
+                                 const float* a_scale, const uint8_t* wq_gate_up, const float* s_gate_up,
+                                 const uint8_t* wq_sh_gate, const float* s_sh_gate, const uint8_t* wq_sh_up,
+                                 const float* s_sh_up, uint16_t* H, int N, int K, int E, int topk,
+                                 hipStream_t stream);
 
 // Grouped gate/up + SwiGLU over routed tiles (no shared-expert rows) that also stores the bf16
 // pre-activations GU [rows, 2N] = [bf16(g) | bf16(u)] next to H [rows, N].

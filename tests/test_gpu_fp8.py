@@ -73,11 +73,14 @@ def _setup(name, T, scale_x=1.0):
 
 
 @pytest.mark.parametrize("name,T,kind", [("c1", 1024, "persistent"), ("c4", 2048, "persistent"),
-                                         ("c4", 1, "small"), ("c4", 16, "small"), ("c4", 272, "small"),
-                                         ("c4", 273, "persistent")])
+                                         ("c4", 1024, "persistent"), ("c4", 1, "small"), ("c4", 16, "small"),
+                                         ("c4", 272, "small"), ("c4", 273, "persistent")])
 def test_fp8_gemm_stages(gpu, name, T, kind):
     """gate/up and down on e4m3 vs the fake-quant oracle, stage by stage on identical inputs, on both
-    tilings (small e4m3 tiles up to configuration 4's threshold, T = 272; h = 256 has none)."""
+    tilings (small e4m3 tiles up to configuration 4's threshold, T = 272; h = 256 has none). At
+    configuration 4 the persistent gate/up is the four-wave kernel: T = 2048 (about 72 row tiles of
+    more than 128 rows, 288 units) and T = 1024 (rows per expert near 80: units of at most 128 rows)
+    both end in a partial round that runs as column halves."""
     ops = _ops()
     wl, x, params, _ = _setup(name, T)
     k, E = wl.topk, wl.experts
