@@ -65,9 +65,9 @@ def test_quantize_rows_nan_row(gpu):
     assert torch.equal(q.cpu()[[0, 1, 2, 3, 4, 6, 7]], rq[[0, 1, 2, 3, 4, 6, 7]])
 
 
-def _setup(name, T, scale_x=1.0):
+def _setup(name, T, scale_x=1.0, **shape):
     from q38 import workloads
-    wl = workloads.get(name)
+    wl = workloads.get(name, **shape)
     x, params, bias = workloads.make(wl, tokens=T)
     return wl, x, params, bias
 
@@ -81,8 +81,20 @@ def test_fp8_gemm_stages(gpu, name, T, kind):
     configuration 4 the persistent gate/up is the four-wave kernel: T = 2048 (about 72 row tiles of
     more than 128 rows, 288 units) and T = 1024 (rows per expert near 80: units of at most 128 rows)
     both end in a partial round that runs as column halves."""
+    _check_fp8_stages(gpu, name, T, kind)
+
+
+@pytest.mark.parametrize("h,I,T", [(1024, 128, 1500), (1024, 384, 700), (1536, 256, 3000)])
+def test_fp8_gemm_stages_four_wave_shapes(gpu, h, I, T):
+    """The four-wave e4m3 gate/up at the edges of its rule: h = 1024 (eight 128-byte slices, the
+    first and the last iteration only, no steady one), one column tile (I = 128), three (I = 384),
+    and h = 1536 (twelve slices: one steady iteration)."""
+    _check_fp8_stages(gpu, "c4", T, "persistent", hidden=h, inter=I, shared_inter=I)
+
+
+def _check_fp8_stages(gpu, name, T, kind, **shape):
     ops = _ops()
-    wl, x, params, _ = _setup(name, T)
+    wl, x, params, _ = _setup(name, T, **shape)
     k, E = wl.topk, wl.experts
     assert ops.gemm_tiling(T, wl.hidden, E, k, wl.inter, T, fp8=True) == kind
     d = {n: p.to(gpu) for n, p in params.items()}
