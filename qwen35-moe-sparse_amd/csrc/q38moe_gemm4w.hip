@@ -486,11 +486,14 @@ __device__ __forceinline__ i32x8_t g4_bload8(__amdgpu_buffer_rsrc_t r, uint32_t 
 
 // One 128-K slice: for each of the NW weight fragments t, the NF MFMAs with activation buffer XB,
 // then the read of pair t + G4_WIN8 (this slice's, from rc0/rc1; past NW - 1 the next slice's, from
-// rn0/rn1, unless !RNEXT). After groups 0-3 the loads of the next slice's activation fragment t (XNF
-// fragments into buffer XB ^ 1, offsets xo at kb0, kb1): every MFMA of a slice reads all four, so
-// they go first (all eight after groups 0 and 1 measured 5 us slower at configuration 4: bursts of
-// memory instructions stall the issuing waves). After groups 4 .. 3 + NW/2 staging store i and
-// staging load i (as g4_step with WS). FIRST, RT: as g4_step.
+// rn0/rn1, unless !RNEXT). After groups 0-7 the loads of the next slice's activation fragments, one
+// per group (group t: step half t % 2 of fragment t / 2, for XNF fragments, into buffer XB ^ 1,
+// offsets xo at kb0, kb1): every MFMA of a slice reads all four fragments, so they go in the first
+// half. After groups NW/2 .. NW - 1 staging store i and staging load i (as g4_step with WS). At
+// configuration 4 this order ran gate/up in 444-445 us against 463-471 us with two activation loads
+// after each of groups 0-3 and the staging after groups 4-11 (three interleaved runs, one box), and
+// all eight activation loads after groups 0 and 1 were 5 us slower still: bursts of memory
+// instructions stall the issuing wave. FIRST, RT: as g4_step.
 template <int NF, int XNF, int XB, bool RNEXT, bool FIRST, int NW, bool RT>
 __device__ __forceinline__ void g4_slice8(f32x4_t (&acc)[NW][NF], i32x8_t (&wp)[G4_WIN8], i32x8_t (&xb)[2][4],
                                           u32x4_t (&wst)[8], const G4State& st, const uint32_t (&xo)[4],
@@ -507,9 +510,17 @@ __device__ __forceinline__ void g4_slice8(f32x4_t (&acc)[NW][NF], i32x8_t (&wp)[
     }
     if (t + G4_WIN8 < NW) wp[t % G4_WIN8] = g4_frag8(rc0, rc1, t + G4_WIN8);
     else if (RNEXT) wp[t % G4_WIN8] = g4_frag8(rn0, rn1, t + G4_WIN8 - NW);
-    if (t < 4 && t < XNF) xb[XB ^ 1][t] = g4_bload8(st.xrs, xo[t], kb0, kb1);
-    if (t >= 4 && t - 4 < NW / 2) {
-      const int i = t - 4;
+    if (t < 8 && (t >> 1) < XNF) {
+      const u32x4_t h = g4_bload(st.xrs, xo[t >> 1], (t & 1) ? kb1 : kb0);
+      i32x8_t& d = xb[XB ^ 1][t >> 1];
+      if (t & 1) {
+        d[4] = (int)h[0]; d[5] = (int)h[1]; d[6] = (int)h[2]; d[7] = (int)h[3];
+      } else {
+        d[0] = (int)h[0]; d[1] = (int)h[1]; d[2] = (int)h[2]; d[3] = (int)h[3];
+      }
+    }
+    if (t >= NW / 2) {
+      const int i = t - NW / 2;
       if (!RT || i < nst) *reinterpret_cast<u32x4_t*>(wdst + 1024 * i) = wst[i];
       if (!RT || i < nld) wst[i] = g4_wload(wu, wj, st.nk, st.K2, st.wl, i);
     }
