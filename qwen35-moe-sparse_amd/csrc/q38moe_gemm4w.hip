@@ -489,17 +489,21 @@ __device__ __forceinline__ i32x8_t g4_bload8(__amdgpu_buffer_rsrc_t r, uint32_t 
 // rn0/rn1, unless !RNEXT). After groups 0-7 the loads of the next slice's activation fragments, one
 // per group (group t: step half t % 2 of fragment t / 2, for XNF fragments, into buffer XB ^ 1,
 // offsets xo at kb0, kb1): every MFMA of a slice reads all four fragments, so they go in the first
-// half. After groups NW/2 .. NW - 1 staging store i and staging load i (as g4_step with WS). At
-// configuration 4 this order ran gate/up in 444-445 us against 463-471 us with two activation loads
-// after each of groups 0-3 and the staging after groups 4-11 (three interleaved runs, one box), and
-// all eight activation loads after groups 0 and 1 were 5 us slower still: bursts of memory
-// instructions stall the issuing wave. FIRST, RT: as g4_step.
+// half. Staging store i (wst[i], loaded one slice earlier, into the slot at wdst) after group
+// ST0 + i, staging load i (slice wj of unit wu into wst[i]) after group LD0 + i (>= ST0 + i). The
+// stores end four groups before the slice does, so at least eight fragment reads (two per group)
+// follow the last of them: the next slice's barrier waits for all but eight of this wave's LDS
+// operations, which LDS completes in order, so it publishes every store. Bursts of memory instructions stall
+// the issuing wave: all eight activation loads after groups 0 and 1 ran 5 us slower at
+// configuration 4 than two after each of groups 0-3. FIRST, RT: as g4_step.
 template <int NF, int XNF, int XB, bool RNEXT, bool FIRST, int NW, bool RT>
 __device__ __forceinline__ void g4_slice8(f32x4_t (&acc)[NW][NF], i32x8_t (&wp)[G4_WIN8], i32x8_t (&xb)[2][4],
                                           u32x4_t (&wst)[8], const G4State& st, const uint32_t (&xo)[4],
                                           uint32_t kb0, uint32_t kb1, const uint8_t* rc0, const uint8_t* rc1,
                                           const uint8_t* rn0, const uint8_t* rn1, uint8_t* wdst, const G4Unit& wu,
                                           int wj, int nst, int nld) {
+  constexpr int ST0 = NW / 2 - 4;          // staging stores after groups ST0 .. NW - 5
+  constexpr int LD0 = NW == 16 ? 8 : 0;    // staging loads after groups LD0 .. LD0 + NW/2 - 1
 #pragma unroll
   for (int t = 0; t < NW; ++t) {
 #pragma unroll
@@ -519,9 +523,12 @@ __device__ __forceinline__ void g4_slice8(f32x4_t (&acc)[NW][NF], i32x8_t (&wp)[
         d[0] = (int)h[0]; d[1] = (int)h[1]; d[2] = (int)h[2]; d[3] = (int)h[3];
       }
     }
-    if (t >= NW / 2) {
-      const int i = t - NW / 2;
+    if (t >= ST0 && t - ST0 < NW / 2) {
+      const int i = t - ST0;
       if (!RT || i < nst) *reinterpret_cast<u32x4_t*>(wdst + 1024 * i) = wst[i];
+    }
+    if (t >= LD0 && t - LD0 < NW / 2) {
+      const int i = t - LD0;
       if (!RT || i < nld) wst[i] = g4_wload(wu, wj, st.nk, st.K2, st.wl, i);
     }
   }
