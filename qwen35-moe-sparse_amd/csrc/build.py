@@ -69,6 +69,35 @@ def mfma_operand_hazards(asm_text):
     return bad
 
 
+def barrier_store_coverage(asm_text):
+    """Ring stores a barrier may not cover. The four-wave kernels publish each ring slice with
+    `s_waitcnt lgkmcnt(n)` + `s_barrier`; LDS operations of a wave complete in order, so the wait
+    retires a `ds_write_b128` only if at least n LDS operations follow it before the wait. Returns
+    (last store, wait) pairs where fewer follow."""
+    bad, seg = [], []
+    for line in asm_text.splitlines():
+        t = line.split(";")[0].strip()
+        if not t or t.startswith("."):
+            continue
+        if t.endswith(":") or t.startswith("s_endpgm"):
+            seg = [] if t.startswith("s_endpgm") else seg
+            continue
+        if t.startswith("s_barrier"):
+            w = [j for j, y in enumerate(seg) if y.startswith("ds_write_b128")]
+            waits = [y for y in seg[w[-1] + 1:] if "lgkmcnt(" in y] if w else []
+            if waits:
+                n = int(re.search(r"lgkmcnt\((\d+)\)", waits[-1]).group(1))
+                after = sum(1 for y in seg[w[-1] + 1:] if y.startswith("ds_"))
+                if after < n:
+                    bad.append((seg[w[-1]], waits[-1]))
+            elif w:
+                bad.append((seg[w[-1]], "no lgkmcnt wait"))
+            seg = []
+            continue
+        seg.append(t)
+    return bad
+
+
 def _compile(src):
     obj = CSRC / "_build" / (Path(src).stem + ".o")
     cmd = [HIPCC, *FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
@@ -84,6 +113,10 @@ def _compile(src):
         if bad:
             rc = 1
             err += "\n".join(["MFMA operand written by VALU without wait states:"] + [f"  {a}  ->  {b}" for a, b in bad[:8]])
+        uncovered = barrier_store_coverage(asm.read_text())
+        if uncovered:
+            rc = 1
+            err += "\n".join(["ring store not covered by the next barrier's wait:"] + [f"  {a}  ->  {b}" for a, b in uncovered[:8]])
     return src, rc, err, obj
 
 
